@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused KAN layer forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--quick]
+
+Prints ONE JSON line.  A "step" is one fused forward over one batch with the
+inputs already resident in HBM.  The headline workload is BASELINE config 3
+(FastKAN Gaussian-RBF, 16384 x 1024 -> 1024, 8 centres on [-2, 2], fp16,
+x = LayerNorm(N(0,1)), W ~ N(0, 1/(1024*8))): the north-star MFMA-bound shape.
+``value`` is its whole-job throughput in TFLOP/s of algorithmic work
+F = 2*B*D_out*D_in*(K + has_base).  The other BASELINE configs are reported
+under ``workloads`` (same timing method).  ``roofline`` uses the dominant
+kernel's mean duration measured with HIP events on the launch stream;
+``cpu_baseline`` times this repo's NumPy restatement of the reference's
+four-stage fp32 CPU path on a bounded row sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "metal-kans_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK = {"f16": 2516.6, "bf16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s (MI355X datasheet)
+HBM_PEAK_GBS = 8000.0
+METRIC = "fused KAN fwd TFLOP/s + % MFMA peak; quantized-weight HBM GB/s (1 MI355X)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class DevBuf:
+    def __init__(self, lib, nbytes):
+        self.lib = lib
+        self.p = ctypes.c_void_p()
+        rc = lib.kans_dev_malloc(ctypes.byref(self.p), nbytes)
+        if rc:
+            raise RuntimeError(lib.kans_last_error().decode())
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        assert self.lib.kans_memcpy_h2d(self.p, a.ctypes.data, a.nbytes) == 0
+
+    def download(self, a: np.ndarray):
+        assert self.lib.kans_memcpy_d2h(a.ctypes.data, self.p, a.nbytes) == 0
+        return a
+
+    def free(self):
+        if self.p:
+            self.lib.kans_dev_free(self.p)
+            self.p = ctypes.c_void_p()
+
+
+def make_layer(mk, kind, d_in, d_out, K, dtype, rng, w_std, grid_range=(-1.0, 1.0)):
+    """Layer with weights drawn in the BASELINE order (x drawn first by the caller): W, then W_base."""
+    if kind == "cheby":
+        L = mk.ChebyKAN(d_in, d_out, degree=K)
+    elif kind == "rbf":
+        L = mk.FastKAN(d_in, d_out, num_centers=K, grid_range=grid_range)
+    else:
+        L = mk.BSplineKAN(d_in, d_out, grid_size=K - 3, grid_range=grid_range)
+    setattr(L, L._weight_attr, rng.normal(0, w_std, (d_out, d_in * K)).astype(np.float32))
+    bound = 1.0 / np.sqrt(d_in)
+    L.w_base = rng.uniform(-bound, bound, (d_out, d_in)).astype(np.float32)
+    L.bias = np.zeros(d_out, np.float32)
+    if dtype == "f16":
+        L.half()
+    elif dtype == "bf16":
+        L.bfloat16()
+    return L
+
+
+def device_layer(L, dtype):
+    """Upload the layer's weights; returns the engine (device handle)."""
+    from metal_kans._engine import DT_BF16, DT_F16, DT_F32
+    eng = L._engine()
+    W = getattr(L, L._weight_attr)
+    if dtype == "bf16":
+        eng.prepare_f32(DT_BF16, W, L.w_base, L.bias, L._basis_params())
+    else:
+        eng.prepare(DT_F16 if dtype == "f16" else DT_F32, W, L.w_base, L.bias, L._basis_params())
+    return eng
+
+
+def host_input(x: np.ndarray, dtype):
+    from metal_kans._engine import to_bf16_bits
+    if dtype == "f16":
+        return np.ascontiguousarray(x, dtype=np.float16)
+    if dtype == "bf16":
+        return to_bf16_bits(x)
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def time_layer(lib, eng, xd, yd, B, d_in, d_out, warmup, iters):
+    ms = ctypes.c_float()
+    rc = lib.kans_layer_time_forward(eng.handle, xd.p, d_in, yd.p, d_out, B, warmup, iters, ctypes.byref(ms))
+    if rc:
+        raise RuntimeError(lib.kans_last_error().decode())
+    return ms.value
+
+
+def run_layer_workload(lib, mk, name, kind, B, d_in, d_out, K, dtype, seed, x_fn, w_std, warmup, iters,
+                       grid_range=(-1.0, 1.0), steps=0):
+    rng = np.random.default_rng(seed)
+    x = x_fn(rng, B, d_in)
+    L = make_layer(mk, kind, d_in, d_out, K, dtype, rng, w_std, grid_range)
+    eng = device_layer(L, dtype)
+    es = 4 if dtype == "f32" else 2
+    xd = DevBuf(lib, B * d_in * es)
+    yd = DevBuf(lib, B * d_out * es)
+    xd.upload(host_input(x, dtype))
+    ms = time_layer(lib, eng, xd, yd, B, d_in, d_out, warmup, iters)
+    flops = 2.0 * B * d_out * d_in * (K + 1)
+    out = {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 2), "frac_mfma_peak": round(flops / ms / 1e9 / PEAK[dtype], 4),
+           "shape": f"{B}x{d_in}->{d_out}", "K": K, "basis": kind, "dtype": dtype}
+    wall = None
+    if steps:
+        lib.kans_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            rc = lib.kans_layer_forward(eng.handle, xd.p, d_in, yd.p, d_out, B, None)
+            assert rc == 0
+        lib.kans_synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+    log(f"[bench] {name}: {out}")
+    state = {"x": x, "L": L, "eng": eng, "xd": xd, "yd": yd, "flops": flops, "wall_ms": wall}
+    return out, state
+
+
+def cpu_baseline_cfg3(x, L, budget_s=12.0):
+    """Oracle fp32 four-stage forward (reference stage order) on a row sample of cfg 3."""
+    from oracle import kan_oracle as O
+    try:
+        from threadpoolctl import threadpool_limits, threadpool_info
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+        threadpool_info = lambda: []  # noqa: E731
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        cores = min(cores, int(env))
+    rows = 2048
+    xs = np.asarray(x[:rows], dtype=np.float32)
+    W = np.asarray(L.w_rbf, dtype=np.float32)
+    Wb = np.asarray(L.w_base, dtype=np.float32)
+    bias = np.asarray(L.bias, dtype=np.float32)
+    params = {"grid": np.asarray(L.grid, np.float32), "inv_den": L.inv_denominator}
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    times = []
+    try:
+        O.kan_forward("rbf", xs[:256], W, Wb, bias, params, acc=np.float32)  # warm-up
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+            t0 = time.perf_counter()
+            O.kan_forward("rbf", xs, W, Wb, bias, params, acc=np.float32)
+            times.append(time.perf_counter() - t0)
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    t = float(np.median(times))
+    d_out, d_in = Wb.shape
+    K = W.shape[1] // d_in
+    flops = 2.0 * rows * d_out * d_in * (K + 1)
+    blas = ""
+    try:
+        info = threadpool_info()
+        blas = ", ".join(f"{i.get('internal_api')} {i.get('version')}" for i in info if i.get("user_api") == "blas")
+    except Exception:
+        pass
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except Exception:
+        pass
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"cfg3 rows 0..{rows - 1} of 16384 (1/8 of the batch), fp32 NumPy four-stage forward "
+                      f"(SiLU+bias, silu(x)W_base^T, Phi, Phi W^T), median of {len(times)} runs "
+                      f"({t * 1e3:.1f} ms each); CPU {cpu_model}; BLAS {blas}"}
+
+
+def run_chain_cfg2(lib, mk, warmup, iters):
+    """ChebyKAN MLP 784 -> 256 -> 256 -> 10, K = 9, fp16, B = 4096, one HIP graph."""
+    rng = np.random.default_rng(1002)
+    B = 4096
+    x = rng.uniform(0, 1, (B, 784)).astype(np.float32)
+    net = mk.MetalKAN([784, 256, 256, 10], basis_type="cheby", degree=9)
+    for layer in net.layers:
+        layer.w_cheby = rng.normal(0, np.sqrt(1.0 / (layer.in_features * 9)),
+                                   layer.w_cheby.shape).astype(np.float32)
+    net.half()
+    y = net(x)  # builds the chain and uploads weights
+    assert y.shape == (B, 10) and np.isfinite(y.astype(np.float32)).all()
+    ms_dev = ctypes.c_float()
+    ms_host = ctypes.c_float()
+    assert lib.kans_chain_time(net._chain, B, warmup, iters, 0, ctypes.byref(ms_dev)) == 0
+    assert lib.kans_chain_time(net._chain, B, warmup, iters, 1, ctypes.byref(ms_host)) == 0
+    flops = sum(2.0 * B * l.out_features * l.in_features * 10 for l in net.layers)
+    out = {"ms_graph_device": round(ms_dev.value, 5), "ms_graph_with_pcie": round(ms_host.value, 5),
+           "tflops": round(flops / ms_dev.value / 1e9, 2),
+           "frac_mfma_peak": round(flops / ms_dev.value / 1e9 / PEAK["f16"], 4),
+           "tokens_per_s": round(B / ms_dev.value * 1e3, 1), "shape": "4096x[784,256,256,10]", "K": 9,
+           "dtype": "f16"}
+    log(f"[bench] cfg2_chain: {out}")
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline only, no secondary workloads / CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs on one GPU only (the fused KAN forward is single-GPU; "
+                                   "multi-GPU sharding is a design note, see DESIGN.md)", "n_gpus": a.gpus}))
+        sys.exit(2)
+    import metal_kans as mk
+    lib = mk.get_metal_bridge()
+    iters = max(a.steps, 1)
+
+    # ---- headline: config 3 ------------------------------------------------
+    def ln_normal(rng, B, d):
+        from oracle.kan_oracle import layer_norm
+        return layer_norm(rng.normal(0, 1, (B, d)).astype(np.float32))
+
+    head, st = run_layer_workload(lib, mk, "cfg3_fastkan_fp16", "rbf", 16384, 1024, 1024, 8, "f16", 1003,
+                                  ln_normal, np.sqrt(1.0 / (1024 * 8)), a.warmup, iters, grid_range=(-2.0, 2.0),
+                                  steps=iters)
+    F = st["flops"]
+    wall_ms = st["wall_ms"]
+    value = F / wall_ms / 1e9
+    kernel_ms = head["ms"]
+    achieved = F / kernel_ms / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": iters,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded NumPy; random-init weights of the BASELINE shapes)",
+        "config": {"workload": "cfg3: FastKAN Gaussian-RBF layer, B=16384, 1024->1024, 8 centres on [-2,2], "
+                               "fp16, x=LayerNorm(N(0,1)), inputs resident in HBM",
+                   "batch": 16384, "d_in": 1024, "d_out": 1024, "K": 8, "has_base": 1,
+                   "flops_per_step": F},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["f16"], "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK["f16"], 4), "traffic": None,
+                     "kernel": "kans::kan_fused_dense<_Float16, BASIS_RBF, 64, 4>",
+                     "kernel_ms": kernel_ms},
+    }
+    workloads = {"cfg3_fastkan_fp16": head}
+    if not a.quick:
+        unif = lambda lo, hi: (lambda rng, B, d: rng.uniform(lo, hi, (B, d)).astype(np.float32))  # noqa: E731
+        for name, kind, B, di, do, K, dt, seed, xf, ws in [
+            ("ns_cheby_fp16", "cheby", 16384, 1024, 1024, 9, "f16", 2001, unif(-1, 1), np.sqrt(1 / (1024 * 9))),
+            ("ns_bspline_fp16", "bspline", 16384, 1024, 1024, 8, "f16", 2002, unif(-1.2, 1.2), np.sqrt(1 / (1024 * 8))),
+            ("cfg4_bspline_bf16", "bspline", 8192, 1024, 4096, 8, "bf16", 1004, unif(-1.2, 1.2), np.sqrt(1 / (1024 * 8))),
+            ("cfg4_bspline_fp32", "bspline", 8192, 1024, 4096, 8, "f32", 1004, unif(-1.2, 1.2), np.sqrt(1 / (1024 * 8))),
+            ("cfg1_cheby_fp32", "cheby", 256, 64, 64, 9, "f32", 1001, lambda rng, B, d: np.tanh(rng.uniform(-1, 1, (B, d))).astype(np.float32), np.sqrt(1 / (64 * 9))),
+        ]:
+            out, s2 = run_layer_workload(lib, mk, name, kind, B, di, do, K, dt, seed, xf, ws, a.warmup, iters)
+            workloads[name] = out
+            s2["xd"].free()
+            s2["yd"].free()
+            del s2
+        workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters)
+    result["workloads"] = workloads
+    if not (a.quick or a.no_cpu):
+        result["cpu_baseline"] = cpu_baseline_cfg3(st["x"], st["L"])
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

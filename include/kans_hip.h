@@ -1,0 +1,218 @@
+/*
+ * kans_hip.h -- C ABI of the MI355X (gfx950) fused KAN forward library
+ * (metal-kans_amd/metal_kans/libkans_hip.so).
+ *
+ * Plain C: pointers, sizes and ints; no HIP or torch types in any signature
+ * (a HIP stream is passed as void*).  Every function returns 0 on success or a
+ * negative KANS_ERR_* code (the benchmark helpers return milliseconds, or a
+ * negative value on failure); kans_last_error() describes the last failure of
+ * the calling thread.  Arguments are validated before any HIP call.
+ *
+ * The first block mirrors the reference's ctypes surface for the hot path
+ * (reference: metal_kans/device.py:64-474, implemented in
+ * metal_kans/kernels/metal_kan_bridge.mm); the names, argument order and
+ * meaning are kept so the reference's bindings apply unchanged.  The second
+ * block is the device-resident layer API that the Python package and the
+ * benchmarks use.
+ */
+#ifndef KANS_HIP_H
+#define KANS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* return codes */
+#define KANS_OK 0
+#define KANS_ERR_ARG (-1)     /* invalid argument (also the reference quantizers' -1) */
+#define KANS_ERR_NODEV (-2)   /* no gfx950 HIP device visible */
+#define KANS_ERR_HIP (-3)     /* a HIP runtime call failed */
+#define KANS_ERR_STATE (-4)   /* object not ready (e.g. weights not loaded) */
+#define KANS_ERR_UNSUPPORTED (-5)
+
+/* basis / dtype codes of the layer API */
+#define KANS_BASIS_CHEBY 0
+#define KANS_BASIS_RBF 1
+#define KANS_BASIS_BSPLINE 2
+#define KANS_DT_F32 0
+#define KANS_DT_F16 1
+#define KANS_DT_BF16 2
+
+const char* kans_last_error(void);
+
+/* ======================================================================= *
+ * Reference-named entry points.  Host pointers; blocking unless async mode  *
+ * is on (then results land in Y at metal_kan_sync()).  Host weight arrays   *
+ * are read on every call, as the reference's zero-copy buffers do.          *
+ * ======================================================================= */
+
+/* replaces metal_kan_init (device.py:65-66, metal_kan_bridge.mm:289-404);
+ * the shader path is ignored (kernels are compiled ahead of time).
+ * Returns -1 when no gfx950 device is visible. */
+int metal_kan_init(const char* shader_path);
+
+/* replace metal_kan_set_async / metal_kan_sync (device.py:212-216,
+ * metal_kan_bridge.mm:275-287) */
+int metal_kan_set_async(int enabled);
+int metal_kan_sync(void);
+
+/* replace metal_kan_cheby_forward[_fp16] (device.py:68-72,227-231;
+ * metal_kan_bridge.mm:443-530,1890-1971).  K = number of Chebyshev
+ * coefficients (the reference's `degree`).  fp16/bf16 arrays are uint16 bit
+ * patterns.  The _bf16 variant has no reference counterpart (new dtype). */
+int metal_kan_cheby_forward(const float* X, const float* W_cheby, const float* W_base, const float* bias,
+                            float* Y, int B, int D_in, int D_out, int K, int has_base, int has_bias);
+int metal_kan_cheby_forward_fp16(const uint16_t* X, const uint16_t* W_cheby, const uint16_t* W_base,
+                                 const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int K,
+                                 int has_base, int has_bias);
+int metal_kan_cheby_forward_bf16(const uint16_t* X, const uint16_t* W_cheby, const uint16_t* W_base,
+                                 const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int K,
+                                 int has_base, int has_bias);
+
+/* replace metal_kan_fastkan_forward[_fp16] (device.py:74-78,233-237;
+ * metal_kan_bridge.mm:532-625,1973-2060).  grid = K centres (fp16 bit
+ * patterns for _fp16, fp32 for _bf16, as FastKAN keeps its grid fp32 there). */
+int metal_kan_fastkan_forward(const float* X, const float* W_rbf, const float* W_base, const float* grid,
+                              const float* bias, float* Y, int B, int D_in, int D_out, int K,
+                              float inv_denominator, int has_base, int has_bias);
+int metal_kan_fastkan_forward_fp16(const uint16_t* X, const uint16_t* W_rbf, const uint16_t* W_base,
+                                   const uint16_t* grid, const uint16_t* bias, uint16_t* Y, int B, int D_in,
+                                   int D_out, int K, float inv_denominator, int has_base, int has_bias);
+int metal_kan_fastkan_forward_bf16(const uint16_t* X, const uint16_t* W_rbf, const uint16_t* W_base,
+                                   const float* grid, const uint16_t* bias, uint16_t* Y, int B, int D_in,
+                                   int D_out, int K, float inv_denominator, int has_base, int has_bias);
+
+/* replace metal_kan_bspline_forward[_fp16] (device.py:110-114,263-267;
+ * metal_kan_bridge.mm:1069-1164,2062-2151).  grid = [grid_min, inv_h] fp32,
+ * read on the host; spline_order is ignored (always cubic, G+3 bases). */
+int metal_kan_bspline_forward(const float* X, const float* W_spline, const float* W_base, const float* grid,
+                              const float* bias, float* Y, int B, int D_in, int D_out, int grid_size,
+                              int spline_order, int has_base, int has_bias);
+int metal_kan_bspline_forward_fp16(const uint16_t* X, const uint16_t* W_spline, const uint16_t* W_base,
+                                   const float* grid, const uint16_t* bias, uint16_t* Y, int B, int D_in,
+                                   int D_out, int grid_size, int spline_order, int has_base, int has_bias);
+int metal_kan_bspline_forward_bf16(const uint16_t* X, const uint16_t* W_spline, const uint16_t* W_base,
+                                   const float* grid, const uint16_t* bias, uint16_t* Y, int B, int D_in,
+                                   int D_out, int grid_size, int spline_order, int has_base, int has_bias);
+
+/* replace benchmark_metal_{cheby,fastkan,bspline} (device.py:124-150,
+ * metal_kan_bridge.mm:1250-1371): mean wall-clock ms per full host call. */
+double benchmark_metal_cheby(const float* X, const float* W_cheby, const float* W_base, const float* bias,
+                             float* Y, int B, int D_in, int D_out, int K, int has_base, int has_bias, int warmup,
+                             int iters);
+double benchmark_metal_fastkan(const float* X, const float* W_rbf, const float* W_base, const float* grid,
+                               const float* bias, float* Y, int B, int D_in, int D_out, int K,
+                               float inv_denominator, int has_base, int has_bias, int warmup, int iters);
+double benchmark_metal_bspline(const float* X, const float* W_spline, const float* W_base, const float* grid,
+                               const float* bias, float* Y, int B, int D_in, int D_out, int grid_size,
+                               int spline_order, int has_base, int has_bias, int warmup, int iters);
+
+/* replace metal_kan_quantize_int{8,4} (device.py:398-416, metal_kan_bridge.mm:4177-4275).
+ * Host (CPU, multi-threaded) quantizers with the rounding of the reference's NumPy fallback
+ * (quantization.py:73-99): fp32 division, round half to even.  `weights` is the zero-padded
+ * [num_groups * group_size] fp32 matrix; qweight is [num_groups][group_size] (INT8) or
+ * [num_groups][group_size/2] (INT4, even index in the low nibble); scales/biases [num_groups]. */
+int metal_kan_quantize_int8(const float* weights, uint8_t* qweight, float* scales, float* biases, int num_groups,
+                            int group_size);
+int metal_kan_quantize_int4(const float* weights, uint8_t* qweight, float* scales, float* biases, int num_groups,
+                            int group_size);
+/* replace metal_kan_dequantize_int{8,4} (device.py:404-416, metal_kan_bridge.mm:4212-4302):
+ * out = fl(fl(q * scale) + bias) on the GPU, bit-identical to quantization.py:136-148. */
+int metal_kan_dequantize_int8(const uint8_t* qweight, const float* scales, const float* biases, float* out,
+                              int num_groups, int group_size);
+int metal_kan_dequantize_int4(const uint8_t* qweight, const float* scales, const float* biases, float* out,
+                              int num_groups, int group_size);
+/* replace metal_kan_quantize_ternary / metal_kan_dequantize_ternary (device.py:376-379,460-463;
+ * metal_kan_bridge.mm:4634-4682,5073-5107).  Quantizer follows quantization.py:231-246
+ * (NumPy pairwise fp32 mean of |w| per (row, group)); packed [D_out][ceil(K_dim/16)] uint32,
+ * scales [D_out][ceil(K_dim/group_size)]. */
+int metal_kan_quantize_ternary(const float* W, uint32_t* packed, float* scales, int D_out, int K_dim,
+                               int group_size);
+int metal_kan_dequantize_ternary(const uint32_t* packed, const float* scales, float* out, int D_out, int K_dim,
+                                 int group_size);
+/* replaces metal_kan_swiglu_forward (device.py:431-434, metal_kan_bridge.mm:4846-4875) */
+int metal_kan_swiglu_forward(const float* gate, const float* up, float* out, int n);
+
+/* replaces metal_kan_chain_pipeline_cheby (device.py:116-122, metal_kan_bridge.mm:1168-1248):
+ * fp32 Chebyshev layers dims[0] -> ... -> dims[num_layers], any K per layer (the reference
+ * hard-codes K = 4); W_bases[l] / biases[l] may be NULL to disable that branch.  Runs as one
+ * replayed HIP graph with device-resident ping-pong activations. */
+int metal_kan_chain_pipeline_cheby(const float* X, float* Y, int B, int num_layers, const int* dims,
+                                   const int* degrees, const float** W_chebys, const float** W_bases,
+                                   const float** biases);
+
+/* ======================================================================= *
+ * Device-resident layer API (no reference counterpart: the reference has   *
+ * unified memory and no device-resident objects).                          *
+ * ======================================================================= */
+typedef struct kans_layer kans_layer;
+
+int kans_init(void);
+void* kans_stream(void); /* the library's HIP stream (hipStream_t) */
+int kans_synchronize(void);
+
+int kans_layer_create(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias,
+                      kans_layer** out);
+int kans_layer_destroy(kans_layer* layer);
+/* RBF: K centres (fp32) and 1/(2h^2); B-spline: G (K = G + 3), grid_min, inv_h */
+int kans_layer_set_rbf(kans_layer* layer, const float* centers, float inv_denominator);
+int kans_layer_set_bspline(kans_layer* layer, int grid_size, float grid_min, float inv_h);
+/* tiling override for tuning: (wm, nb) in {(64,4),(32,4),(32,1)} or (0,0) = automatic; splits >= 0 */
+int kans_layer_set_tiling(kans_layer* layer, int wm, int nb, int splits);
+int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
+/* weights in the layer dtype: W [D_out][D_in*K] (k fastest), W_base [D_out][D_in], bias [D_out] */
+int kans_layer_load_weights(kans_layer* layer, const void* W, const void* W_base, const void* bias);
+int kans_layer_load_weights_device(kans_layer* layer, const void* W, const void* W_base, const void* bias);
+/* host fp32 weights converted on the device to the layer dtype (round to nearest even) */
+int kans_layer_load_weights_f32(kans_layer* layer, const float* W, const float* W_base, const float* bias);
+/* device pointers; X [B][ldx] with ldx >= round_up(D_in, 8), ldx % 8 == 0, X 16-byte aligned and
+ * columns D_in..ldx-1 finite; Y [B][ldy].  Enqueued on `stream` (NULL = kans_stream()). */
+int kans_layer_forward(kans_layer* layer, const void* X, long ldx, void* Y, long ldy, int B, void* stream);
+/* as kans_layer_forward with the element types of X and Y chosen separately: each is the layer dtype or
+ * KANS_DT_F32 (fp32 activations around a 16-bit layer; fp32 X must be 32-byte aligned) */
+int kans_layer_forward_ex(kans_layer* layer, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy,
+                          int B, void* stream);
+/* host pointers, contiguous [B][D_in] -> [B][D_out] in the layer dtype, pinned staging */
+int kans_layer_forward_host(kans_layer* layer, const void* X, void* Y, int B);
+/* as kans_layer_forward_host with X in x_dtype: the layer dtype, or KANS_DT_F32 for a 16-bit layer
+ * (the input is then used unrounded; weights and MFMA stay 16-bit) */
+int kans_layer_forward_host_ex(kans_layer* layer, const void* X, int x_dtype, void* Y, int B);
+/* mean ms per device-resident forward, HIP events on the launch stream */
+int kans_layer_time_forward(kans_layer* layer, const void* X, long ldx, void* Y, long ldy, int B, int warmup,
+                            int iters, float* ms);
+
+/* multi-layer chain of layers with matching dims and one dtype (no reference counterpart
+ * beyond metal_kan_chain_pipeline_cheby): ping-pong device activations kept in fp32 between
+ * layers (also for fp16/bf16 layers), host path captured as a HIP graph per batch size.
+ * Layers must outlive the chain. */
+typedef struct kans_chain kans_chain;
+int kans_chain_create(kans_layer** layers, int n, kans_chain** out);
+int kans_chain_destroy(kans_chain* chain);
+int kans_chain_forward_host(kans_chain* chain, const void* X, void* Y, int B);
+/* X in x_dtype: the chain dtype, or KANS_DT_F32 (unrounded input to a 16-bit chain) */
+int kans_chain_forward_host_ex(kans_chain* chain, const void* X, int x_dtype, void* Y, int B);
+int kans_chain_forward(kans_chain* chain, const void* X, long ldx, void* Y, long ldy, int B, void* stream);
+/* mean ms per graph replay (include_copies: also the pinned H2D/D2H copies) */
+int kans_chain_time(kans_chain* chain, int B, int warmup, int iters, int include_copies, float* ms);
+
+/* bit-exact dequantizers on device pointers (stream NULL = kans_stream()); bits = 8 or 4 */
+int kans_dequantize_affine_device(const void* qweight, const float* scales, const float* biases, float* out,
+                                  long num_groups, int group_size, int bits, void* stream);
+int kans_dequantize_ternary_device(const uint32_t* packed, const float* scales, float* out, int D_out, int K_dim,
+                                   int group_size, void* stream);
+
+/* device memory helpers; kans_copy_device is a plain copy kernel (16-byte multiples) used to
+ * calibrate hardware byte counters */
+int kans_dev_malloc(void** ptr, size_t bytes);
+int kans_dev_free(void* ptr);
+int kans_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int kans_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int kans_copy_device(void* dst, const void* src, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KANS_HIP_H */

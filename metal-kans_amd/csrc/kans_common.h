@@ -1,0 +1,177 @@
+// Shared device-side definitions for the MI355X (gfx950) fused KAN kernels.
+//
+// Element types, MFMA fragment types, the basis generators that run inside the
+// fused kernels, and the tiled weight layout shared by the repack kernel and the
+// fused forward.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kans {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+enum Basis { BASIS_CHEBY = 0, BASIS_RBF = 1, BASIS_BSPLINE = 2 };
+enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Maximum number of RBF centres / basis functions per input feature.
+constexpr int kMaxK = 32;
+
+// Basis parameters passed by value to the fused kernels.
+struct BasisParams {
+  int K;              // basis functions per feature (excluding the SiLU base slot)
+  int grid_size;      // B-spline: number of intervals G (K = G + 3)
+  float grid_min;     // B-spline: left end of the grid
+  float inv_h;        // B-spline: G / (max - min)
+  float neg_l;        // RBF: -inv_den * log2(e)
+  const float* centers;  // RBF centres c_k (device memory, K floats)
+};
+
+// ---------------------------------------------------------------------------
+// Tiled weight layout W'.  The contraction runs over (feature i, slot s) pairs,
+// where slot 0 is the SiLU base branch when has_base and slots has_base.. are the
+// K basis functions.  The inner dimension is reordered so that one MFMA step
+// consumes 16 features of ONE slot:
+//
+//   W'[fb][s][ob][chunk][lane][e]
+//     fb    = i / 16                 (feature block)
+//     s     = slot                   (0 .. KP-1)
+//     ob    = o / 32                 (32-column output block; padded to kObPad)
+//     lane  = (o % 32) + 32 * ((i % 16) / 8)
+//     j     = i % 8,  chunk = j / EPC,  e = j % EPC  (EPC = 16 / sizeof(T))
+//
+// so a lane's 16-byte chunk is exactly its MFMA B-operand for that slot, and one
+// (fb, s) step of an N-tile of NB output blocks is NB contiguous KB-sized tiles.
+// ---------------------------------------------------------------------------
+constexpr int kObPad = 8;  // output blocks padded to a multiple of 8 (max NB)
+
+__host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+template <typename T> struct TypeTag;
+template <> struct TypeTag<_Float16> { static constexpr int dt = DT_F16; };
+template <> struct TypeTag<__bf16> { static constexpr int dt = DT_BF16; };
+template <> struct TypeTag<float> { static constexpr int dt = DT_F32; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(__bf16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) { return (__bf16)v; }
+
+// SiLU on the raw input: x / (1 + e^-x)  (reference: fused_kan.metal:13-16,132-133).
+__device__ __forceinline__ float silu_f32(float x) {
+  float e = __builtin_amdgcn_exp2f(-x * kLog2e);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// ---------------------------------------------------------------------------
+// Basis generators.  A generator holds NV input values of one lane and produces
+// the NV values of basis function k in fp32.  ``begin`` is called once per
+// 16-feature block; then ``pair(k, v0, v1)`` yields functions k and k+1 and
+// ``one(k, v0)`` function k, with k = 0, 2, 4, ... in order within a block.
+// ---------------------------------------------------------------------------
+template <int BASIS, int NV> struct BasisGen;
+
+// Chebyshev T_k(clamp(x,-1,1)) by the three-term recurrence in fp32 registers
+// (reference: fused_kan.metal:205-238 fp32, :1399-1426 fp16 with fma).  The
+// state (p, q) = (T_k, T_{k+1}) advances two functions per pair() without
+// register rotation.
+template <int NV> struct BasisGen<BASIS_CHEBY, NV> {
+  float tw[NV], p[NV], q[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float t = __builtin_fminf(__builtin_fmaxf(x[v], -1.0f), 1.0f);
+      tw[v] = t + t;
+      p[v] = 1.0f;
+      q[v] = t;
+    }
+  }
+  __device__ __forceinline__ void pair(int, const BasisParams&, float* v0, float* v1) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      v0[v] = p[v];
+      v1[v] = q[v];
+      p[v] = __builtin_fmaf(tw[v], q[v], -p[v]);
+      q[v] = __builtin_fmaf(tw[v], p[v], -q[v]);
+    }
+  }
+  __device__ __forceinline__ void one(int, const BasisParams&, float* v0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) v0[v] = p[v];
+  }
+};
+
+// Gaussian RBF exp(-(x - c_k)^2 * inv_den) = exp2(neg_l * (x - c_k)^2)
+// (reference: fused_kan.metal:140-166, fast_kan.py:40-42).
+template <int NV> struct BasisGen<BASIS_RBF, NV> {
+  float xv[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xv[v] = x[v];
+  }
+  __device__ __forceinline__ void one(int k, const BasisParams& bp, float* v0) {
+    const float c = bp.centers[k];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float d = xv[v] - c;
+      v0[v] = __builtin_amdgcn_exp2f(bp.neg_l * d * d);
+    }
+  }
+  __device__ __forceinline__ void pair(int k, const BasisParams& bp, float* v0, float* v1) {
+    one(k, bp, v0);
+    one(k + 1, bp, v1);
+  }
+};
+
+// Clamped uniform cubic B-spline, G+3 bases, four non-zero per input
+// (reference: fused_kan.metal:240-276, bspline_kan.py:40-54):
+//   pos = (x - grid_min) * inv_h, span = clamp(floor(pos), 0, G-1),
+//   u = clamp(pos - span, 0, 1), values at span..span+3.
+template <int NV> struct BasisGen<BASIS_BSPLINE, NV> {
+  float w0[NV], w1[NV], w2[NV], w3[NV];
+  int span[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams& p) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float pos = (x[v] - p.grid_min) * p.inv_h;
+      float fl = __builtin_floorf(pos);
+      fl = __builtin_fminf(__builtin_fmaxf(fl, 0.0f), (float)(p.grid_size - 1));
+      float u = __builtin_fminf(__builtin_fmaxf(pos - fl, 0.0f), 1.0f);
+      float om = 1.0f - u;
+      float u2 = u * u, u3 = u2 * u;
+      const float inv6 = 1.0f / 6.0f;
+      w0[v] = om * om * om * inv6;
+      w1[v] = (3.0f * u3 - 6.0f * u2 + 4.0f) * inv6;
+      w2[v] = (-3.0f * u3 + 3.0f * u2 + 3.0f * u + 1.0f) * inv6;
+      w3[v] = u3 * inv6;
+      span[v] = (int)fl;
+    }
+  }
+  __device__ __forceinline__ void one(int k, const BasisParams&, float* v0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int d = k - span[v];
+      float r = 0.0f;
+      r = (d == 0) ? w0[v] : r;
+      r = (d == 1) ? w1[v] : r;
+      r = (d == 2) ? w2[v] : r;
+      r = (d == 3) ? w3[v] : r;
+      v0[v] = r;
+    }
+  }
+  __device__ __forceinline__ void pair(int k, const BasisParams& bp, float* v0, float* v1) {
+    one(k, bp, v0);
+    one(k + 1, bp, v1);
+  }
+};
+
+}  // namespace kans

@@ -1,0 +1,469 @@
+// Fused KAN layer forward for gfx950: basis expansion + output contraction in
+// one kernel, so the expanded Phi tensor never exists in memory.
+//
+//   y[b,o] = bias[o] + sum_i SiLU(x[b,i]) W_base[o,i] + sum_{i,k} phi_k(x[b,i]) W[o,i*K+k]
+//
+// Replaces the reference's four-stage dispatch (eval_base_and_bias, MPS GEMM,
+// eval_*_basis into a B*D_in*K scratch buffer, MPS GEMM) of
+// metal_kan_bridge.mm:443-625,1069-1164,1890-2151.
+//
+// Work decomposition (one workgroup = 4 waves = 256 threads, two resident per CU):
+//   * a wave owns WM rows (32 or 64) x NB*32 output columns; the 4 waves stack
+//     along rows, so a workgroup tile is 4*WM x NB*32;
+//   * the inner dimension is walked as steps (feature block fb of 16 inputs,
+//     slot s): slot 0 is SiLU(x) when the layer has the base branch, the rest
+//     are the K basis functions.  Each lane holds 8 inputs of each of its row
+//     blocks, evaluates the slot's basis value for them in fp32 registers (the
+//     Chebyshev / RBF / B-spline generators advance slot by slot), and packs
+//     them straight into the MFMA A-fragment;
+//   * the B-fragments come from a 3-stage LDS ring filled cooperatively from the
+//     pre-tiled weights (one (fb, s) step of an N-tile is NB contiguous KB);
+//   * fp16 / bf16 use v_mfma_f32_32x32x16_{f16,bf16}; fp32 uses
+//     v_mfma_f32_32x32x2_f32 eight times per step.  Accumulation is fp32.
+//   * an optional split over feature blocks writes fp32 partials that a finalize
+//     kernel reduces (used when the output tile count alone cannot fill the GPU).
+#include "kans_common.h"
+#include "kans_api_internal.h"
+#include <algorithm>
+#include <type_traits>
+
+namespace kans {
+
+constexpr int kStages = 3;
+constexpr int kThreads = 256;
+
+template <typename T> struct Mfma;
+template <> struct Mfma<_Float16> {
+  typedef half8 frag;
+  static __device__ __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<__bf16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Remap the linear workgroup id so that consecutive ids of one XCD (the hardware
+// deals workgroups round-robin over 8 XCDs) cover neighbouring tiles that share
+// the same weight N-tile; keeps each XCD's L2 working on one slice of W'.
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  if ((total & 7) != 0) return id;
+  int per = total >> 3;
+  return (id & 7) * per + (id >> 3);
+}
+
+// Per-lane uint4 chunks of one 32-column block for element type T.
+template <typename T> struct Chunks { static constexpr int CPL = (8 * (int)sizeof(T)) / 16; };
+
+// T: weight / MFMA operand type; TX: input element type; TY: output element
+// type (TX, TY in {T, float}: a 16-bit chain keeps fp32 activations between
+// layers).
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
+__global__ void __launch_bounds__(kThreads, 2)
+kan_fused_dense(const TX* __restrict__ X, long ldx,
+                const uint4* __restrict__ Wt, int nob_pad,
+                const T* __restrict__ bias,
+                TY* __restrict__ Y, long ldy,
+                float* __restrict__ Ypart,
+                int B, int D_in, int D_out, int m_tiles, int n_tiles,
+                int nfb_total, int fb_per_split, int has_base, BasisParams bp) {
+  constexpr int RB = WM / 32;           // 32-row blocks per wave
+  constexpr int NV = RB * 8;            // inputs held per lane
+  constexpr int CPL = Chunks<T>::CPL;   // uint4 per lane per 32-col block
+  constexpr int CPX = Chunks<TX>::CPL;  // uint4 per lane per row block of inputs
+  constexpr int SU = NB * 64 * CPL;     // uint4 per pipeline stage
+  constexpr int LPT = (SU + kThreads - 1) / kThreads;
+  constexpr bool kHalf = sizeof(T) == 2;
+
+  __shared__ uint4 lds[kStages][SU];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tiles = m_tiles * n_tiles;
+  const int lin = xcd_remap(blockIdx.x, tiles);
+  const int n_tile = lin / m_tiles;
+  const int m_tile = lin - n_tile * m_tiles;
+  const int split = blockIdx.y;
+
+  const int row0 = m_tile * (4 * WM) + wave * WM;
+  const int ob0 = n_tile * NB;
+  const int fb_begin = split * fb_per_split;
+  const int fb_end = min(nfb_total, fb_begin + fb_per_split);
+  const int K = bp.K;
+  const int KP = K + has_base;
+  const int nsteps = (fb_end - fb_begin) * KP;
+
+  // ---- global -> LDS weight pipeline ------------------------------------
+  // Step t covers (fb, slot) = (fb_begin + t / KP, t % KP); its tile for this
+  // N-tile is SU contiguous uint4 of W'.  Stage ring of kStages; step t+2 is
+  // fetched into registers at the top of step t and written to LDS at its
+  // bottom, so the load latency hides behind step t's MFMAs (and the other
+  // resident workgroup).
+  const uint4* wbase = Wt + (long)ob0 * (64 * CPL) + tid;
+  const long slot_stride = (long)nob_pad * (64 * CPL);
+  uint4 rg[LPT];
+  auto gload = [&](int t) {
+    const uint4* src = wbase + ((long)fb_begin * KP + t) * slot_stride;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (q * kThreads + tid < SU) rg[q] = src[q * kThreads];
+  };
+  auto lstore = [&](int t) {
+    uint4* dst = lds[t % kStages] + tid;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (q * kThreads + tid < SU) dst[q * kThreads] = rg[q];
+  };
+
+  // ---- input rows ---------------------------------------------------------
+  // lane holds x[row0 + rb*32 + lane%32][fb*16 + 8*(lane/32) + j], j = 0..7
+  uint4 xr[RB][CPX];
+  auto xload = [&](int fbx) {
+    const int f0 = fbx * 16 + 8 * (lane >> 5);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = row0 + rb * 32 + (lane & 31);
+      const bool ok = (row < B) && (f0 < D_in);
+      const uint4* p = reinterpret_cast<const uint4*>(X + (long)row * ldx + f0);
+#pragma unroll
+      for (int c = 0; c < CPX; ++c) xr[rb][c] = ok ? p[c] : make_uint4(0, 0, 0, 0);
+      if (ok && f0 + 8 > D_in) {
+        // tail chunk: inputs at or beyond D_in read as 0 whatever the padding holds
+#pragma unroll
+        for (int c = 0; c < CPX; ++c) {
+          unsigned w[4] = {xr[rb][c].x, xr[rb][c].y, xr[rb][c].z, xr[rb][c].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (sizeof(TX) == 4) {
+              if (f0 + c * 4 + q >= D_in) w[q] = 0u;
+            } else {
+              if (f0 + 2 * q >= D_in) w[q] &= 0xffff0000u;
+              if (f0 + 2 * q + 1 >= D_in) w[q] &= 0x0000ffffu;
+            }
+          }
+          xr[rb][c] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    }
+  };
+
+  floatx16 acc[RB][NB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
+
+  if (nsteps <= 0) return;  // uniform per workgroup (empty split)
+
+  // prologue: steps 0 and 1 into LDS.
+  gload(0);
+  lstore(0);
+  if (nsteps > 1) { gload(1); lstore(1); }
+  xload(fb_begin);
+  __syncthreads();
+
+  int t = 0;  // global step counter
+  // One step: fetch step t+2, multiply the slot's A-fragment (basis values v)
+  // by the B-fragments of step t, store step t+2, barrier.
+  auto step = [&](const float* v) {
+    const bool pf = t + 2 < nsteps;
+    if (pf) gload(t + 2);
+    const uint4* st = lds[t % kStages];
+    if constexpr (kHalf) {
+      typedef typename Mfma<T>::frag frag;
+      frag a[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[rb][j] = from_f32<T>(v[rb * 8 + j]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        uint4 u = st[nb * 64 + lane];
+        frag b = *reinterpret_cast<frag*>(&u);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = Mfma<T>::mma(a[rb], b, acc[rb][nb]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float bv[NB][4];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          uint4 u = st[(nb * 2 + c) * 64 + lane];
+          bv[nb][0] = __uint_as_float(u.x);
+          bv[nb][1] = __uint_as_float(u.y);
+          bv[nb][2] = __uint_as_float(u.z);
+          bv[nb][3] = __uint_as_float(u.w);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              acc[rb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v[rb * 8 + c * 4 + e], bv[nb][e], acc[rb][nb],
+                                                                  0, 0, 0);
+      }
+    }
+    if (pf) lstore(t + 2);
+    ++t;
+    __syncthreads();
+  };
+
+  BasisGen<BASIS, NV> gen;
+  for (int fb = fb_begin; fb < fb_end; ++fb) {
+    float xf[NV];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int c = 0; c < CPX; ++c) {
+        const uint4 u = xr[rb][c];
+        if constexpr (sizeof(TX) == 4) {
+          xf[rb * 8 + c * 4 + 0] = __uint_as_float(u.x);
+          xf[rb * 8 + c * 4 + 1] = __uint_as_float(u.y);
+          xf[rb * 8 + c * 4 + 2] = __uint_as_float(u.z);
+          xf[rb * 8 + c * 4 + 3] = __uint_as_float(u.w);
+        } else {
+          const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            TX lo, hi;
+            const unsigned short l16 = (unsigned short)(w[q] & 0xffffu), h16 = (unsigned short)(w[q] >> 16);
+            __builtin_memcpy(&lo, &l16, 2);
+            __builtin_memcpy(&hi, &h16, 2);
+            xf[rb * 8 + 2 * q] = to_f32(lo);
+            xf[rb * 8 + 2 * q + 1] = to_f32(hi);
+          }
+        }
+      }
+    if (fb + 1 < fb_end) xload(fb + 1);
+    gen.begin(xf, bp);
+    if (has_base) {
+      float v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) v[i] = silu_f32(xf[i]);
+      step(v);
+    }
+    int k = 0;
+    for (; k + 1 < K; k += 2) {
+      float v0[NV], v1[NV];
+      gen.pair(k, bp, v0, v1);
+      step(v0);
+      step(v1);
+    }
+    if (k < K) {
+      float v0[NV];
+      gen.one(k, bp, v0);
+      step(v0);
+    }
+  }
+
+  // ---- epilogue -------------------------------------------------------------
+  // acc register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  const int rbase = row0 + 4 * (lane >> 5);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = (ob0 + nb) * 32 + (lane & 31);
+    if (col < D_out) {
+      if (Ypart != nullptr) {
+        float* out = Ypart + ((long)split * B + rbase) * D_out + col;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = rb * 32 + 8 * (r >> 2) + (r & 3);
+            if (rbase + dr < B) out[(long)dr * D_out] = acc[rb][nb][r];
+          }
+      } else {
+        const float bcol = bias != nullptr ? to_f32(bias[col]) : 0.0f;
+        TY* out = Y + (long)rbase * ldy + col;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = rb * 32 + 8 * (r >> 2) + (r & 3);
+            if (rbase + dr < B) out[(long)dr * ldy] = from_f32<TY>(acc[rb][nb][r] + bcol);
+          }
+      }
+    }
+  }
+}
+
+// Split reduction: y = sum_split part[split] + bias, converted to T.
+template <typename T, typename TY>
+__global__ void kan_split_finalize(const float* __restrict__ part, int splits, const T* __restrict__ bias,
+                                   TY* __restrict__ Y, long ldy, int B, int D_out) {
+  long n = (long)B * D_out;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    int row = (int)(idx / D_out), col = (int)(idx - (long)row * D_out);
+    float s = bias ? to_f32(bias[col]) : 0.0f;
+    for (int k = 0; k < splits; ++k) s += part[(long)k * n + idx];
+    Y[(long)row * ldy + col] = from_f32<TY>(s);
+  }
+}
+
+// Repack raw weights W[D_out][D_in*K] (k fastest) and W_base[D_out][D_in], of
+// element type S, into the tiled layout W'[fb][s][ob][chunk][lane][e] of type T
+// (see kans_common.h), converting S -> T with round-to-nearest-even; zero
+// padding for o >= D_out and i >= D_in.
+template <typename S, typename T>
+__global__ void kan_repack_weights(const S* __restrict__ W, const S* __restrict__ Wb, uint4* __restrict__ Wt,
+                                   int D_in, int D_out, int K, int has_base, int nfb, int nob_pad) {
+  constexpr int CPL = Chunks<T>::CPL;
+  constexpr int EPC = 16 / (int)sizeof(T);
+  const int KP = K + has_base;
+  const long total = (long)nfb * KP * nob_pad * CPL * 64;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    long r = idx;
+    const int lane = (int)(r % 64); r /= 64;
+    const int chunk = (int)(r % CPL); r /= CPL;
+    const int ob = (int)(r % nob_pad); r /= nob_pad;
+    const int s = (int)(r % KP); r /= KP;
+    const int fb = (int)r;
+    const int o = ob * 32 + (lane & 31);
+    const int ibase = fb * 16 + 8 * (lane >> 5) + chunk * EPC;
+    T vals[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int i = ibase + e;
+      float w = 0.0f;
+      if (o < D_out && i < D_in) {
+        if (has_base && s == 0) w = to_f32(Wb[(long)o * D_in + i]);
+        else w = to_f32(W[((long)o * D_in + i) * K + (s - has_base)]);
+      }
+      vals[e] = from_f32<T>(w);
+    }
+    Wt[idx] = *reinterpret_cast<uint4*>(vals);
+  }
+}
+
+template <typename S, typename T>
+__global__ void kan_convert(const S* __restrict__ src, T* __restrict__ dst, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    dst[i] = from_f32<T>(to_f32(src[i]));
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch.
+// ---------------------------------------------------------------------------
+
+
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
+static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
+  const int m_tiles = (L.B + 4 * WM - 1) / (4 * WM);
+  const int nob = (L.D_out + 31) / 32;
+  const int n_tiles = (nob + NB - 1) / NB;
+  const int fbps = (L.nfb + L.splits - 1) / L.splits;
+  const int splits = (L.nfb + fbps - 1) / fbps;
+  dim3 grid(m_tiles * n_tiles, splits);
+  float* part = splits > 1 ? L.part : nullptr;
+  hipLaunchKernelGGL((kan_fused_dense<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
+                     L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
+                     L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (splits > 1) {
+    long n = (long)L.B * L.D_out;
+    int blocks = (int)std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL((kan_split_finalize<T, TY>), dim3(blocks), dim3(256), 0, st, part, splits,
+                       (const T*)L.bias, (TY*)L.Y, L.ldy, L.B, L.D_out);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+// Instantiated tile configurations (WM rows per wave, NB 32-column blocks):
+// (64,4) (32,4) (32,1); at most 128 fp32 accumulators per lane so two
+// workgroups (8 waves) stay resident per CU.  Keep in sync with
+// dense_config_supported().
+template <typename T, typename TX, typename TY, int BASIS>
+static hipError_t launch_dense_cfg(const DenseLaunch& L, hipStream_t st) {
+  if (L.wm == 64 && L.nb == 4) return launch_dense_t<T, TX, TY, BASIS, 64, 4>(L, st);
+  if (L.wm == 32 && L.nb == 4) return launch_dense_t<T, TX, TY, BASIS, 32, 4>(L, st);
+  if (L.wm == 32 && L.nb == 1) return launch_dense_t<T, TX, TY, BASIS, 32, 1>(L, st);
+  return hipErrorInvalidValue;
+}
+
+bool dense_config_supported(int wm, int nb) {
+  return (wm == 64 && nb == 4) || (wm == 32 && (nb == 4 || nb == 1));
+}
+
+template <typename T, typename TX, typename TY>
+static hipError_t launch_dense_io(const DenseLaunch& L, hipStream_t st) {
+  switch (L.basis) {
+    case BASIS_CHEBY: return launch_dense_cfg<T, TX, TY, BASIS_CHEBY>(L, st);
+    case BASIS_RBF: return launch_dense_cfg<T, TX, TY, BASIS_RBF>(L, st);
+    default: return launch_dense_cfg<T, TX, TY, BASIS_BSPLINE>(L, st);
+  }
+}
+
+// x_dtype / y_dtype: the layer dtype or DT_F32 (fp32 activations around a 16-bit layer).
+template <typename T>
+static hipError_t launch_dense_type(const DenseLaunch& L, hipStream_t st) {
+  const bool xf = L.x_dtype == DT_F32 && L.dtype != DT_F32;
+  const bool yf = L.y_dtype == DT_F32 && L.dtype != DT_F32;
+  if (!xf && !yf) return launch_dense_io<T, T, T>(L, st);
+  if constexpr (sizeof(T) == 2) {
+    if (xf && yf) return launch_dense_io<T, float, float>(L, st);
+    if (xf) return launch_dense_io<T, float, T>(L, st);
+    return launch_dense_io<T, T, float>(L, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dense(const DenseLaunch& L, hipStream_t st) {
+  switch (L.dtype) {
+    case DT_F16: return launch_dense_type<_Float16>(L, st);
+    case DT_BF16: return launch_dense_type<__bf16>(L, st);
+    default: return launch_dense_type<float>(L, st);
+  }
+}
+
+template <typename S, typename T>
+static hipError_t repack_t(const void* W, const void* Wb, void* Wt, int D_in, int D_out, int K, int has_base,
+                           int nfb, int nob_pad, hipStream_t st) {
+  const int KP = K + has_base;
+  long total = (long)nfb * KP * nob_pad * Chunks<T>::CPL * 64;
+  int blocks = (int)std::min<long>((total + 255) / 256, 16384);
+  hipLaunchKernelGGL((kan_repack_weights<S, T>), dim3(blocks), dim3(256), 0, st, (const S*)W, (const S*)Wb,
+                     (uint4*)Wt, D_in, D_out, K, has_base, nfb, nob_pad);
+  return hipGetLastError();
+}
+
+// src_dtype: element type of W / Wb (same as dtype, or DT_F32 for a converting upload).
+hipError_t launch_repack(int src_dtype, int dtype, const void* W, const void* Wb, void* Wt, int D_in, int D_out,
+                         int K, int has_base, int nfb, int nob_pad, hipStream_t st) {
+  if (src_dtype == dtype) {
+    switch (dtype) {
+      case DT_F16: return repack_t<_Float16, _Float16>(W, Wb, Wt, D_in, D_out, K, has_base, nfb, nob_pad, st);
+      case DT_BF16: return repack_t<__bf16, __bf16>(W, Wb, Wt, D_in, D_out, K, has_base, nfb, nob_pad, st);
+      default: return repack_t<float, float>(W, Wb, Wt, D_in, D_out, K, has_base, nfb, nob_pad, st);
+    }
+  }
+  if (src_dtype != DT_F32) return hipErrorInvalidValue;
+  switch (dtype) {
+    case DT_F16: return repack_t<float, _Float16>(W, Wb, Wt, D_in, D_out, K, has_base, nfb, nob_pad, st);
+    case DT_BF16: return repack_t<float, __bf16>(W, Wb, Wt, D_in, D_out, K, has_base, nfb, nob_pad, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_convert(int src_dtype, int dtype, const void* src, void* dst, long n, hipStream_t st) {
+  int blocks = (int)std::min<long>((n + 255) / 256, 4096);
+  if (src_dtype != DT_F32 || dtype == DT_F32) return hipErrorInvalidValue;
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL((kan_convert<float, _Float16>), dim3(blocks), dim3(256), 0, st, (const float*)src,
+                       (_Float16*)dst, n);
+  else
+    hipLaunchKernelGGL((kan_convert<float, __bf16>), dim3(blocks), dim3(256), 0, st, (const float*)src,
+                       (__bf16*)dst, n);
+  return hipGetLastError();
+}
+
+}  // namespace kans

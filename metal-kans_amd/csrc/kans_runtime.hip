@@ -1,0 +1,1093 @@
+// Host runtime and C-ABI of the MI355X fused KAN library (libkans_hip.so).
+//
+// Replaces the reference's Objective-C++ bridge for the hot path
+// (metal_kans/kernels/metal_kan_bridge.mm): device/queue setup (:289-404), the
+// zero-copy host buffer cache (:409-441), the fp32/fp16 forwards
+// (:443-625,1069-1164,1890-2151), the chain pipeline (:1168-1248), the async
+// flag (:84-97,275-287) and the benchmark helpers (:1250-1371).
+//
+// Design (MI355X, discrete HBM):
+//   * one HIP device, one non-blocking stream at default priority;
+//   * a kans_layer owns its weights in HBM, re-tiled once on upload for the
+//     fused kernel; the reference-named entry points keep their semantics (the
+//     host arrays are read on every call) by uploading through a layer cache;
+//   * host arrays move through pinned staging buffers with hipMemcpyAsync;
+//   * async mode defers the copy of results into the caller's arrays to
+//     metal_kan_sync();
+//   * every entry point validates its arguments before any HIP call and
+//     returns 0 or a negative code; kans_last_error() describes the failure.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+#include <chrono>
+
+#include "kans_common.h"
+#include "kans_api_internal.h"
+
+using namespace kans;
+
+namespace kans {
+hipError_t launch_dense(const DenseLaunch& L, hipStream_t st);
+bool dense_config_supported(int wm, int nb);
+hipError_t launch_repack(int src_dtype, int dtype, const void* W, const void* Wb, void* Wt, int D_in, int D_out,
+                         int K, int has_base, int nfb, int nob_pad, hipStream_t st);
+hipError_t launch_convert(int src_dtype, int dtype, const void* src, void* dst, long n, hipStream_t st);
+}  // namespace kans
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+int kans_fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t _e = (expr);                                                                 \
+    if (_e != hipSuccess)                                                                   \
+      return kans_fail(KANS_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                       __FILE__, __LINE__);                                                 \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device state
+// ---------------------------------------------------------------------------
+static std::mutex g_mu;            // serialises the library (the reference is single-threaded too)
+static bool g_ready = false;
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+static thread_local int g_async = 0;  // reference: thread_local g_async_mode
+
+struct Pending {  // a deferred device->host result copy (async mode); dst null: just free
+  void* pinned;
+  void* dst;
+  size_t bytes;
+};
+static std::vector<Pending> g_pending;
+
+// grow-only pinned staging buffers (synchronous mode)
+struct Pinned {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+static Pinned g_pin_in, g_pin_out;
+
+static int pinned_reserve(Pinned& b, size_t bytes) {
+  if (bytes <= b.cap) return 0;
+  if (b.p) HIP_TRY(hipHostFree(b.p));
+  b.p = nullptr;
+  b.cap = 0;
+  size_t cap = bytes + bytes / 4;
+  HIP_TRY(hipHostMalloc(&b.p, cap, hipHostMallocDefault));
+  b.cap = cap;
+  return 0;
+}
+
+static int ensure_init() {
+  if (g_ready) return 0;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return kans_fail(KANS_ERR_NODEV, "no HIP device visible (hipGetDeviceCount: %s, count=%d)",
+                     hipGetErrorString(e), n);
+  HIP_TRY(hipGetDevice(&g_device));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, g_device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return kans_fail(KANS_ERR_NODEV, "device %d is %s; this library is built for gfx950 only", g_device,
+                     prop.gcnArchName);
+  HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  g_ready = true;
+  return 0;
+}
+
+hipStream_t kans_default_stream() { return g_stream; }
+
+// ---------------------------------------------------------------------------
+// Device buffers
+// ---------------------------------------------------------------------------
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  ~DevBuf() { if (p) (void)hipFree(p); }
+  int reserve(size_t bytes) {
+    if (bytes <= cap) return 0;
+    if (p) HIP_TRY(hipFree(p));
+    p = nullptr;
+    cap = 0;
+    HIP_TRY(hipMalloc(&p, bytes));
+    cap = bytes;
+    return 0;
+  }
+};
+
+static size_t dtype_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// Layer
+// ---------------------------------------------------------------------------
+struct kans_layer {
+  int basis, dtype, D_in, D_out, K, has_base, has_bias;
+  int D_in8, nfb, nob_pad;
+  BasisParams bp{};
+  std::vector<float> centers;
+  DevBuf centers_d, Wt, bias_d, part, x_d, y_d, raw_w, raw_wb;
+  bool have_weights = false;
+  int forced_wm = 0, forced_nb = 0, forced_splits = 0;  // tuning overrides (0 = heuristic)
+  unsigned gen = 0;  // bumped whenever a buffer captured by a graph may have moved
+};
+
+static int validate_dims(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias) {
+  if (basis < 0 || basis > 2) return kans_fail(KANS_ERR_ARG, "unknown basis %d", basis);
+  if (dtype < 0 || dtype > 2) return kans_fail(KANS_ERR_ARG, "unknown dtype %d", dtype);
+  if (D_in <= 0 || D_out <= 0) return kans_fail(KANS_ERR_ARG, "bad dims D_in=%d D_out=%d", D_in, D_out);
+  if (K <= 0 || K > kMaxK) return kans_fail(KANS_ERR_ARG, "K=%d outside [1, %d]", K, kMaxK);
+  if ((has_base != 0 && has_base != 1) || (has_bias != 0 && has_bias != 1))
+    return kans_fail(KANS_ERR_ARG, "has_base/has_bias must be 0 or 1");
+  return 0;
+}
+
+extern "C" {
+
+const char* kans_last_error(void) { return g_err.c_str(); }
+
+int kans_layer_create(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias,
+                      kans_layer** out) {
+  if (!out) return kans_fail(KANS_ERR_ARG, "null out pointer");
+  int rc = validate_dims(basis, dtype, D_in, D_out, K, has_base, has_bias);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if ((rc = ensure_init())) return rc;
+  auto* L = new kans_layer();
+  L->basis = basis;
+  L->dtype = dtype;
+  L->D_in = D_in;
+  L->D_out = D_out;
+  L->K = K;
+  L->has_base = has_base;
+  L->has_bias = has_bias;
+  L->D_in8 = round_up(D_in, 8);
+  L->nfb = (D_in + 15) / 16;
+  L->nob_pad = round_up((D_out + 31) / 32, kObPad);
+  L->bp.K = K;
+  *out = L;
+  return 0;
+}
+
+int kans_layer_destroy(kans_layer* L) {
+  if (!L) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ready) (void)hipStreamSynchronize(g_stream);
+  delete L;
+  return 0;
+}
+
+int kans_layer_set_rbf(kans_layer* L, const float* centers, float inv_den) {
+  if (!L || !centers) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (L->basis != BASIS_RBF) return kans_fail(KANS_ERR_ARG, "layer basis is not RBF");
+  std::lock_guard<std::mutex> lk(g_mu);
+  L->centers.assign(centers, centers + L->K);
+  void* old = L->centers_d.p;
+  int rc = L->centers_d.reserve(sizeof(float) * kMaxK);
+  if (rc) return rc;
+  if (old != L->centers_d.p) ++L->gen;
+  HIP_TRY(hipMemcpy(L->centers_d.p, L->centers.data(), sizeof(float) * L->K, hipMemcpyHostToDevice));
+  L->bp.centers = (const float*)L->centers_d.p;
+  L->bp.neg_l = -inv_den * kLog2e;
+  return 0;
+}
+
+int kans_layer_set_bspline(kans_layer* L, int grid_size, float grid_min, float inv_h) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  if (L->basis != BASIS_BSPLINE) return kans_fail(KANS_ERR_ARG, "layer basis is not B-spline");
+  if (grid_size <= 0 || grid_size + 3 != L->K)
+    return kans_fail(KANS_ERR_ARG, "grid_size=%d inconsistent with K=%d (K = G + 3)", grid_size, L->K);
+  L->bp.grid_size = grid_size;
+  L->bp.grid_min = grid_min;
+  L->bp.inv_h = inv_h;
+  ++L->gen;  // basis parameters are baked into captured kernel arguments
+  return 0;
+}
+
+int kans_layer_set_tiling(kans_layer* L, int wm, int nb, int splits) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  if (wm != 0 && wm != 32 && wm != 64) return kans_fail(KANS_ERR_ARG, "wm must be 0, 32 or 64");
+  if ((wm == 0) != (nb == 0)) return kans_fail(KANS_ERR_ARG, "wm and nb must both be 0 or both set");
+  if (wm != 0 && !dense_config_supported(wm, nb))
+    return kans_fail(KANS_ERR_ARG, "tile (wm=%d, nb=%d) not instantiated; use (64,4) (32,4) (32,1)", wm, nb);
+  if (splits < 0) return kans_fail(KANS_ERR_ARG, "splits must be >= 0");
+  L->forced_wm = wm;
+  L->forced_nb = nb;
+  L->forced_splits = splits;
+  ++L->gen;
+  return 0;
+}
+
+// Upload weights (host or device memory) whose element type is src_dtype (the
+// layer dtype, or fp32 for a converting upload).  W: [D_out][D_in*K];
+// W_base: [D_out][D_in] (ignored unless has_base); bias: [D_out] (ignored
+// unless has_bias).  Re-tiles W/W_base into the fused kernel's layout.
+static int layer_upload_locked(kans_layer* L, const void* W, const void* Wb, const void* bias, bool device_src,
+                               int src_dtype) {
+  const size_t es = dtype_size(src_dtype);
+  const size_t wbytes = (size_t)L->D_out * L->D_in * L->K * es;
+  const size_t wbbytes = (size_t)L->D_out * L->D_in * es;
+  const int KP = L->K + L->has_base;
+  const size_t tbytes = (size_t)L->nfb * KP * L->nob_pad * 64 * 16 * (L->dtype == DT_F32 ? 2 : 1);
+  int rc;
+  void* old_wt = L->Wt.p;
+  void* old_bias = L->bias_d.p;
+  if ((rc = L->Wt.reserve(tbytes))) return rc;
+  const void* w_src = W;
+  const void* wb_src = Wb;
+  const void* b_src = bias;
+  if (!device_src) {
+    if ((rc = L->raw_w.reserve(wbytes + (L->has_bias ? (size_t)L->D_out * es : 0)))) return rc;
+    HIP_TRY(hipMemcpyAsync(L->raw_w.p, W, wbytes, hipMemcpyHostToDevice, g_stream));
+    w_src = L->raw_w.p;
+    if (L->has_bias) {
+      HIP_TRY(hipMemcpyAsync((char*)L->raw_w.p + wbytes, bias, (size_t)L->D_out * es, hipMemcpyHostToDevice,
+                             g_stream));
+      b_src = (char*)L->raw_w.p + wbytes;
+    }
+    if (L->has_base) {
+      if ((rc = L->raw_wb.reserve(wbbytes))) return rc;
+      HIP_TRY(hipMemcpyAsync(L->raw_wb.p, Wb, wbbytes, hipMemcpyHostToDevice, g_stream));
+      wb_src = L->raw_wb.p;
+    }
+  }
+  HIP_TRY(launch_repack(src_dtype, L->dtype, w_src, L->has_base ? wb_src : nullptr, L->Wt.p, L->D_in, L->D_out,
+                        L->K, L->has_base, L->nfb, L->nob_pad, g_stream));
+  if (L->has_bias) {
+    const size_t bbytes = (size_t)L->D_out * dtype_size(L->dtype);
+    if ((rc = L->bias_d.reserve(bbytes))) return rc;
+    if (src_dtype == L->dtype) {
+      HIP_TRY(hipMemcpyAsync(L->bias_d.p, b_src, bbytes, hipMemcpyDeviceToDevice, g_stream));
+    } else {
+      HIP_TRY(launch_convert(src_dtype, L->dtype, b_src, L->bias_d.p, L->D_out, g_stream));
+    }
+  }
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  if (L->Wt.p != old_wt || L->bias_d.p != old_bias) ++L->gen;
+  L->have_weights = true;
+  return 0;
+}
+
+int kans_layer_load_weights(kans_layer* L, const void* W, const void* W_base, const void* bias) {
+  if (!L || !W) return kans_fail(KANS_ERR_ARG, "null layer or W");
+  if (L->has_base && !W_base) return kans_fail(KANS_ERR_ARG, "has_base=1 but W_base is null");
+  if (L->has_bias && !bias) return kans_fail(KANS_ERR_ARG, "has_bias=1 but bias is null");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_upload_locked(L, W, W_base, bias, false, L->dtype);
+}
+
+int kans_layer_load_weights_f32(kans_layer* L, const float* W, const float* W_base, const float* bias) {
+  if (!L || !W) return kans_fail(KANS_ERR_ARG, "null layer or W");
+  if (L->has_base && !W_base) return kans_fail(KANS_ERR_ARG, "has_base=1 but W_base is null");
+  if (L->has_bias && !bias) return kans_fail(KANS_ERR_ARG, "has_bias=1 but bias is null");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_upload_locked(L, W, W_base, bias, false, DT_F32);
+}
+
+int kans_layer_load_weights_device(kans_layer* L, const void* W, const void* W_base, const void* bias) {
+  if (!L || !W) return kans_fail(KANS_ERR_ARG, "null layer or W");
+  if (L->has_base && !W_base) return kans_fail(KANS_ERR_ARG, "has_base=1 but W_base is null");
+  if (L->has_bias && !bias) return kans_fail(KANS_ERR_ARG, "has_bias=1 but bias is null");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_upload_locked(L, W, W_base, bias, true, L->dtype);
+}
+
+}  // extern "C"
+
+// Tile configuration: among the instantiated (WM, NB) shapes, take the first
+// (largest tile first: basis generation and LDS traffic amortised best) that
+// gives every CU its two resident workgroups; otherwise the one with the most
+// tiles, then split the feature blocks until ~512 workgroups exist.
+static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
+  static const int cand[3][2] = {{64, 4}, {32, 4}, {32, 1}};  // largest tile first
+  const int nob = (L->D_out + 31) / 32;
+  auto tiles = [&](int ww, int nn) { return ((B + 4 * ww - 1) / (4 * ww)) * ((nob + nn - 1) / nn); };
+  int bw = 32, bn = 1, bt = tiles(32, 1);  // (32, 1) always fits
+  for (auto& c : cand) {
+    const int padded = ((nob + c[1] - 1) / c[1]) * c[1];
+    if (c[1] > 1 && 2 * nob < padded) continue;  // over half of the N-tile would be padding
+    const int t = tiles(c[0], c[1]);
+    if (t >= 512) { bw = c[0]; bn = c[1]; bt = t; break; }
+    if (t > bt) { bw = c[0]; bn = c[1]; bt = t; }
+  }
+  int s = 1;
+  if (bt < 384) {
+    s = (512 + bt - 1) / bt;
+    if (s > L->nfb) s = L->nfb;
+    if (s < 1) s = 1;
+  }
+  if (L->forced_wm && L->forced_nb) { bw = L->forced_wm; bn = L->forced_nb; }
+  if (L->forced_splits) s = L->forced_splits;
+  *wm = bw;
+  *nb = bn;
+  *splits = s;
+}
+
+// Reserve the split workspace a forward of batch B needs (no launch).
+static int layer_reserve_locked(kans_layer* L, int B) {
+  int wm, nb, splits;
+  choose_tiling(L, B, &wm, &nb, &splits);
+  if (splits > 1) {
+    void* old = L->part.p;
+    int rc = L->part.reserve((size_t)splits * B * L->D_out * sizeof(float));
+    if (rc) return rc;
+    if (old != L->part.p) ++L->gen;
+  }
+  return 0;
+}
+
+// Enqueue one fused forward; allocates nothing when layer_reserve_locked(L, B)
+// ran before (the chain relies on this while capturing a graph).
+static int layer_launch_locked(kans_layer* L, const void* X, long ldx, void* Y, long ldy, int B, hipStream_t st,
+                               int x_dtype = -1, int y_dtype = -1) {
+  if (x_dtype < 0) x_dtype = L->dtype;
+  if (y_dtype < 0) y_dtype = L->dtype;
+  if ((x_dtype != L->dtype && x_dtype != DT_F32) || (y_dtype != L->dtype && y_dtype != DT_F32))
+    return kans_fail(KANS_ERR_ARG, "input/output dtype must be the layer dtype or fp32");
+  if (!L->have_weights) return kans_fail(KANS_ERR_STATE, "layer has no weights loaded");
+  if (L->basis == BASIS_RBF && !L->bp.centers) return kans_fail(KANS_ERR_STATE, "RBF centres not set");
+  if (L->basis == BASIS_BSPLINE && L->bp.grid_size <= 0) return kans_fail(KANS_ERR_STATE, "B-spline grid not set");
+  if (B <= 0) return 0;
+  if (ldx < L->D_in8 || (ldx % 8) != 0)
+    return kans_fail(KANS_ERR_ARG, "ldx=%ld must be >= %d and a multiple of 8", ldx, L->D_in8);
+  if (x_dtype == DT_F32 && L->dtype != DT_F32 && ((uintptr_t)X & 31) != 0)
+    return kans_fail(KANS_ERR_ARG, "fp32 X must be 32-byte aligned");
+  if (ldy < L->D_out) return kans_fail(KANS_ERR_ARG, "ldy=%ld < D_out=%d", ldy, L->D_out);
+  if (((uintptr_t)X & 15) != 0) return kans_fail(KANS_ERR_ARG, "X must be 16-byte aligned");
+  DenseLaunch D{};
+  D.dtype = L->dtype;
+  D.x_dtype = x_dtype;
+  D.y_dtype = y_dtype;
+  D.basis = L->basis;
+  D.has_base = L->has_base;
+  D.X = X;
+  D.ldx = ldx;
+  D.Wt = L->Wt.p;
+  D.nob_pad = L->nob_pad;
+  D.bias = L->has_bias ? L->bias_d.p : nullptr;
+  D.Y = Y;
+  D.ldy = ldy;
+  D.B = B;
+  D.D_in = L->D_in;
+  D.D_out = L->D_out;
+  D.nfb = L->nfb;
+  D.bp = L->bp;
+  choose_tiling(L, B, &D.wm, &D.nb, &D.splits);
+  if (D.splits > 1) {
+    if (L->part.cap < (size_t)D.splits * B * L->D_out * sizeof(float))
+      return kans_fail(KANS_ERR_STATE, "split workspace not reserved");
+    D.part = (float*)L->part.p;
+  }
+  HIP_TRY(launch_dense(D, st));
+  return 0;
+}
+
+static int layer_forward_locked(kans_layer* L, const void* X, long ldx, void* Y, long ldy, int B, hipStream_t st) {
+  int rc = layer_reserve_locked(L, B);
+  if (rc) return rc;
+  return layer_launch_locked(L, X, ldx, Y, ldy, B, st);
+}
+
+// Host-memory forward: X [B][D_in] (layer dtype, or fp32 for a 16-bit layer)
+// and Y [B][D_out] (layer dtype), contiguous; pinned staging.
+static int layer_forward_host_locked(kans_layer* L, const void* X, void* Y, int B, int x_dtype = -1) {
+  if (B <= 0) return 0;
+  if (x_dtype < 0) x_dtype = L->dtype;
+  const size_t es = dtype_size(L->dtype);
+  const size_t xes = dtype_size(x_dtype);
+  const long ldx = L->D_in8;
+  const size_t xbytes = (size_t)B * ldx * xes;
+  const size_t ybytes = (size_t)B * L->D_out * es;
+  int rc;
+  if ((rc = L->x_d.reserve(xbytes))) return rc;
+  if ((rc = L->y_d.reserve(ybytes))) return rc;
+  void* pin_in;
+  void* pin_out;
+  if (g_async) {
+    HIP_TRY(hipHostMalloc(&pin_in, xbytes, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc(&pin_out, ybytes, hipHostMallocDefault));
+  } else {
+    if ((rc = pinned_reserve(g_pin_in, xbytes))) return rc;
+    if ((rc = pinned_reserve(g_pin_out, ybytes))) return rc;
+    pin_in = g_pin_in.p;
+    pin_out = g_pin_out.p;
+  }
+  if (ldx == L->D_in) {
+    memcpy(pin_in, X, xbytes);
+  } else {  // pad each row with zeros to a multiple of 8 features
+    const size_t rb = (size_t)L->D_in * xes, pb = (size_t)ldx * xes;
+    for (int r = 0; r < B; ++r) {
+      memcpy((char*)pin_in + r * pb, (const char*)X + r * rb, rb);
+      memset((char*)pin_in + r * pb + rb, 0, pb - rb);
+    }
+  }
+  HIP_TRY(hipMemcpyAsync(L->x_d.p, pin_in, xbytes, hipMemcpyHostToDevice, g_stream));
+  if ((rc = layer_reserve_locked(L, B))) return rc;
+  if ((rc = layer_launch_locked(L, L->x_d.p, ldx, L->y_d.p, L->D_out, B, g_stream, x_dtype, L->dtype))) return rc;
+  HIP_TRY(hipMemcpyAsync(pin_out, L->y_d.p, ybytes, hipMemcpyDeviceToHost, g_stream));
+  if (g_async) {
+    g_pending.push_back({pin_out, Y, ybytes});
+    g_pending.push_back({pin_in, nullptr, 0});
+    return 0;
+  }
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  memcpy(Y, pin_out, ybytes);
+  return 0;
+}
+
+static int sync_locked() {
+  if (!g_ready) return 0;
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  for (auto& p : g_pending) {
+    if (p.dst) memcpy(p.dst, p.pinned, p.bytes);
+    (void)hipHostFree(p.pinned);
+  }
+  g_pending.clear();
+  return 0;
+}
+
+extern "C" {
+
+int kans_layer_forward(kans_layer* L, const void* X, long ldx, void* Y, long ldy, int B, void* stream) {
+  if (!L || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_forward_locked(L, X, ldx, Y, ldy, B, stream ? (hipStream_t)stream : g_stream);
+}
+
+int kans_layer_forward_ex(kans_layer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                          void* stream) {
+  if (!L || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = layer_reserve_locked(L, B);
+  if (rc) return rc;
+  return layer_launch_locked(L, X, ldx, Y, ldy, B, stream ? (hipStream_t)stream : g_stream, x_dtype, y_dtype);
+}
+
+int kans_layer_forward_host(kans_layer* L, const void* X, void* Y, int B) {
+  if (!L || (B > 0 && (!X || !Y))) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_forward_host_locked(L, X, Y, B);
+}
+
+int kans_layer_forward_host_ex(kans_layer* L, const void* X, int x_dtype, void* Y, int B) {
+  if (!L || (B > 0 && (!X || !Y))) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (x_dtype != L->dtype && x_dtype != DT_F32)
+    return kans_fail(KANS_ERR_ARG, "x_dtype must be the layer dtype or fp32");
+  std::lock_guard<std::mutex> lk(g_mu);
+  return layer_forward_host_locked(L, X, Y, B, x_dtype);
+}
+
+int kans_layer_describe(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
+  if (!L || !wm || !nb || !splits) return kans_fail(KANS_ERR_ARG, "null argument");
+  choose_tiling(L, B, wm, nb, splits);
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Device memory / stream / timing helpers (tests, benchmarks, integrations).
+// ---------------------------------------------------------------------------
+int kans_init(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return ensure_init();
+}
+
+void* kans_stream(void) { return (void*)g_stream; }
+
+int kans_dev_malloc(void** p, size_t bytes) {
+  if (!p) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  if (rc) return rc;
+  HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
+  return 0;
+}
+
+int kans_dev_free(void* p) {
+  if (!p) return 0;
+  HIP_TRY(hipFree(p));
+  return 0;
+}
+
+int kans_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  if (!dst || !src) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+int kans_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  if (!dst || !src) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+int kans_synchronize(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_ready) return 0;
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+// Time `iters` back-to-back device-resident forwards with HIP events recorded on
+// the stream the kernels run on; returns the mean per forward in *ms.
+int kans_layer_time_forward(kans_layer* L, const void* X, long ldx, void* Y, long ldy, int B, int warmup,
+                            int iters, float* ms) {
+  if (!L || !X || !Y || !ms || iters <= 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc;
+  for (int i = 0; i < warmup; ++i)
+    if ((rc = layer_forward_locked(L, X, ldx, Y, ldy, B, g_stream))) return rc;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, g_stream));
+  for (int i = 0; i < iters; ++i)
+    if ((rc = layer_forward_locked(L, X, ldx, Y, ldy, B, g_stream))) return rc;
+  HIP_TRY(hipEventRecord(e1, g_stream));
+  HIP_TRY(hipEventSynchronize(e1));
+  float t = 0;
+  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Reference-named entry points (metal_kans/device.py:64-474 argtypes).
+// ---------------------------------------------------------------------------
+int metal_kan_init(const char* /*shader_path: unused, kernels are compiled ahead of time*/) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  return rc ? -1 : 0;  // reference: -1 = no device (metal_kan_bridge.mm:293)
+}
+
+int metal_kan_set_async(int enabled) {
+  g_async = enabled ? 1 : 0;
+  return 0;
+}
+
+int metal_kan_sync(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return sync_locked();
+}
+
+}  // extern "C"
+
+// A layer per (shape, params) signature serves the reference-named calls; the
+// caller's host weights are uploaded on every call (the reference reads them
+// in place through zero-copy buffers, so in-place edits must be honoured).
+typedef std::tuple<int, int, int, int, int, int, int, std::vector<float>> SigKey;
+static std::map<SigKey, std::unique_ptr<kans_layer>> g_sig_layers;
+
+static int sig_layer(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias,
+                     const std::vector<float>& params, kans_layer** out) {
+  SigKey key(basis, dtype, D_in, D_out, K, has_base, has_bias, params);
+  auto it = g_sig_layers.find(key);
+  if (it != g_sig_layers.end()) {
+    *out = it->second.get();
+    return 0;
+  }
+  int rc = ensure_init();
+  if (rc) return rc;
+  auto L = std::make_unique<kans_layer>();
+  L->basis = basis;
+  L->dtype = dtype;
+  L->D_in = D_in;
+  L->D_out = D_out;
+  L->K = K;
+  L->has_base = has_base;
+  L->has_bias = has_bias;
+  L->D_in8 = round_up(D_in, 8);
+  L->nfb = (D_in + 15) / 16;
+  L->nob_pad = round_up((D_out + 31) / 32, kObPad);
+  L->bp.K = K;
+  if (basis == BASIS_RBF) {
+    L->centers.assign(params.begin(), params.begin() + K);
+    if ((rc = L->centers_d.reserve(sizeof(float) * kMaxK))) return rc;
+    HIP_TRY(hipMemcpy(L->centers_d.p, L->centers.data(), sizeof(float) * K, hipMemcpyHostToDevice));
+    L->bp.centers = (const float*)L->centers_d.p;
+    L->bp.neg_l = -params[K] * kLog2e;
+  } else if (basis == BASIS_BSPLINE) {
+    L->bp.grid_size = K - 3;
+    L->bp.grid_min = params[0];
+    L->bp.inv_h = params[1];
+  }
+  if (g_sig_layers.size() > 64) g_sig_layers.clear();
+  *out = L.get();
+  g_sig_layers.emplace(key, std::move(L));
+  return 0;
+}
+
+static int ref_forward(int basis, int dtype, const void* X, const void* W, const void* Wb, const void* bias, void* Y,
+                       int B, int D_in, int D_out, int K, int has_base, int has_bias,
+                       const std::vector<float>& params) {
+  if (!X || !W || !Y) return kans_fail(KANS_ERR_ARG, "null X, W or Y");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  int rc = validate_dims(basis, dtype, D_in, D_out, K, has_base, has_bias);
+  if (rc) return rc;
+  if (has_base && !Wb) return kans_fail(KANS_ERR_ARG, "has_base=1 but W_base is null");
+  if (has_bias && !bias) return kans_fail(KANS_ERR_ARG, "has_bias=1 but bias is null");
+  std::lock_guard<std::mutex> lk(g_mu);
+  kans_layer* L;
+  if ((rc = sig_layer(basis, dtype, D_in, D_out, K, has_base, has_bias, params, &L))) return rc;
+  if ((rc = layer_upload_locked(L, W, Wb, bias, false, dtype))) return rc;
+  return layer_forward_host_locked(L, X, Y, B);
+}
+
+static void half_to_floats(const uint16_t* h, float* f, int n) {
+  for (int i = 0; i < n; ++i) {
+    _Float16 v;
+    memcpy(&v, &h[i], 2);
+    f[i] = (float)v;
+  }
+}
+
+extern "C" {
+
+int metal_kan_cheby_forward(const float* X, const float* W, const float* Wb, const float* bias, float* Y, int B,
+                            int D_in, int D_out, int K, int has_base, int has_bias) {
+  return ref_forward(BASIS_CHEBY, DT_F32, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, {});
+}
+int metal_kan_cheby_forward_fp16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const uint16_t* bias,
+                                 uint16_t* Y, int B, int D_in, int D_out, int K, int has_base, int has_bias) {
+  return ref_forward(BASIS_CHEBY, DT_F16, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, {});
+}
+int metal_kan_cheby_forward_bf16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const uint16_t* bias,
+                                 uint16_t* Y, int B, int D_in, int D_out, int K, int has_base, int has_bias) {
+  return ref_forward(BASIS_CHEBY, DT_BF16, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, {});
+}
+
+int metal_kan_fastkan_forward(const float* X, const float* W, const float* Wb, const float* grid, const float* bias,
+                              float* Y, int B, int D_in, int D_out, int K, float inv_den, int has_base,
+                              int has_bias) {
+  if (!grid || K <= 0 || K > kMaxK) return kans_fail(KANS_ERR_ARG, "null grid or bad K");
+  std::vector<float> p(grid, grid + K);
+  p.push_back(inv_den);
+  return ref_forward(BASIS_RBF, DT_F32, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, p);
+}
+int metal_kan_fastkan_forward_fp16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const uint16_t* grid,
+                                   const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int K,
+                                   float inv_den, int has_base, int has_bias) {
+  if (!grid || K <= 0 || K > kMaxK) return kans_fail(KANS_ERR_ARG, "null grid or bad K");
+  std::vector<float> p(K);
+  half_to_floats(grid, p.data(), K);
+  p.push_back(inv_den);
+  return ref_forward(BASIS_RBF, DT_F16, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, p);
+}
+int metal_kan_fastkan_forward_bf16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const float* grid,
+                                   const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int K,
+                                   float inv_den, int has_base, int has_bias) {
+  if (!grid || K <= 0 || K > kMaxK) return kans_fail(KANS_ERR_ARG, "null grid or bad K");
+  std::vector<float> p(grid, grid + K);
+  p.push_back(inv_den);
+  return ref_forward(BASIS_RBF, DT_BF16, X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias, p);
+}
+
+static int bspline_common(int dtype, const void* X, const void* W, const void* Wb, const float* grid,
+                          const void* bias, void* Y, int B, int D_in, int D_out, int G, int has_base,
+                          int has_bias) {
+  if (!grid) return kans_fail(KANS_ERR_ARG, "null grid params");
+  if (G <= 0 || G + 3 > kMaxK) return kans_fail(KANS_ERR_ARG, "grid_size=%d out of range", G);
+  std::vector<float> p{grid[0], grid[1]};
+  return ref_forward(BASIS_BSPLINE, dtype, X, W, Wb, bias, Y, B, D_in, D_out, G + 3, has_base, has_bias, p);
+}
+
+// grid = [grid_min, inv_h] (fp32, read on the host as metal_kan_bridge.mm:1138-1139 does);
+// spline_order is accepted and ignored, as in the reference (always cubic).
+int metal_kan_bspline_forward(const float* X, const float* W, const float* Wb, const float* grid, const float* bias,
+                              float* Y, int B, int D_in, int D_out, int G, int /*spline_order*/, int has_base,
+                              int has_bias) {
+  return bspline_common(DT_F32, X, W, Wb, grid, bias, Y, B, D_in, D_out, G, has_base, has_bias);
+}
+int metal_kan_bspline_forward_fp16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const float* grid,
+                                   const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int G,
+                                   int /*spline_order*/, int has_base, int has_bias) {
+  return bspline_common(DT_F16, X, W, Wb, grid, bias, Y, B, D_in, D_out, G, has_base, has_bias);
+}
+int metal_kan_bspline_forward_bf16(const uint16_t* X, const uint16_t* W, const uint16_t* Wb, const float* grid,
+                                   const uint16_t* bias, uint16_t* Y, int B, int D_in, int D_out, int G,
+                                   int /*spline_order*/, int has_base, int has_bias) {
+  return bspline_common(DT_BF16, X, W, Wb, grid, bias, Y, B, D_in, D_out, G, has_base, has_bias);
+}
+
+// Wall-clock per full host call, warmup then iters (metal_kan_bridge.mm:1250-1277).
+double benchmark_metal_cheby(const float* X, const float* W, const float* Wb, const float* bias, float* Y, int B,
+                             int D_in, int D_out, int K, int has_base, int has_bias, int warmup, int iters) {
+  for (int i = 0; i < warmup; ++i)
+    if (metal_kan_cheby_forward(X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias)) return -1.0;
+  auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < iters; ++i)
+    if (metal_kan_cheby_forward(X, W, Wb, bias, Y, B, D_in, D_out, K, has_base, has_bias)) return -1.0;
+  auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration<double, std::milli>(t1 - t0).count() / (iters > 0 ? iters : 1);
+}
+
+double benchmark_metal_fastkan(const float* X, const float* W, const float* Wb, const float* grid, const float* bias,
+                               float* Y, int B, int D_in, int D_out, int K, float inv_den, int has_base,
+                               int has_bias, int warmup, int iters) {
+  for (int i = 0; i < warmup; ++i)
+    if (metal_kan_fastkan_forward(X, W, Wb, grid, bias, Y, B, D_in, D_out, K, inv_den, has_base, has_bias))
+      return -1.0;
+  auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < iters; ++i)
+    if (metal_kan_fastkan_forward(X, W, Wb, grid, bias, Y, B, D_in, D_out, K, inv_den, has_base, has_bias))
+      return -1.0;
+  auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration<double, std::milli>(t1 - t0).count() / (iters > 0 ? iters : 1);
+}
+
+double benchmark_metal_bspline(const float* X, const float* W, const float* Wb, const float* grid, const float* bias,
+                               float* Y, int B, int D_in, int D_out, int G, int order, int has_base, int has_bias,
+                               int warmup, int iters) {
+  for (int i = 0; i < warmup; ++i)
+    if (metal_kan_bspline_forward(X, W, Wb, grid, bias, Y, B, D_in, D_out, G, order, has_base, has_bias))
+      return -1.0;
+  auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < iters; ++i)
+    if (metal_kan_bspline_forward(X, W, Wb, grid, bias, Y, B, D_in, D_out, G, order, has_base, has_bias))
+      return -1.0;
+  auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration<double, std::milli>(t1 - t0).count() / (iters > 0 ? iters : 1);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Multi-layer chain (replaces metal_kan_chain_pipeline_cheby,
+// metal_kan_bridge.mm:1168-1248, which is fp32 / K=4 only and allocates its
+// ping-pong buffers per call).  Device-resident ping-pong activations; the
+// host path (H2D, every layer, D2H) is captured once per batch size as a HIP
+// graph and replayed.
+// ---------------------------------------------------------------------------
+struct kans_chain {
+  std::vector<kans_layer*> layers;
+  std::vector<std::unique_ptr<kans_layer>> owned;  // layers created by metal_kan_chain_pipeline_cheby
+  int dtype = 0;
+  int mid_dtype = 0;  // activations between layers: fp32 (also for 16-bit chains)
+  long ld_in = 0, ld_mid = 0, ld_out = 0;
+  int cap_B = 0;
+  DevBuf x_d, ping, pong, y_d;
+  Pinned pin_in, pin_out;
+  int in_dtype = 0;  // element type of the chain input (chain dtype or fp32)
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int graph_B = -1;
+  int graph_in = -1;
+  unsigned graph_gen = 0;
+  bool graph_copies = false;
+  ~kans_chain() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (pin_in.p) (void)hipHostFree(pin_in.p);
+    if (pin_out.p) (void)hipHostFree(pin_out.p);
+  }
+};
+
+static unsigned chain_gen(const kans_chain* C) {
+  unsigned g = 0;
+  for (auto* L : C->layers) g = g * 31u + L->gen;
+  return g;
+}
+
+static int chain_reserve(kans_chain* C, int B) {
+  int rc;
+  if (B > C->cap_B) {
+    const size_t es = dtype_size(C->dtype);
+    void* olds[4] = {C->x_d.p, C->ping.p, C->pong.p, C->y_d.p};
+    if ((rc = C->x_d.reserve((size_t)B * C->ld_in * 4))) return rc;  // room for an fp32 input
+    const size_t ms = dtype_size(C->mid_dtype);
+    if ((rc = C->ping.reserve((size_t)B * C->ld_mid * ms))) return rc;
+    if ((rc = C->pong.reserve((size_t)B * C->ld_mid * ms))) return rc;
+    if ((rc = C->y_d.reserve((size_t)B * C->ld_out * es))) return rc;
+    // padding columns must hold finite values; zero everything once, outside any graph
+    HIP_TRY(hipMemsetAsync(C->x_d.p, 0, C->x_d.cap, g_stream));
+    HIP_TRY(hipMemsetAsync(C->ping.p, 0, C->ping.cap, g_stream));
+    HIP_TRY(hipMemsetAsync(C->pong.p, 0, C->pong.cap, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    if ((rc = pinned_reserve(C->pin_in, (size_t)B * C->ld_in * 4))) return rc;
+    if ((rc = pinned_reserve(C->pin_out, (size_t)B * C->ld_out * es))) return rc;
+    C->cap_B = B;
+    void* news[4] = {C->x_d.p, C->ping.p, C->pong.p, C->y_d.p};
+    for (int i = 0; i < 4; ++i)
+      if (olds[i] != news[i]) C->graph_B = -1;
+  }
+  for (auto* L : C->layers)
+    if ((rc = layer_reserve_locked(L, B))) return rc;
+  return 0;
+}
+
+// Enqueue all layers: X (ldx) -> ... -> Y (ldy) through the ping-pong buffers.
+static int chain_launch(kans_chain* C, const void* X, long ldx, void* Y, long ldy, int B, hipStream_t st) {
+  const void* src = X;
+  long lds = ldx;
+  const size_t n = C->layers.size();
+  for (size_t l = 0; l < n; ++l) {
+    void* dst = (l + 1 == n) ? Y : ((l % 2 == 0) ? C->pong.p : C->ping.p);
+    long ldd = (l + 1 == n) ? ldy : C->ld_mid;
+    const int xdt = (l == 0) ? C->in_dtype : C->mid_dtype;
+    const int ydt = (l + 1 == n) ? C->dtype : C->mid_dtype;
+    int rc = layer_launch_locked(C->layers[l], src, lds, dst, ldd, B, st, xdt, ydt);
+    if (rc) return rc;
+    src = dst;
+    lds = ldd;
+  }
+  return 0;
+}
+
+static int chain_capture(kans_chain* C, int B, bool copies) {
+  if (C->exec) { (void)hipGraphExecDestroy(C->exec); C->exec = nullptr; }
+  if (C->graph) { (void)hipGraphDestroy(C->graph); C->graph = nullptr; }
+  const size_t es = dtype_size(C->dtype);
+  const size_t ies = dtype_size(C->in_dtype);
+  HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+  int rc = 0;
+  if (copies) {
+    hipError_t e = hipMemcpyAsync(C->x_d.p, C->pin_in.p, (size_t)B * C->ld_in * ies, hipMemcpyHostToDevice, g_stream);
+    if (e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "capture H2D: %s", hipGetErrorString(e));
+  }
+  if (!rc) rc = chain_launch(C, C->x_d.p, C->ld_in, C->y_d.p, C->ld_out, B, g_stream);
+  if (!rc && copies) {
+    hipError_t e = hipMemcpyAsync(C->pin_out.p, C->y_d.p, (size_t)B * C->ld_out * es, hipMemcpyDeviceToHost,
+                                  g_stream);
+    if (e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "capture D2H: %s", hipGetErrorString(e));
+  }
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+  if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  C->graph = g;
+  HIP_TRY(hipGraphInstantiate(&C->exec, C->graph, nullptr, nullptr, 0));
+  C->graph_B = B;
+  C->graph_in = C->in_dtype;
+  C->graph_gen = chain_gen(C);
+  C->graph_copies = copies;
+  return 0;
+}
+
+static int chain_graph_ready(kans_chain* C, int B, bool copies) {
+  int rc = chain_reserve(C, B);
+  if (rc) return rc;
+  if (C->exec && C->graph_B == B && C->graph_in == C->in_dtype && C->graph_gen == chain_gen(C) &&
+      C->graph_copies == copies)
+    return 0;
+  return chain_capture(C, B, copies);
+}
+
+extern "C" {
+
+int kans_chain_create(kans_layer** layers, int n, kans_chain** out) {
+  if (!layers || n <= 0 || !out) return kans_fail(KANS_ERR_ARG, "bad chain arguments");
+  for (int i = 0; i < n; ++i)
+    if (!layers[i]) return kans_fail(KANS_ERR_ARG, "null layer %d", i);
+  for (int i = 0; i + 1 < n; ++i) {
+    if (layers[i]->D_out != layers[i + 1]->D_in)
+      return kans_fail(KANS_ERR_ARG, "layer %d D_out=%d != layer %d D_in=%d", i, layers[i]->D_out, i + 1,
+                       layers[i + 1]->D_in);
+    if (layers[i]->dtype != layers[i + 1]->dtype) return kans_fail(KANS_ERR_ARG, "mixed dtypes in chain");
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  if (rc) return rc;
+  auto* C = new kans_chain();
+  C->layers.assign(layers, layers + n);
+  C->dtype = layers[0]->dtype;
+  C->in_dtype = C->dtype;
+  C->mid_dtype = DT_F32;
+  C->ld_in = layers[0]->D_in8;
+  long mid = 8;
+  for (int i = 0; i + 1 < n; ++i) mid = std::max<long>(mid, round_up(layers[i]->D_out, 8));
+  C->ld_mid = mid;
+  C->ld_out = layers[n - 1]->D_out;
+  *out = C;
+  return 0;
+}
+
+int kans_chain_destroy(kans_chain* C) {
+  if (!C) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ready) (void)hipStreamSynchronize(g_stream);
+  delete C;
+  return 0;
+}
+
+// Host arrays [B][D_in0] (x_dtype: chain dtype, or fp32) -> [B][D_out_last]
+// (chain dtype), one graph replay.
+int kans_chain_forward_host_ex(kans_chain* C, const void* X, int x_dtype, void* Y, int B) {
+  if (!C || (B > 0 && (!X || !Y)) || B < 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  if (x_dtype != C->dtype && x_dtype != DT_F32) return kans_fail(KANS_ERR_ARG, "x_dtype must be the chain dtype or fp32");
+  if (B == 0) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  C->in_dtype = x_dtype;
+  const bool async = g_async != 0;
+  // async mode: kernels-only graph with per-call pinned staging (results land at metal_kan_sync)
+  int rc = chain_graph_ready(C, B, !async);
+  if (rc) return rc;
+  const size_t es = dtype_size(C->dtype);
+  const size_t xes = dtype_size(x_dtype);
+  const int D0 = C->layers[0]->D_in;
+  const size_t in_bytes = (size_t)B * C->ld_in * xes, out_bytes = (size_t)B * C->ld_out * es;
+  void* pin_in = C->pin_in.p;
+  void* pin_out = C->pin_out.p;
+  if (async) {
+    HIP_TRY(hipHostMalloc(&pin_in, in_bytes, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault));
+  }
+  if (C->ld_in == D0) {
+    memcpy(pin_in, X, (size_t)B * D0 * xes);
+  } else {
+    for (int r = 0; r < B; ++r) {
+      memcpy((char*)pin_in + (size_t)r * C->ld_in * xes, (const char*)X + (size_t)r * D0 * xes, (size_t)D0 * xes);
+      memset((char*)pin_in + ((size_t)r * C->ld_in + D0) * xes, 0, (size_t)(C->ld_in - D0) * xes);
+    }
+  }
+  if (async) {
+    HIP_TRY(hipMemcpyAsync(C->x_d.p, pin_in, in_bytes, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipGraphLaunch(C->exec, g_stream));
+    HIP_TRY(hipMemcpyAsync(pin_out, C->y_d.p, out_bytes, hipMemcpyDeviceToHost, g_stream));
+    g_pending.push_back({pin_out, Y, out_bytes});
+    g_pending.push_back({pin_in, nullptr, 0});
+    return 0;
+  }
+  HIP_TRY(hipGraphLaunch(C->exec, g_stream));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  memcpy(Y, pin_out, out_bytes);
+  return 0;
+}
+
+int kans_chain_forward_host(kans_chain* C, const void* X, void* Y, int B) {
+  return kans_chain_forward_host_ex(C, X, C ? C->dtype : 0, Y, B);
+}
+
+// Device arrays: X [B][ldx] (ldx >= round_up(D_in0, 8), multiple of 8), Y [B][ldy]; eager launches.
+int kans_chain_forward(kans_chain* C, const void* X, long ldx, void* Y, long ldy, int B, void* stream) {
+  if (!C || !X || !Y || B < 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = chain_reserve(C, B);
+  if (rc) return rc;
+  C->in_dtype = C->dtype;
+  return chain_launch(C, X, ldx, Y, ldy, B, stream ? (hipStream_t)stream : g_stream);
+}
+
+// Time `iters` replays of the chain graph; include_copies = 1 also replays the
+// pinned H2D / D2H copies.  *ms = mean per replay (HIP events on the stream).
+int kans_chain_time(kans_chain* C, int B, int warmup, int iters, int include_copies, float* ms) {
+  if (!C || B <= 0 || iters <= 0 || !ms) return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(g_mu);  // replays the graph of the last host call's input dtype
+  int rc = chain_graph_ready(C, B, include_copies != 0);
+  if (rc) return rc;
+  for (int i = 0; i < warmup; ++i) HIP_TRY(hipGraphLaunch(C->exec, g_stream));
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, g_stream));
+  for (int i = 0; i < iters; ++i) HIP_TRY(hipGraphLaunch(C->exec, g_stream));
+  HIP_TRY(hipEventRecord(e1, g_stream));
+  HIP_TRY(hipEventSynchronize(e1));
+  float t = 0;
+  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return 0;
+}
+
+// Reference-named fp32 Chebyshev chain (device.py:116-122): host weights are
+// read on every call (uploaded into the chain's own layers), the activations
+// never leave the device between layers.  A null W_bases[l] / biases[l]
+// disables that branch for layer l, as in the reference.  Generalises the
+// reference (any K per layer, not only 4).
+typedef std::vector<int> ChainKey;
+static std::map<ChainKey, std::unique_ptr<kans_chain>> g_ref_chains;
+
+int metal_kan_chain_pipeline_cheby(const float* X, float* Y, int B, int num_layers, const int* dims,
+                                   const int* degrees, const float** W_chebys, const float** W_bases,
+                                   const float** biases) {
+  if (!X || !Y || B < 0 || num_layers <= 0 || !dims || !degrees || !W_chebys)
+    return kans_fail(KANS_ERR_ARG, "chain: bad argument");
+  ChainKey key;
+  for (int l = 0; l < num_layers; ++l) {
+    if (!W_chebys[l]) return kans_fail(KANS_ERR_ARG, "chain: null W_cheby[%d]", l);
+    int rc = validate_dims(BASIS_CHEBY, DT_F32, dims[l], dims[l + 1], degrees[l], 0, 0);
+    if (rc) return rc;
+    key.insert(key.end(), {dims[l], dims[l + 1], degrees[l], (W_bases && W_bases[l]) ? 1 : 0,
+                           (biases && biases[l]) ? 1 : 0});
+  }
+  if (B == 0) return 0;
+  kans_chain* C = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_init();
+    if (rc) return rc;
+    auto it = g_ref_chains.find(key);
+    if (it == g_ref_chains.end()) {
+      auto ch = std::make_unique<kans_chain>();
+      for (int l = 0; l < num_layers; ++l) {
+        auto L = std::make_unique<kans_layer>();
+        L->basis = BASIS_CHEBY;
+        L->dtype = DT_F32;
+        L->D_in = dims[l];
+        L->D_out = dims[l + 1];
+        L->K = degrees[l];
+        L->has_base = key[5 * l + 3];
+        L->has_bias = key[5 * l + 4];
+        L->D_in8 = round_up(L->D_in, 8);
+        L->nfb = (L->D_in + 15) / 16;
+        L->nob_pad = round_up((L->D_out + 31) / 32, kObPad);
+        L->bp.K = L->K;
+        ch->layers.push_back(L.get());
+        ch->owned.push_back(std::move(L));
+      }
+      ch->dtype = DT_F32;
+      ch->in_dtype = DT_F32;
+      ch->mid_dtype = DT_F32;
+      ch->ld_in = ch->layers[0]->D_in8;
+      long mid = 8;
+      for (int l = 0; l + 1 < num_layers; ++l) mid = std::max<long>(mid, round_up(dims[l + 1], 8));
+      ch->ld_mid = mid;
+      ch->ld_out = dims[num_layers];
+      if (g_ref_chains.size() > 16) g_ref_chains.clear();
+      it = g_ref_chains.emplace(key, std::move(ch)).first;
+    }
+    C = it->second.get();
+    for (int l = 0; l < num_layers; ++l) {
+      kans_layer* L = C->layers[l];
+      rc = layer_upload_locked(L, W_chebys[l], L->has_base ? W_bases[l] : nullptr, L->has_bias ? biases[l] : nullptr,
+                               false, DT_F32);
+      if (rc) return rc;
+    }
+  }
+  return kans_chain_forward_host(C, X, Y, B);
+}
+
+}  // extern "C"

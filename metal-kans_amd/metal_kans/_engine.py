@@ -1,0 +1,164 @@
+"""Device-resident execution of one KAN layer through the HIP library.
+
+The reference re-reads the host weight arrays on every call through zero-copy
+Metal buffers (metal_kan_bridge.mm:409-441).  On a discrete GPU the weights live
+in HBM, re-tiled for the fused kernel, and are re-uploaded only when they
+change.  A change is detected by
+
+* identity: a different array object, data pointer, shape or dtype (covers
+  ``half()``, ``float()``, ``to_int4()``, attribute assignment);
+* content, for arrays of at most ``VERIFY_BYTES`` bytes: compared byte-for-byte
+  against the last uploaded copy (covers in-place edits such as the
+  finite-difference loops in the reference's tests).
+
+In-place edits of larger arrays must be announced with ``layer.invalidate()``.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import device
+
+BASIS = {"cheby": 0, "rbf": 1, "bspline": 2}
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+VERIFY_BYTES = 4 << 20
+
+
+def dtype_code(kind: str) -> int:
+    return {"float32": DT_F32, "float16": DT_F16, "bfloat16": DT_BF16}[kind]
+
+
+class _Snapshot:
+    __slots__ = ("ref", "ptr", "shape", "dtype", "copy")
+
+    def __init__(self, a: Optional[np.ndarray]):
+        self.ref = a
+        if a is None:
+            self.ptr, self.shape, self.dtype, self.copy = 0, None, None, None
+            return
+        self.ptr = a.ctypes.data
+        self.shape = a.shape
+        self.dtype = a.dtype.str
+        self.copy = a.copy() if a.nbytes <= VERIFY_BYTES else None
+
+    def same(self, a: Optional[np.ndarray]) -> bool:
+        if a is None or self.ref is None:
+            return a is None and self.ref is None
+        if a is not self.ref or a.ctypes.data != self.ptr or a.shape != self.shape or a.dtype.str != self.dtype:
+            return False
+        if self.copy is not None:
+            return bool(np.array_equal(a.view(np.uint8), self.copy.view(np.uint8)))
+        return True
+
+
+class LayerEngine:
+    """Owns a ``kans_layer`` handle (device weights) for one Python layer."""
+
+    def __init__(self, basis: str, d_in: int, d_out: int, K: int, has_base: int, has_bias: int):
+        self.basis = basis
+        self.d_in = int(d_in)
+        self.d_out = int(d_out)
+        self.K = int(K)
+        self.has_base = int(has_base)
+        self.has_bias = int(has_bias)
+        self.handle = ctypes.c_void_p()
+        self.dt = None
+        self.params = None
+        self.snaps: Optional[Sequence[_Snapshot]] = None
+        self.tiling = (0, 0, 0)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                device.load_library().kans_layer_destroy(self.handle)
+        except Exception:
+            pass
+
+    def invalidate(self) -> None:
+        self.snaps = None
+
+    def _ensure_handle(self, dt: int) -> ctypes.CDLL:
+        lib = device.get_metal_bridge()
+        if self.handle and self.dt == dt:
+            return lib
+        if self.handle:
+            lib.kans_layer_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+        h = ctypes.c_void_p()
+        device.check(lib.kans_layer_create(BASIS[self.basis], dt, self.d_in, self.d_out, self.K, self.has_base,
+                                           self.has_bias, ctypes.byref(h)), "kans_layer_create")
+        self.handle = h
+        self.dt = dt
+        self.params = None
+        self.snaps = None
+        if self.tiling != (0, 0, 0):
+            device.check(lib.kans_layer_set_tiling(self.handle, *self.tiling), "kans_layer_set_tiling")
+        return lib
+
+    def set_tiling(self, wm: int, nb: int, splits: int = 0) -> None:
+        self.tiling = (int(wm), int(nb), int(splits))
+        if self.handle:
+            device.check(device.get_metal_bridge().kans_layer_set_tiling(self.handle, *self.tiling),
+                         "kans_layer_set_tiling")
+
+    def prepare_f32(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
+                    params: tuple) -> None:
+        """As ``prepare`` with float32 host arrays converted on the device to dtype ``dt``."""
+        self.prepare(dt, W, W_base, bias, params, src_f32=True)
+
+    def prepare(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
+                params: tuple, src_f32: bool = False) -> None:
+        """Make the device copy current: handle for dtype, basis params, weights."""
+        lib = self._ensure_handle(dt)
+        if params != self.params:
+            if self.basis == "rbf":
+                centers = np.ascontiguousarray(params[0], dtype=np.float32)
+                device.check(lib.kans_layer_set_rbf(self.handle, centers.ctypes.data, float(params[1])),
+                             "kans_layer_set_rbf")
+            elif self.basis == "bspline":
+                device.check(lib.kans_layer_set_bspline(self.handle, int(params[0]), float(params[1]),
+                                                        float(params[2])), "kans_layer_set_bspline")
+            self.params = params
+        arrays = (W, W_base if self.has_base else None, bias if self.has_bias else None)
+        if self.snaps is not None and all(s.same(a) for s, a in zip(self.snaps, arrays)):
+            return
+        for a in arrays:
+            if a is not None and not a.flags["C_CONTIGUOUS"]:
+                raise ValueError("weights must be C-contiguous")
+        load = lib.kans_layer_load_weights_f32 if src_f32 else lib.kans_layer_load_weights
+        device.check(load(
+            self.handle, W.ctypes.data,
+            arrays[1].ctypes.data if arrays[1] is not None else None,
+            arrays[2].ctypes.data if arrays[2] is not None else None), "kans_layer_load_weights")
+        self.snaps = tuple(_Snapshot(a) for a in arrays)
+
+    def forward_host(self, x: np.ndarray, y: np.ndarray) -> None:
+        """x in the layer dtype, or float32 for a 16-bit layer (used unrounded)."""
+        lib = device.get_metal_bridge()
+        if x.dtype == np.float32 and self.dt != DT_F32:
+            device.check(lib.kans_layer_forward_host_ex(self.handle, x.ctypes.data, DT_F32, y.ctypes.data,
+                                                        int(x.shape[0])), "kans_layer_forward_host_ex")
+            return
+        device.check(lib.kans_layer_forward_host(self.handle, x.ctypes.data, y.ctypes.data, int(x.shape[0])),
+                     "kans_layer_forward_host")
+
+
+# ----------------------------------------------------------------------------
+# bfloat16 host storage (NumPy has no bf16): uint16 bit patterns, RNE rounding.
+# ----------------------------------------------------------------------------
+
+def to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(a, dtype=np.float32)
+    u = f.view(np.uint32)
+    out = ((u + (((u >> 16) & 1) + np.uint32(0x7FFF))) >> 16).astype(np.uint16)
+    nan = np.isnan(f)
+    if nan.any():
+        out[nan] = np.uint16(0x7FC0)
+    return out
+
+
+def from_bf16_bits(u: np.ndarray) -> np.ndarray:
+    return (np.asarray(u, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)

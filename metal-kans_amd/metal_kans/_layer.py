@@ -1,0 +1,164 @@
+"""Shared forward plumbing of the ChebyKAN / FastKAN / BSplineKAN layers.
+
+The forward mirrors the reference layers (cheby_kan.py:92-141,
+fast_kan.py:99-147, bspline_kan.py:104-152): cast x to the compute dtype,
+flatten leading dims, make it C-contiguous, keep it in ``_saved_x``, check
+``in_features``, allocate ``y`` and call the device.  The device call is the
+fused HIP kernel through a device-resident layer (weights uploaded and re-tiled
+once, see ``_engine.py``).
+
+Compute dtypes: ``float32`` and ``float16`` as in the reference (``.float()``,
+``.half()``); ``bfloat16`` is new (``.bfloat16()``).  NumPy has no bf16, so a
+bf16 layer keeps float32 attribute arrays holding bf16-rounded values and
+returns float32 arrays holding bf16 values.
+
+Inputs of 16-bit layers: an fp16 input to an fp16 layer is used as given (the
+reference casts x to the weight dtype, cheby_kan.py:97-101); a float32 input
+is NOT rounded to 16 bits first -- the kernel reads it in fp32 and evaluates the
+basis in fp32 ("FP32-internal"), only the weights and the MFMA operands are
+16-bit.  Rounding x first costs accuracy for large K: T_k'(+-1) = k^2.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from ._engine import DT_BF16, DT_F16, DT_F32, LayerEngine, from_bf16_bits, to_bf16_bits
+from . import device
+
+
+class KANLayerBase:
+    _basis: str = ""
+    _weight_attr: str = ""
+
+    # subclasses set: in_features, out_features, has_base, has_bias, w_base, bias
+    _compute: str = "float32"
+    _engine_obj: Optional[LayerEngine] = None
+
+    # ---- to be provided by subclasses ------------------------------------
+    def _num_basis(self) -> int:
+        raise NotImplementedError
+
+    def _basis_params(self) -> tuple:
+        return ()
+
+    # ---- dtype handling --------------------------------------------------
+    @property
+    def dtype(self) -> np.dtype:
+        """dtype of the basis weight array, as in the reference."""
+        return getattr(self, self._weight_attr).dtype
+
+    @property
+    def compute_dtype(self) -> str:
+        """'float32' | 'float16' | 'bfloat16': the arithmetic the forward runs in."""
+        return self._compute
+
+    def _cast_params(self, dtype) -> None:
+        setattr(self, self._weight_attr, getattr(self, self._weight_attr).astype(dtype))
+        if self.has_base:
+            self.w_base = self.w_base.astype(dtype)
+        if self.has_bias:
+            self.bias = self.bias.astype(dtype)
+
+    def bfloat16(self):
+        """Converts layer parameters to bfloat16 (stored as bf16-rounded float32 arrays)."""
+        def rnd(a):
+            return from_bf16_bits(to_bf16_bits(a)).reshape(a.shape)
+        setattr(self, self._weight_attr, rnd(getattr(self, self._weight_attr)))
+        if self.has_base:
+            self.w_base = rnd(self.w_base)
+        if self.has_bias:
+            self.bias = rnd(self.bias)
+        self._compute = "bfloat16"
+        return self
+
+    def invalidate(self) -> None:
+        """Announce an in-place edit of a weight array larger than 4 MB."""
+        if self._engine_obj is not None:
+            self._engine_obj.invalidate()
+
+    def set_tiling(self, wm: int, nb: int, splits: int = 0) -> None:
+        """Force the fused kernel's tile shape (tuning/testing); (0, 0) restores the heuristic."""
+        self._engine().set_tiling(wm, nb, splits)
+
+    def _engine(self) -> LayerEngine:
+        if self._engine_obj is None:
+            self._engine_obj = LayerEngine(self._basis, self.in_features, self.out_features, self._num_basis(),
+                                           self.has_base, self.has_bias)
+        return self._engine_obj
+
+    def _resolve_compute(self) -> str:
+        wd = self.dtype
+        if self._compute == "bfloat16":
+            return "bfloat16"
+        if self._compute == "float16" and getattr(self, "_quantized_from", None) == "float16":
+            return "float16"  # quantized layer keeps its fp16 activations
+        return "float16" if wd == np.float16 else "float32"
+
+    # ---- forward ----------------------------------------------------------
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        compute = self._resolve_compute()
+        x = x if isinstance(x, np.ndarray) else np.asarray(x)
+        if compute == "float32":
+            io_dtype = np.float32
+        elif compute == "float16" and x.dtype == np.float16:
+            io_dtype = np.float16          # fp16 input used as given (reference semantics)
+        else:
+            io_dtype = np.float32          # fp32 input to a 16-bit layer is not rounded first
+        if x.dtype != io_dtype:
+            x = x.astype(io_dtype)
+        orig_shape = x.shape
+        if x.ndim > 2:
+            x = x.reshape(-1, self.in_features)
+        if not x.flags["C_CONTIGUOUS"]:
+            x = np.ascontiguousarray(x)
+        self._saved_x = x
+        self._saved_shape = orig_shape
+        B, D_in = x.shape
+        if D_in != self.in_features:
+            raise ValueError(f"Expected in_features={self.in_features}, got {D_in}")
+
+        W = getattr(self, self._weight_attr)
+        Wb = self.w_base if self.has_base else None
+        bias = self.bias if self.has_bias else None
+        eng = self._engine()
+        if compute == "bfloat16":
+            eng.prepare_f32(DT_BF16, np.ascontiguousarray(W, dtype=np.float32),
+                            None if Wb is None else np.ascontiguousarray(Wb, dtype=np.float32),
+                            None if bias is None else np.ascontiguousarray(bias, dtype=np.float32),
+                            self._basis_params())
+            yb = np.empty((B, self.out_features), dtype=np.uint16)
+            eng.forward_host(x, yb)
+            y = from_bf16_bits(yb).reshape(B, self.out_features)
+        else:
+            np_dt = np.float16 if compute == "float16" else np.float32
+            dt = DT_F16 if compute == "float16" else DT_F32
+
+            def conv(a):
+                if a is None:
+                    return None
+                return a if (a.dtype == np_dt and a.flags["C_CONTIGUOUS"]) else self._converted(a, np_dt)
+            eng.prepare(dt, conv(W), conv(Wb), conv(bias), self._basis_params())
+            y = np.empty((B, self.out_features), dtype=np_dt)
+            eng.forward_host(x, y)
+        if len(orig_shape) > 2:
+            return y.reshape(*orig_shape[:-1], self.out_features)
+        return y
+
+    __call__ = forward
+
+    def _converted(self, a: np.ndarray, np_dt) -> np.ndarray:
+        """Cached dtype conversion of a parameter array (keyed on the source object)."""
+        cache = self.__dict__.setdefault("_conv_cache", {})
+        key = id(a)
+        hit = cache.get(key)
+        if hit is not None and hit[0] is a and hit[1] == a.ctypes.data and (
+                a.nbytes > (4 << 20) or np.array_equal(hit[2], a)):
+            return hit[3]
+        conv = np.ascontiguousarray(a, dtype=np_dt)
+        cache[key] = (a, a.ctypes.data, a.copy() if a.nbytes <= (4 << 20) else None, conv)
+        return conv
+
+    def backward(self, *args, **kwargs):
+        raise NotImplementedError("training (backward) is outside this build's forward-only scope")

@@ -1,0 +1,100 @@
+"""GatedKAN: SwiGLU-style block of three Chebyshev KAN layers.
+
+Drop-in for the reference ``metal_kans/gated_kan.py`` forward surface:
+constructor (gated_kan.py:36-84: gate, up, down ChebyKAN built in that order,
+``.half()`` when dtype is float16), ``forward`` (:86-138: gate = Gate(x),
+up = Up(x), hidden = SiLU(gate) * up with the +-20 clip, out = Down(hidden),
+(B, S, d) inputs flattened), ``to_int8`` / ``to_int4`` / ``to_ternary``
+(:239-258), ``parameter_count``.  SwiGLU runs on the GPU for every dtype.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from . import device
+from .cheby_kan import ChebyKAN
+from .quantization import to_int4, to_int8, to_ternary
+
+
+class GatedKAN:
+    """out = Down(SiLU(Gate(x)) * Up(x)) with Chebyshev KAN projections."""
+
+    def __init__(self, d_model: int, d_ffn: Optional[int] = None, degree: int = 4, has_base: bool = True,
+                 has_bias: bool = False, dtype: np.dtype = np.float32):
+        self.d_model = int(d_model)
+        self.d_ffn = int(d_ffn if d_ffn is not None else 2 * d_model)
+        self.degree = int(degree)
+        self.has_base = bool(has_base)
+        self.has_bias = bool(has_bias)
+        self.dtype = np.dtype(dtype)
+        self.gate_kan = ChebyKAN(self.d_model, self.d_ffn, degree=self.degree, bias=self.has_bias,
+                                 use_base=self.has_base)
+        self.up_kan = ChebyKAN(self.d_model, self.d_ffn, degree=self.degree, bias=self.has_bias,
+                               use_base=self.has_base)
+        self.down_kan = ChebyKAN(self.d_ffn, self.d_model, degree=self.degree, bias=self.has_bias,
+                                 use_base=self.has_base)
+        if self.dtype == np.float16:
+            self.gate_kan.half()
+            self.up_kan.half()
+            self.down_kan.half()
+        self._saved_x = None
+        self._saved_gate = None
+        self._saved_up = None
+        self._saved_hidden = None
+
+    def _swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        u = np.ascontiguousarray(up, dtype=np.float32)
+        out = np.empty_like(g)
+        device.check(device.get_metal_bridge().metal_kan_swiglu_forward(g.ctypes.data, u.ctypes.data,
+                                                                       out.ctypes.data, g.size),
+                     "metal_kan_swiglu_forward")
+        return out.astype(gate.dtype, copy=False)
+
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
+        self._saved_x = x_2d
+        gate = self.gate_kan(x_2d)
+        up = self.up_kan(x_2d)
+        self._saved_gate = gate
+        self._saved_up = up
+        hidden = self._swiglu(gate, up)
+        self._saved_hidden = hidden
+        out = self.down_kan(hidden)
+        if len(orig_shape) > 2:
+            return out.reshape(*orig_shape[:-1], self.d_model)
+        return out
+
+    __call__ = forward
+
+    def to_int8(self, group_size: int = 64) -> "GatedKAN":
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            to_int8(kan, group_size=group_size)
+        return self
+
+    def to_int4(self, group_size: int = 64) -> "GatedKAN":
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            to_int4(kan, group_size=group_size)
+        return self
+
+    def to_ternary(self, group_size: int = 32) -> "GatedKAN":
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            to_ternary(kan, group_size=group_size)
+        return self
+
+    def parameter_count(self) -> int:
+        count = 0
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            count += kan.w_cheby.size
+            if kan.has_base and kan.w_base is not None:
+                count += kan.w_base.size
+            if kan.has_bias and kan.bias is not None:
+                count += kan.bias.size
+        return count
+
+    def __repr__(self) -> str:
+        return (f"GatedKAN(d_model={self.d_model}, d_ffn={self.d_ffn}, degree={self.degree}, "
+                f"has_base={self.has_base}, params={self.parameter_count():,})")

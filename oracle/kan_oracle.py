@@ -1,0 +1,353 @@
+"""CPU oracle for the fused KAN layer forward -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The shipped path (``metal-kans_amd/metal_kans`` + the HIP library)
+must not import, call or fall back to anything here.
+
+It restates, in NumPy, what the reference computes on the hot path:
+
+* basis evaluators          -- ``metal_kans/kernels/fused_kan.metal:13-16,116-166,205-276``
+                               and the fp16 variants ``:1373-1450,1476-1512``
+* four-stage forward order  -- ``metal_kans/kernels/metal_kan_bridge.mm:443-625,1069-1164``
+                               (SiLU+bias, SiLU(x)@W_base^T, Phi, Phi@W^T)
+* layer parameters          -- ``metal_kans/cheby_kan.py:38-42``, ``fast_kan.py:40-47``,
+                               ``bspline_kan.py:40-54``
+* INT8/INT4 quantizer       -- NumPy fallback ``metal_kans/quantization.py:24-35,73-99``
+* INT8/INT4 dequantizer     -- NumPy fallback ``quantization.py:136-148``
+* ternary (de)quantizer     -- NumPy fallback ``quantization.py:196-246,275-286``
+* GatedKAN block            -- ``metal_kans/gated_kan.py:15-16,86-138``
+* SwiGLU kernel             -- ``fused_kan.metal:2284-2296``
+
+Two accumulation modes exist for the forward: ``acc=np.float64`` (the
+correctness reference: float64 arithmetic on the original inputs) and
+``acc=np.float32`` (the reference's own four fp32 stages, used as the timed CPU
+baseline).
+
+Pinning (what checks each function, beyond retyping it) lives in
+``tests/test_oracle.py``: Chebyshev against cos(k*theta) and T_k(+-1),
+B-spline against partition of unity / knot values / a textbook Cox-de Boor
+recursion on the extended uniform knot vector, RBF against phi(c_k)=1 and the
+cfg3 constant inv_den=49/32, the contraction against brute-force loops and the
+K=1 / W=0 reductions, and the quantizers bit-for-bit against golden vectors
+written by the reference's own NumPy fallback (``tests/golden/``).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+LOG2E = 1.4426950408889634
+
+
+# ----------------------------------------------------------------------------
+# Basis evaluators.  All return Phi with shape (B, D_in, K) in ``dtype``.
+# ----------------------------------------------------------------------------
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """x / (1 + e^-x) on the raw (unclamped) input (fused_kan.metal:13-16,132-133)."""
+    return x / (1.0 + np.exp(-x))
+
+
+def cheby_basis(x: np.ndarray, K: int, dtype=np.float64) -> np.ndarray:
+    """T_0..T_{K-1}(clamp(x,-1,1)) by the 3-term recurrence (fused_kan.metal:205-238).
+
+    ``K`` is the number of coefficients (the reference's ``degree`` argument,
+    cheby_kan.py:40).
+    """
+    t = np.clip(np.asarray(x, dtype=dtype), -1.0, 1.0)
+    out = np.empty(t.shape + (K,), dtype=dtype)
+    out[..., 0] = 1.0
+    if K > 1:
+        out[..., 1] = t
+    for k in range(2, K):
+        out[..., k] = 2.0 * t * out[..., k - 1] - out[..., k - 2]
+    return out
+
+
+def rbf_grid(grid_range: Tuple[float, float], num_centers: int):
+    """Centres and 1/(2h^2) exactly as FastKAN.__init__ builds them (fast_kan.py:40-42)."""
+    grid = np.linspace(grid_range[0], grid_range[1], num_centers, dtype=np.float32)
+    h = (grid_range[1] - grid_range[0]) / (num_centers - 1)
+    inv_den = float(1.0 / (2.0 * (h ** 2)))
+    return grid, inv_den
+
+
+def rbf_basis(x: np.ndarray, grid: np.ndarray, inv_den: float, dtype=np.float64) -> np.ndarray:
+    """exp(-(x - c_k)^2 * inv_den) (fused_kan.metal:140-166)."""
+    xv = np.asarray(x, dtype=dtype)[..., None]
+    c = np.asarray(grid, dtype=dtype)
+    d = xv - c
+    return np.exp(-(d * d) * dtype(inv_den)).astype(dtype)
+
+
+def bspline_params(grid_size: int, grid_range: Sequence[float] = (-1.0, 1.0)):
+    """[grid_min, inv_h] in fp32 as BSplineKAN.__init__ stores them (bspline_kan.py:44-49)."""
+    gmin = float(grid_range[0])
+    gmax = float(grid_range[1])
+    inv_h = float(grid_size) / (gmax - gmin)
+    return np.array([gmin, inv_h], dtype=np.float32)
+
+
+def bspline_basis(x: np.ndarray, grid_size: int, grid_min: float, inv_h: float,
+                  dtype=np.float64) -> np.ndarray:
+    """Clamped closed-form uniform cubic B-spline, G+3 bases (fused_kan.metal:240-276).
+
+    span = clamp(floor(pos), 0, G-1), u = clamp(pos - span, 0, 1); the four
+    non-zero values sit at span..span+3, everything else is 0.  Outside the grid
+    the reference saturates (it does not extrapolate).
+    """
+    xv = np.asarray(x, dtype=dtype)
+    nb = grid_size + 3
+    pos = (xv - dtype(grid_min)) * dtype(inv_h)
+    span = np.clip(np.floor(pos), 0, grid_size - 1).astype(np.int64)
+    u = np.clip(pos - span, 0.0, 1.0)
+    om = 1.0 - u
+    b0 = om * om * om / 6.0
+    b1 = (3.0 * u ** 3 - 6.0 * u ** 2 + 4.0) / 6.0
+    b2 = (-3.0 * u ** 3 + 3.0 * u ** 2 + 3.0 * u + 1.0) / 6.0
+    b3 = u ** 3 / 6.0
+    out = np.zeros(xv.shape + (nb,), dtype=dtype)
+    idx = np.indices(xv.shape)
+    for j, bj in enumerate((b0, b1, b2, b3)):
+        out[tuple(idx) + (span + j,)] = bj
+    return out
+
+
+def basis(kind: str, x: np.ndarray, params: dict, dtype=np.float64) -> np.ndarray:
+    if kind == "cheby":
+        return cheby_basis(x, params["K"], dtype)
+    if kind == "rbf":
+        return rbf_basis(x, params["grid"], params["inv_den"], dtype)
+    if kind == "bspline":
+        return bspline_basis(x, params["G"], params["grid_min"], params["inv_h"], dtype)
+    raise ValueError(kind)
+
+
+# ----------------------------------------------------------------------------
+# Forward.
+# ----------------------------------------------------------------------------
+
+def round_to(a: np.ndarray, kind: Optional[str]) -> np.ndarray:
+    """Round values to fp16 / bf16 (RNE) and return them widened back; None = unchanged."""
+    if kind is None:
+        return a
+    if kind == "float16":
+        return np.asarray(a).astype(np.float16).astype(np.asarray(a).dtype)
+    if kind == "bfloat16":
+        return bf16_to_f32(bf16_round(np.asarray(a, dtype=np.float32))).astype(np.asarray(a).dtype)
+    raise ValueError(kind)
+
+
+def kan_forward(kind: str, x: np.ndarray, W: np.ndarray, W_base: Optional[np.ndarray],
+                bias: Optional[np.ndarray], params: dict, acc=np.float64,
+                operands: Optional[str] = None) -> np.ndarray:
+    """y = bias + SiLU(x) @ W_base^T + Phi(x) @ W^T, in the reference's stage order.
+
+    Follows metal_kan_bridge.mm:472-523: (1) Y = bias (or 0), (2) Y += SiLU(x)
+    W_base^T, (3) Phi = basis(x) laid out [B, D_in*K] k-fastest, (4) Y += Phi W^T.
+    ``W`` has shape (D_out, D_in*K); ``W_base`` (D_out, D_in) or None; ``bias``
+    (D_out,) or None.  ``operands`` ('float16' / 'bfloat16') rounds SiLU(x) and
+    Phi to that type before the contraction, as a 16-bit GEMM stage does (the
+    reference's fp16 path stores Phi in half, fused_kan.metal:1399-1426).
+    """
+    x = np.asarray(x)
+    B, D_in = x.shape
+    Wf = np.asarray(W, dtype=acc)
+    D_out = Wf.shape[0]
+    xa = x.astype(acc)
+    y = np.zeros((B, D_out), dtype=acc)
+    if bias is not None:
+        y += np.asarray(bias, dtype=acc)[None, :]
+    if W_base is not None:
+        y += round_to(silu(xa), operands) @ np.asarray(W_base, dtype=acc).T
+    phi = round_to(basis(kind, xa, params, acc).reshape(B, -1), operands)
+    y += phi @ Wf.T
+    return y
+
+
+def rel_err(y: np.ndarray, y_ref: np.ndarray) -> float:
+    """Norm-wise max|y - y_ref| / max|y_ref| (the parity metric)."""
+    y = np.asarray(y, dtype=np.float64)
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    den = float(np.max(np.abs(y_ref)))
+    num = float(np.max(np.abs(y - y_ref)))
+    return num / den if den > 0 else num
+
+
+def chain_forward(layers: Sequence[dict], x: np.ndarray, acc=np.float64,
+                  operands: Optional[str] = None) -> np.ndarray:
+    """Sequential layers (metal_kan.py:133-135; chain at metal_kan_bridge.mm:1168-1248)."""
+    h = np.asarray(x, dtype=acc)
+    for L in layers:
+        h = kan_forward(L["kind"], h, L["W"], L.get("W_base"), L.get("bias"), L["params"], acc, operands)
+    return h
+
+
+def silu_clipped(x: np.ndarray) -> np.ndarray:
+    """GatedKAN's SiLU with the +-20 clip in the exponent (gated_kan.py:15-16, fused_kan.metal:2284-2296)."""
+    return x / (1.0 + np.exp(-np.clip(x, -20.0, 20.0)))
+
+
+def gated_forward(x: np.ndarray, gate: dict, up: dict, down: dict, acc=np.float64) -> np.ndarray:
+    """out = Down(SiLU(Gate(x)) * Up(x)) (gated_kan.py:86-138); dicts hold W, W_base, bias, K."""
+    def f(L, h):
+        return kan_forward("cheby", h, L["W"], L.get("W_base"), L.get("bias"), {"K": L["K"]}, acc)
+    g = f(gate, x)
+    u = f(up, x)
+    hidden = silu_clipped(g) * u
+    return f(down, hidden)
+
+
+# ----------------------------------------------------------------------------
+# Quantizers / dequantizers (NumPy-fallback semantics of quantization.py).
+# ----------------------------------------------------------------------------
+
+def quantize_affine(weight: np.ndarray, bits: int, group_size: int):
+    """Block-affine min/max quantizer: returns (qweight, scales, biases, padded_in).
+
+    quantization.py:24-35 (zero padding of the input dim to a multiple of the
+    group), :74-99 (min/max, range floor 1e-7, scale = range / (2^bits - 1),
+    q = round-half-even((w - min) / scale) clipped, INT4: even index -> low nibble).
+    All arithmetic in fp32, as NumPy does on fp32 arrays.
+    """
+    w = np.asarray(weight)
+    out_f, in_f = w.shape
+    pad_in = (group_size - (in_f % group_size)) % group_size
+    if pad_in > 0:
+        padded = np.pad(w, ((0, 0), (0, pad_in)), mode="constant", constant_values=0.0)
+    else:
+        padded = w.copy()
+    padded = np.ascontiguousarray(padded, dtype=np.float32)
+    grouped = padded.reshape(-1, group_size)
+    min_vals = grouped.min(axis=1, keepdims=True)
+    max_vals = grouped.max(axis=1, keepdims=True)
+    range_vals = np.maximum(max_vals - min_vals, np.float32(1e-7))
+    max_int = (1 << bits) - 1
+    scales = range_vals / np.float32(max_int)
+    biases = min_vals
+    q = np.round((grouped - biases) / scales).astype(np.int32)
+    q = np.clip(q, 0, max_int)
+    scales = scales.astype(np.float32)
+    biases = biases.astype(np.float32)
+    if bits == 8:
+        qweight = q.astype(np.uint8)
+    elif bits == 4:
+        qweight = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    else:
+        raise ValueError(bits)
+    return qweight, scales, biases, padded.shape[1]
+
+
+def dequantize_affine(qweight: np.ndarray, scales: np.ndarray, biases: np.ndarray, bits: int,
+                      group_size: int, shape: Tuple[int, int], padded_in: int) -> np.ndarray:
+    """q * scale + bias with two separate fp32 roundings (quantization.py:136-148)."""
+    if bits == 8:
+        q = qweight.astype(np.float32)
+    else:
+        q = np.empty((qweight.shape[0], group_size), dtype=np.float32)
+        q[:, 0::2] = (qweight & 0x0F).astype(np.float32)
+        q[:, 1::2] = ((qweight >> 4) & 0x0F).astype(np.float32)
+    restored = (q * scales + biases).reshape(-1, padded_in)
+    return restored[: shape[0], : shape[1]].astype(np.float32)
+
+
+def quantize_ternary(weight: np.ndarray, group_size: int = 32):
+    """Absmean ternary quantizer: returns (w_packed uint32 (D_out, ceil(K/16)), scales (D_out, ceil(K/g))).
+
+    quantization.py:196-246: per (row, group) sc = float32 mean(|w|) (1e-4 if the
+    mean is 0), codes 0 (w/sc < -0.5), 2 (> 0.5) else 1, 16 codes per uint32 at bit
+    2*(k % 16).  Vectorised; per-group means are bitwise identical to the
+    reference's per-slice np.mean (checked in tests/test_oracle.py).
+    """
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    D_out, K_dim = w.shape
+    words = (K_dim + 15) // 16
+    gpr = (K_dim + group_size - 1) // group_size
+    scales = np.zeros((D_out, gpr), dtype=np.float32)
+    codes = np.empty((D_out, K_dim), dtype=np.uint32)
+    nfull = K_dim // group_size
+    absw = np.abs(w)
+
+    def group_scale(mean32):
+        sc = mean32.astype(np.float32)
+        return np.where(sc > 0, sc, np.float32(1e-4)).astype(np.float32)
+
+    if nfull > 0:
+        blk = w[:, : nfull * group_size].reshape(D_out, nfull, group_size)
+        m = np.mean(absw[:, : nfull * group_size].reshape(D_out * nfull, group_size), axis=1)
+        sc = group_scale(m).reshape(D_out, nfull)
+        scales[:, :nfull] = sc
+        norm = blk / sc[:, :, None]
+        codes[:, : nfull * group_size] = np.where(norm < -0.5, 0, np.where(norm > 0.5, 2, 1)).reshape(
+            D_out, nfull * group_size)
+    if K_dim % group_size:
+        start = nfull * group_size
+        tail = np.ascontiguousarray(absw[:, start:])
+        m = np.mean(tail, axis=1)
+        sc = group_scale(m)
+        scales[:, nfull] = sc
+        norm = w[:, start:] / sc[:, None]
+        codes[:, start:] = np.where(norm < -0.5, 0, np.where(norm > 0.5, 2, 1))
+    pad = words * 16 - K_dim
+    if pad:
+        codes = np.pad(codes, ((0, 0), (0, pad)), constant_values=0)
+    c = codes.reshape(D_out, words, 16)
+    shifts = (np.arange(16, dtype=np.uint32) * 2)[None, None, :]
+    packed = np.bitwise_or.reduce(c << shifts, axis=2).astype(np.uint32)
+    return packed, scales
+
+
+def ternary_codes(w_packed: np.ndarray, K_dim: int) -> np.ndarray:
+    """Unpack 2-bit codes, code k at bits 2*(k%16) of word k//16 (quantization.py:279-281)."""
+    D_out, words = w_packed.shape
+    shifts = (np.arange(16, dtype=np.uint32) * 2)[None, None, :]
+    c = (w_packed[:, :, None] >> shifts) & np.uint32(3)
+    return c.reshape(D_out, words * 16)[:, :K_dim]
+
+
+def dequantize_ternary(w_packed: np.ndarray, scales: np.ndarray, shape: Tuple[int, int],
+                       group_size: int = 32) -> np.ndarray:
+    """{0:-1, 1:0, 2:+1, 3:0}[code] * scale in fp32 (quantization.py:275-286)."""
+    D_out, K_dim = shape
+    c = ternary_codes(w_packed, K_dim)
+    val = np.where(c < 3, c.astype(np.float32) - np.float32(1.0), np.float32(0.0)).astype(np.float32)
+    g = np.arange(K_dim) // group_size
+    return (val * scales[:, g]).astype(np.float32)
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """(g * sigmoid(clamp(g, +-20))) * u in fp32 (fused_kan.metal:2284-2296)."""
+    g = np.asarray(gate, dtype=np.float32)
+    u = np.asarray(up, dtype=np.float32)
+    sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-np.clip(g, -20.0, 20.0)))
+    return ((g * sig) * u).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------
+# Synthetic workloads named in BASELINE.json (seeded: rng = default_rng(1000+cfg),
+# draw order x, W, W_base, bias).
+# ----------------------------------------------------------------------------
+
+def layer_norm(x: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """Non-affine LayerNorm over the feature axis in fp32 (cfg3 input conditioning)."""
+    x = np.asarray(x, dtype=np.float32)
+    mu = x.mean(axis=-1, keepdims=True)
+    var = x.var(axis=-1, keepdims=True)
+    return ((x - mu) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit pattern (uint16) with round-to-nearest-even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rounding = ((u >> 16) & 1) + np.uint32(0x7FFF)
+    out = ((u + rounding) >> 16).astype(np.uint16)
+    nan = np.isnan(np.ascontiguousarray(x, dtype=np.float32))
+    out[nan] = 0x7FC0
+    return out
+
+
+def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (np.asarray(u16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)

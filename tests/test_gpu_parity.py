@@ -1,0 +1,434 @@
+"""GPU parity of the fused HIP path against the CPU oracle (run on an MI355X).
+
+Metric: max|y - y_ref| / max|y_ref| with y_ref the float64 oracle on the
+original fp32 inputs and weights (the reference's fp16 test compares against
+its fp32 path the same way, tests/test_metal_kans.py:257-308).
+Tolerances: fp32 <= 1e-4, fp16 / bf16 <= 2e-2.
+Dequantization: bit-exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kan_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"float32": 1e-4, "float16": 2e-2, "bfloat16": 2e-2}
+
+
+def make_layer(mk, kind, d_in, d_out, K, bias=True, base=True, seed=0, grid_range=(-1.0, 1.0)):
+    np.random.seed(seed)
+    if kind == "cheby":
+        L = mk.ChebyKAN(d_in, d_out, degree=K, bias=bias, use_base=base)
+    elif kind == "rbf":
+        L = mk.FastKAN(d_in, d_out, num_centers=K, grid_range=grid_range, bias=bias, use_base=base)
+    else:
+        L = mk.BSplineKAN(d_in, d_out, grid_size=K - 3, grid_range=grid_range, bias=bias, use_base=base)
+    if bias:
+        L.bias = np.random.normal(0, 0.1, d_out).astype(np.float32)
+    return L
+
+
+def oracle_of(L, x):
+    kind = L._basis
+    W = getattr(L, L._weight_attr).astype(np.float64)
+    Wb = L.w_base.astype(np.float64) if L.has_base else None
+    bias = L.bias.astype(np.float64) if L.has_bias else None
+    if kind == "cheby":
+        p = {"K": L.degree}
+    elif kind == "rbf":
+        p = {"grid": np.asarray(L.grid, np.float64), "inv_den": L.inv_denominator}
+    else:
+        p = {"G": L.grid_size, "grid_min": float(L.grid_params[0]), "inv_h": float(L.grid_params[1])}
+    return O.kan_forward(kind, x.astype(np.float64), W, Wb, bias, p)
+
+
+def cast(L, dtype):
+    if dtype == "float16":
+        L.half()
+    elif dtype == "bfloat16":
+        L.bfloat16()
+    return L
+
+
+SHAPES = [
+    (1, 3, 5),        # single row, D_in not a multiple of 8
+    (37, 24, 70),     # ragged rows / columns, D_in % 16 == 8
+    (256, 64, 64),    # config 1 shape
+    (300, 130, 200),  # several feature blocks, ragged everything
+]
+KINDS = [("cheby", 9), ("cheby", 4), ("rbf", 8), ("bspline", 8)]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("kind,K", KINDS)
+@pytest.mark.parametrize("B,d_in,d_out", SHAPES)
+def test_layer_parity(gpu, dtype, kind, K, B, d_in, d_out):
+    import metal_kans as mk
+    print(f"case {kind} K={K} {dtype} B={B} {d_in}->{d_out}", flush=True)
+    L = make_layer(mk, kind, d_in, d_out, K, seed=B + d_in, grid_range=(-1.5, 1.5) if kind == "rbf" else (-1, 1))
+    rng = np.random.default_rng(B * 7 + d_out)
+    x = rng.uniform(-1.2, 1.2, (B, d_in)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    y = cast(L, dtype)(x)
+    assert y.shape == (B, d_out)
+    assert np.isfinite(y).all()
+    assert O.rel_err(y, y_ref) <= TOL[dtype], O.rel_err(y, y_ref)
+
+
+@pytest.mark.parametrize("base,bias", [(False, False), (False, True), (True, False)])
+@pytest.mark.parametrize("kind,K", [("cheby", 5), ("rbf", 6), ("bspline", 7)])
+def test_branch_flags(gpu, kind, K, base, bias):
+    import metal_kans as mk
+    L = make_layer(mk, kind, 40, 33, K, bias=bias, base=base, seed=3)
+    x = np.random.default_rng(1).uniform(-1.1, 1.1, (65, 40)).astype(np.float32)
+    assert O.rel_err(L(x), oracle_of(L, x)) <= 1e-4
+
+
+@pytest.mark.parametrize("wm,nb,splits", [(64, 4, 1), (32, 4, 1), (32, 1, 1), (64, 4, 3), (32, 4, 5)])
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_tilings_and_splits(gpu, wm, nb, splits, dtype):
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 200, 150, 6, seed=11)
+    L.set_tiling(wm, nb, splits)
+    x = np.random.default_rng(2).uniform(-1, 1, (333, 200)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    assert O.rel_err(cast(L, dtype)(x), y_ref) <= TOL[dtype]
+
+
+def test_rbf_arbitrary_centres(gpu):
+    import metal_kans as mk
+    L = make_layer(mk, "rbf", 48, 40, 5, seed=4)
+    L.grid = np.array([-1.7, -0.2, 0.0, 0.9, 2.4], np.float32)   # non-uniform centres
+    x = np.random.default_rng(3).normal(0, 1, (90, 48)).astype(np.float32)
+    assert O.rel_err(L(x), oracle_of(L, x)) <= 1e-4
+
+
+def test_inputs_outside_grid_and_extremes(gpu):
+    import metal_kans as mk
+    x = np.random.default_rng(8).uniform(-6, 6, (64, 32)).astype(np.float32)
+    x[0, :8] = [0.0, 1.0, -1.0, 1e4, -1e4, 1.0000001, -0.99999, 5.0]
+    for kind, K in (("cheby", 9), ("bspline", 8), ("rbf", 8)):
+        L = make_layer(mk, kind, 32, 48, K, seed=5)
+        y = L(x)
+        assert np.isfinite(y).all()
+        assert O.rel_err(y, oracle_of(L, x)) <= 1e-4, kind
+
+
+def test_multi_dim_input_and_dtype_cast(gpu):
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 16, 8, 4)
+    x = np.random.default_rng(0).uniform(-1, 1, (2, 5, 16))
+    y = L(x)                      # float64 input is cast to float32 as in the reference
+    assert y.shape == (2, 5, 8) and y.dtype == np.float32
+    assert O.rel_err(y.reshape(10, 8), oracle_of(L, x.reshape(10, 16).astype(np.float32))) <= 1e-4
+    with pytest.raises(ValueError):
+        L(np.zeros((3, 15), np.float32))
+
+
+def test_in_place_weight_edit_is_seen(gpu):
+    """The reference's finite-difference tests edit weights in place (test_training.py:59-67)."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 3, 2, 4)
+    x = np.random.default_rng(0).uniform(-0.8, 0.8, (4, 3)).astype(np.float32)
+    y0 = L(x).copy()
+    L.w_cheby[1, 5] += 1e-2
+    y1 = L(x)
+    assert O.rel_err(y1, oracle_of(L, x)) <= 1e-4
+    assert not np.array_equal(y0, y1)
+
+
+# ---------------------------------------------------------------- reference tests, on this build
+def test_reference_fp16_vs_fp32(gpu):
+    """tests/test_metal_kans.py:257-308: fp16 output within atol 1e-2 of fp32."""
+    import metal_kans as mk
+    np.random.seed(42)
+    for ctor, xr in ((lambda: mk.ChebyKAN(8, 16, degree=4), 1.0), (lambda: mk.FastKAN(8, 16, num_centers=8), 1.0),
+                     (lambda: mk.BSplineKAN(8, 16, grid_size=5, spline_order=3), 0.9)):
+        layer = ctor()
+        x = np.random.uniform(-xr, xr, (64, 8)).astype(np.float32)
+        y32 = layer(x)
+        layer.half()
+        y16 = layer(x.astype(np.float16))
+        assert y16.dtype == np.float16
+        np.testing.assert_allclose(y16.astype(np.float32), y32, atol=1e-2)
+
+
+def test_reference_fp16_boundary(gpu):
+    """tests/test_optimizations.py:17-26: fp16 Chebyshev at x = +-1, K = 8 stays finite."""
+    import metal_kans as mk
+    layer = mk.ChebyKAN(in_features=8, out_features=4, degree=8).half()
+    X = np.array([[-1.0, -0.999, 0.0, 0.999, 1.0, -0.5, 0.5, 0.0] for _ in range(4)], dtype=np.float16)
+    Y = layer(X)
+    assert Y.shape == (4, 4) and np.isfinite(Y.astype(np.float32)).all()
+
+
+def test_reference_chain_vs_layers(gpu):
+    """tests/test_metal_kans.py:145-160: chained network equals per-layer dispatch (abs < 1e-4)."""
+    import metal_kans as mk
+    np.random.seed(42)
+    net = mk.MetalKAN([4, 16, 8, 2], basis_type="cheby", degree=4, pipeline=True)
+    x = np.random.uniform(-1.0, 1.0, (128, 4)).astype(np.float32)
+    y_chain = net(x)
+    h = x
+    for layer in net.layers:
+        h = layer(h)
+    assert np.max(np.abs(y_chain - h)) < 1e-4
+    ref = O.chain_forward([{"kind": "cheby", "W": l.w_cheby, "W_base": l.w_base, "bias": l.bias,
+                            "params": {"K": 4}} for l in net.layers], x)
+    assert O.rel_err(y_chain, ref) <= 1e-4
+
+
+def test_reference_quantization_error_bounds(gpu):
+    """tests/test_metal_kans.py:163-181."""
+    import metal_kans as mk
+    np.random.seed(42)
+    w = np.random.normal(0.0, 1.0, (32, 64)).astype(np.float32)
+    assert np.max(np.abs(w - mk.QuantizedWeight(w, bits=8, group_size=32).dequantize())) < 0.05
+    assert np.max(np.abs(w - mk.QuantizedWeight(w, bits=4, group_size=32).dequantize())) < 0.35
+    net = mk.MetalKAN([8, 16, 4], basis_type="cheby")
+    mk.to_int8(net)
+    assert net(np.random.uniform(-1, 1, (16, 8)).astype(np.float32)).shape == (16, 4)
+
+
+def test_reference_ternary_cosine(gpu):
+    """tests/test_optimizations.py:104-120."""
+    import metal_kans as mk
+    np.random.seed(42)
+    layer = mk.ChebyKAN(in_features=16, out_features=8, degree=4)
+    x = np.random.uniform(-0.8, 0.8, (4, 16)).astype(np.float32)
+    out32 = layer(x)
+    mk.to_ternary(layer, group_size=32)
+    assert hasattr(layer, "_w_cheby_ternary")
+    out_t = layer(x)
+    cos = np.dot(out32.ravel(), out_t.ravel()) / (np.linalg.norm(out32) * np.linalg.norm(out_t) + 1e-8)
+    assert cos > 0.4
+
+
+def test_reference_async_stream(gpu):
+    """tests/test_metal_kans.py:318-332."""
+    import metal_kans as mk
+    np.random.seed(42)
+    net = mk.MetalKAN([8, 16, 2], basis_type="fastkan", degree=8)
+    batches = [np.random.uniform(-1.0, 1.0, (32, 8)).astype(np.float32) for _ in range(8)]
+    y_sync = [net(b) for b in batches]
+    y_async = net.async_stream(batches)
+    for a, s in zip(y_async, y_sync):
+        np.testing.assert_allclose(a, s, atol=1e-5)
+
+
+# ---------------------------------------------------------------- quantization on device
+@pytest.mark.parametrize("bits", [8, 4])
+def test_dequant_affine_bit_exact(gpu, bits):
+    import metal_kans as mk
+    w = np.random.default_rng(bits).normal(0, 0.02, (70, 300)).astype(np.float32)
+    qw = mk.QuantizedWeight(w, bits=bits, group_size=64)
+    dq = qw.dequantize()
+    ref = O.dequantize_affine(qw.qweight, qw.scales, qw.biases, bits, 64, w.shape, qw.padded_in_features)
+    np.testing.assert_array_equal(dq.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_ternary_bit_exact(gpu):
+    import metal_kans as mk
+    w = np.random.default_rng(3).normal(0, 0.02, (50, 1000)).astype(np.float32)
+    tq = mk.TernaryQuantizedWeight(w, group_size=32)
+    ref = O.dequantize_ternary(tq.w_packed, tq.scales, w.shape, 32)
+    np.testing.assert_array_equal(tq.dequantize().view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_golden_bit_exact(gpu, request):
+    import os
+    from metal_kans import device
+    lib = device.get_metal_bridge()
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz"))
+    for n in sorted({k.split("__")[0] for k in g.files}):
+        for bits, gs in ((8, 64), (4, 32)):
+            t = f"{n}__int{bits}_g{gs}"
+            q, s, b = g[t + "__q"], g[t + "__s"], g[t + "__b"]
+            out = np.empty(s.shape[0] * gs, np.float32)
+            fn = lib.metal_kan_dequantize_int8 if bits == 8 else lib.metal_kan_dequantize_int4
+            assert fn(q.ctypes.data, s.ctypes.data, b.ctypes.data, out.ctypes.data, s.shape[0], gs) == 0
+            w = g[f"{n}__w"]
+            dq = out.reshape(w.shape[0], -1)[:, : w.shape[1]]
+            np.testing.assert_array_equal(dq.view(np.uint32), g[t + "__dq"].view(np.uint32), err_msg=t)
+        t = f"{n}__tern_g32"
+        p, s = g[t + "__p"], g[t + "__s"]
+        w = g[f"{n}__w"]
+        out = np.empty(w.shape, np.float32)
+        assert lib.metal_kan_dequantize_ternary(p.ctypes.data, s.ctypes.data, out.ctypes.data, w.shape[0],
+                                                w.shape[1], 32) == 0
+        np.testing.assert_array_equal(out.view(np.uint32), g[t + "__dq"].view(np.uint32), err_msg=t)
+
+
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+def test_quantized_layer_forward(gpu, quant):
+    """Quantized forward = forward(x, dequant(quant(W))) (quantization.py:168-171)."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 64, 48, 4, seed=9)
+    getattr(mk, f"to_{quant}")(L)
+    assert L.w_cheby.dtype == np.float32
+    x = np.random.default_rng(4).uniform(-1, 1, (40, 64)).astype(np.float32)
+    assert O.rel_err(L(x), oracle_of(L, x)) <= 1e-4
+
+
+def test_swiglu(gpu):
+    from metal_kans import device
+    lib = device.get_metal_bridge()
+    rng = np.random.default_rng(0)
+    g = rng.normal(0, 8, 1000).astype(np.float32)
+    u = rng.normal(0, 1, 1000).astype(np.float32)
+    out = np.empty_like(g)
+    assert lib.metal_kan_swiglu_forward(g.ctypes.data, u.ctypes.data, out.ctypes.data, g.size) == 0
+    np.testing.assert_allclose(out, O.swiglu(g, u), rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_gated_kan(gpu, dtype):
+    import metal_kans as mk
+    np.random.seed(1)
+    blk = mk.GatedKAN(d_model=32, d_ffn=64, degree=4, dtype=np.float16 if dtype == "float16" else np.float32)
+    x = np.random.uniform(-0.8, 0.8, (6, 32)).astype(np.float32)
+    ref = O.gated_forward(x, *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                               for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    out = blk(x)
+    assert out.shape == (6, 32)
+    assert O.rel_err(out, ref) <= TOL[dtype]
+    out3 = blk(x.reshape(2, 3, 32))
+    assert out3.shape == (2, 3, 32)
+
+
+# ---------------------------------------------------------------- reference-named C-ABI entry points
+def test_reference_named_entry_points(gpu):
+    lib = gpu
+    rng = np.random.default_rng(6)
+    B, Di, Do = 50, 20, 30
+    x = rng.uniform(-1.1, 1.1, (B, Di)).astype(np.float32)
+    Wb = rng.normal(0, 0.2, (Do, Di)).astype(np.float32)
+    bias = rng.normal(0, 0.1, Do).astype(np.float32)
+    y = np.empty((B, Do), np.float32)
+    # Chebyshev fp32 / fp16
+    W = rng.normal(0, 0.1, (Do, Di * 5)).astype(np.float32)
+    assert lib.metal_kan_cheby_forward(x.ctypes.data, W.ctypes.data, Wb.ctypes.data, bias.ctypes.data,
+                                       y.ctypes.data, B, Di, Do, 5, 1, 1) == 0
+    ref = O.kan_forward("cheby", x, W, Wb, bias, {"K": 5})
+    assert O.rel_err(y, ref) <= 1e-4
+    h = [a.astype(np.float16) for a in (x, W, Wb, bias)]
+    y16 = np.empty((B, Do), np.float16)
+    assert lib.metal_kan_cheby_forward_fp16(h[0].ctypes.data, h[1].ctypes.data, h[2].ctypes.data, h[3].ctypes.data,
+                                            y16.ctypes.data, B, Di, Do, 5, 1, 1) == 0
+    assert O.rel_err(y16, ref) <= 2e-2
+    # FastKAN fp32
+    grid, inv = O.rbf_grid((-1.0, 1.0), 6)
+    W6 = rng.normal(0, 0.1, (Do, Di * 6)).astype(np.float32)
+    assert lib.metal_kan_fastkan_forward(x.ctypes.data, W6.ctypes.data, Wb.ctypes.data, grid.ctypes.data,
+                                         bias.ctypes.data, y.ctypes.data, B, Di, Do, 6, ctypes.c_float(inv),
+                                         1, 1) == 0
+    assert O.rel_err(y, O.kan_forward("rbf", x, W6, Wb, bias, {"grid": grid, "inv_den": inv})) <= 1e-4
+    # B-spline fp32 (grid = [min, inv_h], read on the host)
+    gp = O.bspline_params(5)
+    W8 = rng.normal(0, 0.1, (Do, Di * 8)).astype(np.float32)
+    assert lib.metal_kan_bspline_forward(x.ctypes.data, W8.ctypes.data, Wb.ctypes.data, gp.ctypes.data,
+                                         bias.ctypes.data, y.ctypes.data, B, Di, Do, 5, 3, 1, 1) == 0
+    assert O.rel_err(y, O.kan_forward("bspline", x, W8, Wb, bias,
+                                      {"G": 5, "grid_min": float(gp[0]), "inv_h": float(gp[1])})) <= 1e-4
+    # in-place edit between calls is honoured (host arrays are read every call)
+    W[0, 0] += 0.5
+    assert lib.metal_kan_cheby_forward(x.ctypes.data, W.ctypes.data, Wb.ctypes.data, bias.ctypes.data,
+                                       y.ctypes.data, B, Di, Do, 5, 1, 1) == 0
+    assert O.rel_err(y, O.kan_forward("cheby", x, W, Wb, bias, {"K": 5})) <= 1e-4
+    ms = lib.benchmark_metal_cheby(x.ctypes.data, W.ctypes.data, Wb.ctypes.data, bias.ctypes.data, y.ctypes.data,
+                                   B, Di, Do, 5, 1, 1, 1, 3)
+    assert ms > 0
+
+
+def test_reference_chain_entry_point(gpu):
+    lib = gpu
+    rng = np.random.default_rng(12)
+    dims = [12, 24, 24, 7]
+    degs = [3, 6, 4]
+    Ws = [rng.normal(0, 0.2, (dims[l + 1], dims[l] * degs[l])).astype(np.float32) for l in range(3)]
+    Wbs = [rng.normal(0, 0.2, (dims[l + 1], dims[l])).astype(np.float32) for l in range(3)]
+    bs = [rng.normal(0, 0.1, dims[l + 1]).astype(np.float32) for l in range(3)]
+    x = rng.uniform(-1, 1, (77, 12)).astype(np.float32)
+    y = np.empty((77, 7), np.float32)
+    P = ctypes.c_void_p * 3
+    rc = lib.metal_kan_chain_pipeline_cheby(x.ctypes.data, y.ctypes.data, 77, 3, (ctypes.c_int * 4)(*dims),
+                                            (ctypes.c_int * 3)(*degs), P(*[w.ctypes.data for w in Ws]),
+                                            P(Wbs[0].ctypes.data, None, Wbs[2].ctypes.data),
+                                            P(None, bs[1].ctypes.data, bs[2].ctypes.data))
+    assert rc == 0
+    layers = [{"kind": "cheby", "W": Ws[0], "W_base": Wbs[0], "bias": None, "params": {"K": 3}},
+              {"kind": "cheby", "W": Ws[1], "W_base": None, "bias": bs[1], "params": {"K": 6}},
+              {"kind": "cheby", "W": Ws[2], "W_base": Wbs[2], "bias": bs[2], "params": {"K": 4}}]
+    assert O.rel_err(y, O.chain_forward(layers, x)) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_metal_kan_chain(gpu, dtype):
+    """Config-2 shape (784 -> 256 -> 256 -> 10, K = 9) on a smaller batch.
+
+    With K = 9 this network amplifies 16-bit rounding (T_k'(+-1) = k^2 at the
+    clamp edge): exact arithmetic on fp16 weights alone is ~1.4% away from the
+    fp32 network, and the MFMA's 16-bit basis operands add more; an fp16 input
+    would cost another ~7%, so the input stays fp32.  Checked: (a) against the
+    oracle on the same (rounded) weights with the BASELINE tolerance, and (b)
+    tightly against the oracle that also rounds the contraction operands to the
+    MFMA type, which is what the kernel computes."""
+    import metal_kans as mk
+    np.random.seed(2)
+    net = mk.MetalKAN([784, 256, 256, 10], basis_type="cheby", degree=9)
+    x = np.random.default_rng(1).uniform(0, 1, (512, 784)).astype(np.float32)
+    if dtype == "float16":
+        net.half()
+    elif dtype == "bfloat16":
+        net.bfloat16()
+    ref = O.chain_forward([{"kind": "cheby", "W": l.w_cheby, "W_base": l.w_base, "bias": l.bias,
+                            "params": {"K": 9}} for l in net.layers], x)
+    y1 = net(x)
+    y2 = net(x)   # graph replay
+    np.testing.assert_array_equal(np.asarray(y1), np.asarray(y2))
+    ops = None if dtype == "float32" else dtype
+    ref_ops = O.chain_forward([{"kind": "cheby", "W": l.w_cheby, "W_base": l.w_base, "bias": l.bias,
+                                "params": {"K": 9}} for l in net.layers], x, operands=ops)
+    e_same, e_ops = O.rel_err(y1, ref), O.rel_err(y1, ref_ops)
+    print(f"chain {dtype}: rel err vs same weights {e_same:.2e}, vs operand-rounded oracle {e_ops:.2e}")
+    assert e_ops <= (1e-4 if dtype == "float32" else 5e-3)
+    if dtype != "bfloat16":  # bf16's 8-bit mantissa: ~6% here, inherent to bf16 operands at K = 9
+        assert e_same <= TOL[dtype]
+
+
+def test_fp16_layer_input_semantics(gpu):
+    """fp16 input: used as given (the reference casts x to the weight dtype);
+    fp32 input to an fp16 layer: read unrounded by the kernel."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 64, 32, 9, seed=13)
+    x = np.random.default_rng(5).uniform(0.9, 1.0, (50, 64)).astype(np.float32)  # near the clamp edge
+    L.half()
+    W = {"kind": "cheby", "W": L.w_cheby, "W_base": L.w_base, "bias": L.bias, "params": {"K": 9}}
+    y16 = L(x.astype(np.float16))
+    assert y16.dtype == np.float16
+    assert O.rel_err(y16, O.chain_forward([W], x.astype(np.float16))) <= 2e-2
+    y32in = L(x)
+    assert y32in.dtype == np.float16
+    assert O.rel_err(y32in, O.chain_forward([W], x)) <= 2e-2
+
+
+# ---------------------------------------------------------------- full-size properties
+@pytest.mark.parametrize("kind,K", [("cheby", 9), ("rbf", 8), ("bspline", 8)])
+def test_full_size_sampled_rows(gpu, kind, K):
+    """16384 x 1024 -> 1024 fp16 (north-star shape): rows are independent, so a
+    seeded sample of rows is checked against the float64 oracle; a second run
+    must be bitwise identical."""
+    import metal_kans as mk
+    L = make_layer(mk, kind, 1024, 1024, K, bias=False, seed=21, grid_range=(-2, 2) if kind == "rbf" else (-1, 1))
+    rng = np.random.default_rng(100)
+    x = (rng.normal(0, 1, (16384, 1024)) if kind == "rbf" else rng.uniform(-1.2, 1.2, (16384, 1024))).astype(np.float32)
+    rows = np.sort(rng.choice(16384, 48, replace=False))
+    y_ref = oracle_of(L, x[rows])
+    L.half()
+    y = L(x)
+    y2 = L(x)
+    np.testing.assert_array_equal(y.view(np.uint16), y2.view(np.uint16))
+    assert O.rel_err(y[rows], y_ref) <= 2e-2
