@@ -223,6 +223,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary workloads / CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="only run kans_copy_device over MIB MiB, 5 times (byte-counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only (the fused KAN forward is single-GPU; "
@@ -231,6 +233,14 @@ def main():
     import metal_kans as mk
     lib = mk.get_metal_bridge()
     iters = max(a.steps, 1)
+    if a.calib_copy:
+        nbytes = a.calib_copy << 20
+        src, dst = DevBuf(lib, nbytes), DevBuf(lib, nbytes)
+        for _ in range(5):
+            assert lib.kans_copy_device(dst.p, src.p, nbytes, None) == 0
+        lib.kans_synchronize()
+        print(json.dumps({"calib_copy_bytes_read": nbytes, "calib_copy_bytes_written": nbytes, "dispatches": 5}))
+        return
 
     # ---- headline: config 3 ------------------------------------------------
     def ln_normal(rng, B, d):

@@ -16,6 +16,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 enum Basis { BASIS_CHEBY = 0, BASIS_RBF = 1, BASIS_BSPLINE = 2 };
+// Kernel-only basis id: Gaussian RBF on uniformly spaced centres (see
+// BasisGen<BASIS_RBF_UNIFORM>); the public API never sees it.
+constexpr int BASIS_RBF_UNIFORM = 3;
 enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -29,7 +32,15 @@ struct BasisParams {
   float grid_min;     // B-spline: left end of the grid
   float inv_h;        // B-spline: G / (max - min)
   float neg_l;        // RBF: -inv_den * log2(e)
-  const float* centers;  // RBF centres c_k (device memory, K floats)
+  int have_centers;   // RBF: centres set
+  int rbf_uniform;    // RBF: centres are c_0 + k*h (to 1e-6 relative)
+  float rbf_s;        // RBF: sqrt(-neg_l), so phi_k = exp2(-(s*x - s*c_k)^2)
+  float rbf_sc0;      // RBF: s * c_0
+  float rbf_sh;       // RBF: s * h
+  // RBF centres c_k, by value: the kernels read them with scalar loads from the
+  // argument segment, which do not wait on the vector-memory counter that the
+  // weight / input prefetch uses.
+  float centers[kMaxK];
 };
 
 // ---------------------------------------------------------------------------
@@ -73,40 +84,54 @@ __device__ __forceinline__ float silu_f32(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Basis generators.  A generator holds NV input values of one lane and produces
-// the NV values of basis function k in fp32.  ``begin`` is called once per
-// 16-feature block; then ``pair(k, v0, v1)`` yields functions k and k+1 and
-// ``one(k, v0)`` function k, with k = 0, 2, 4, ... in order within a block.
+// Basis generators.  A generator holds NV input values of one lane.  ``begin``
+// is called once per 16-feature block; then ``one(k, v)`` yields basis
+// function k (k = 0, 1, 2, ... in order within a block) for all NV inputs in
+// fp32, and ``pair(k, v0, v1)`` functions k and k+1 (k even).
 // ---------------------------------------------------------------------------
 template <int BASIS, int NV> struct BasisGen;
 
 // Chebyshev T_k(clamp(x,-1,1)) by the three-term recurrence in fp32 registers
-// (reference: fused_kan.metal:205-238 fp32, :1399-1426 fp16 with fma).  The
-// state (p, q) = (T_k, T_{k+1}) advances two functions per pair() without
-// register rotation.
+// (reference: fused_kan.metal:205-238 fp32, :1399-1426 fp16 with fma).  Two
+// registers r0, r1 hold consecutive T's; a step of parity P emits r_P and
+// advances it by two degrees (r_P <- 2t r_{1-P} - r_P), so consecutive steps
+// alternate registers without any register rotation.  ``begin(.., swap)``
+// places T_0 in r1 instead of r0 when basis 0 is emitted at an odd step.
 template <int NV> struct BasisGen<BASIS_CHEBY, NV> {
-  float tw[NV], p[NV], q[NV];
-  __device__ __forceinline__ void begin(const float* x, const BasisParams&) {
+  float tw[NV], r0[NV], r1[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool swap = false) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       float t = __builtin_fminf(__builtin_fmaxf(x[v], -1.0f), 1.0f);
       tw[v] = t + t;
-      p[v] = 1.0f;
-      q[v] = t;
+      r0[v] = swap ? t : 1.0f;
+      r1[v] = swap ? 1.0f : t;
     }
+  }
+  template <int P>
+  __device__ __forceinline__ void step(int, const BasisParams&, float* v0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if constexpr (P == 0) {
+        v0[v] = r0[v];
+        r0[v] = __builtin_fmaf(tw[v], r1[v], -r0[v]);
+      } else {
+        v0[v] = r1[v];
+        r1[v] = __builtin_fmaf(tw[v], r0[v], -r1[v]);
+      }
+    }
+  }
+  __device__ __forceinline__ void one(int k, const BasisParams& bp, float* v0) {
+    if ((k & 1) == 0) step<0>(k, bp, v0); else step<1>(k, bp, v0);
   }
   __device__ __forceinline__ void pair(int, const BasisParams&, float* v0, float* v1) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      v0[v] = p[v];
-      v1[v] = q[v];
-      p[v] = __builtin_fmaf(tw[v], q[v], -p[v]);
-      q[v] = __builtin_fmaf(tw[v], p[v], -q[v]);
+      v0[v] = r0[v];
+      v1[v] = r1[v];
+      r0[v] = __builtin_fmaf(tw[v], r1[v], -r0[v]);
+      r1[v] = __builtin_fmaf(tw[v], r0[v], -r1[v]);
     }
-  }
-  __device__ __forceinline__ void one(int, const BasisParams&, float* v0) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) v0[v] = p[v];
   }
 };
 
@@ -114,7 +139,9 @@ template <int NV> struct BasisGen<BASIS_CHEBY, NV> {
 // (reference: fused_kan.metal:140-166, fast_kan.py:40-42).
 template <int NV> struct BasisGen<BASIS_RBF, NV> {
   float xv[NV];
-  __device__ __forceinline__ void begin(const float* x, const BasisParams&) {
+  template <int P>
+  __device__ __forceinline__ void step(int k, const BasisParams& bp, float* v0) { one(k, bp, v0); }
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool = false) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) xv[v] = x[v];
   }
@@ -132,6 +159,28 @@ template <int NV> struct BasisGen<BASIS_RBF, NV> {
   }
 };
 
+// Gaussian RBF on uniform centres c_k = c_0 + k*h:
+//   phi_k = exp2(-t_k^2),  t_k = s*x - (s*c_0 + k*s*h),  s = sqrt(-neg_l)
+// one fma, one multiply and one exp2 per value, and no per-slot centre load
+// (s*c_k is formed from two kernel arguments).  Same function as the direct
+// form exp2(neg_l * (x - c_k)^2) up to fp32 rounding of t_k.
+template <int NV> struct BasisGen<BASIS_RBF_UNIFORM, NV> {
+  float xv[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool = false) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xv[v] = x[v];
+  }
+  template <int P>
+  __device__ __forceinline__ void step(int k, const BasisParams& bp, float* v0) {
+    const float sck = __builtin_fmaf((float)k, bp.rbf_sh, bp.rbf_sc0);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float t = __builtin_fmaf(xv[v], bp.rbf_s, -sck);
+      v0[v] = __builtin_amdgcn_exp2f(-(t * t));
+    }
+  }
+};
+
 // Clamped uniform cubic B-spline, G+3 bases, four non-zero per input
 // (reference: fused_kan.metal:240-276, bspline_kan.py:40-54):
 //   pos = (x - grid_min) * inv_h, span = clamp(floor(pos), 0, G-1),
@@ -139,7 +188,9 @@ template <int NV> struct BasisGen<BASIS_RBF, NV> {
 template <int NV> struct BasisGen<BASIS_BSPLINE, NV> {
   float w0[NV], w1[NV], w2[NV], w3[NV];
   int span[NV];
-  __device__ __forceinline__ void begin(const float* x, const BasisParams& p) {
+  template <int P>
+  __device__ __forceinline__ void step(int k, const BasisParams& bp, float* v0) { one(k, bp, v0); }
+  __device__ __forceinline__ void begin(const float* x, const BasisParams& p, bool = false) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       float pos = (x[v] - p.grid_min) * p.inv_h;

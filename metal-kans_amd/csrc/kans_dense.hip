@@ -16,12 +16,19 @@
 //     blocks, evaluates the slot's basis value for them in fp32 registers (the
 //     Chebyshev / RBF / B-spline generators advance slot by slot), and packs
 //     them straight into the MFMA A-fragment;
-//   * the B-fragments come from a 3-stage LDS ring filled cooperatively from the
-//     pre-tiled weights (one (fb, s) step of an N-tile is NB contiguous KB);
+//   * the B-fragments come from LDS, filled from the pre-tiled weights (one
+//     (fb, s) step of an N-tile is NB contiguous KB);
 //   * fp16 / bf16 use v_mfma_f32_32x32x16_{f16,bf16}; fp32 uses
 //     v_mfma_f32_32x32x2_f32 eight times per step.  Accumulation is fp32.
 //   * an optional split over feature blocks writes fp32 partials that a finalize
 //     kernel reduces (used when the output tile count alone cannot fill the GPU).
+//
+// Two kernels share this decomposition:
+//   kan_fused_block  fp16/bf16 Chebyshev and uniform-centre RBF with K+base <= 10:
+//                    one barrier per feature block, global->LDS DMA of the next
+//                    block's weights, basis generation interleaved with the MFMAs;
+//   kan_fused_dense  everything else (fp32, B-spline, arbitrary RBF centres,
+//                    larger K): one barrier per slot, register-staged weights.
 #include "kans_common.h"
 #include "kans_api_internal.h"
 #include <algorithm>
@@ -53,6 +60,20 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
   if ((total & 7) != 0) return id;
   int per = total >> 3;
   return (id & 7) * per + (id >> 3);
+}
+
+// Tile of linear index `lin` (after xcd_remap): tiles are visited in groups of
+// GM m-tiles x all n-tiles, m fastest, so the 1/8 of the grid one XCD owns is a
+// GM x (n_tiles/8)-ish block: its workgroups share input rows (x) and weight
+// N-tiles (W') in that XCD's L2.
+__device__ __forceinline__ void tile_of(int lin, int m_tiles, int n_tiles, int& m_tile, int& n_tile) {
+  constexpr int GM = 16;
+  const int group = lin / (GM * n_tiles);
+  const int first_m = group * GM;
+  const int gm = min(GM, m_tiles - first_m);
+  const int in = lin - group * GM * n_tiles;
+  m_tile = first_m + in % gm;
+  n_tile = in / gm;
 }
 
 // Per-lane uint4 chunks of one 32-column block for element type T.
@@ -295,6 +316,252 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 / bf16 kernel with one barrier per feature block.
+//
+// The weights of a whole feature block (KP slots x NB KB for the workgroup's
+// N-tile) sit in one of two LDS stages.  At the start of block fb every wave
+// issues (a) the global -> LDS DMA (global_load_lds_dwordx4, 1 KB per
+// instruction) of block fb+1's weights into the other stage and (b) the load
+// of block fb+1's input rows into registers; both are waited for by the
+// barrier that closes block fb, so their latency hides behind KP slot steps.
+// The two stages are separate __shared__ arrays and the block loop is unrolled
+// by two, so the compiler can tell that the B-fragment reads of the current
+// stage do not depend on the DMA in flight into the other one.
+//
+// Within a block a wave walks the KP slots without synchronisation: the
+// B-fragments of slot s are read from LDS while the basis values of slot s+1
+// are generated into the second A-fragment buffer, then the MFMAs of slot s
+// run.  Slots are unrolled by two so the fragment buffers and the Chebyshev
+// recurrence roles are fixed at compile time.
+//
+// Requires KP = K + has_base <= kBlockSlots (the launcher checks).
+// ---------------------------------------------------------------------------
+constexpr int kBlockSlots = 10;
+
+// VALU instructions of one slot's basis generation per MFMA of that slot
+// (scheduling hint): Chebyshev 1 fma per value, uniform RBF fma + mul + exp2,
+// plus the fp32 -> 16-bit packing.
+template <int BASIS, int NV, int MFMAS>
+constexpr int kValuPerMfma = ((BASIS == BASIS_CHEBY ? 1 : 3) * NV + NV / 2 + MFMAS - 1) / MFMAS;
+
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
+__global__ void __launch_bounds__(kThreads, 2)
+kan_fused_block(const TX* __restrict__ X, long ldx,
+                const uint4* __restrict__ Wt, int nob_pad,
+                const T* __restrict__ bias,
+                TY* __restrict__ Y, long ldy,
+                float* __restrict__ Ypart,
+                int B, int D_in, int D_out, int m_tiles, int n_tiles,
+                int nfb_total, int fb_per_split, int has_base, BasisParams bp) {
+  constexpr int RB = WM / 32;           // 32-row blocks per wave
+  constexpr int NV = RB * 8;            // inputs held per lane
+  constexpr int CPX = Chunks<TX>::CPL;  // uint4 per lane per row block of inputs
+  constexpr int SLOT = NB * 64;         // uint4 per slot of the N-tile
+  typedef typename Mfma<T>::frag frag;
+
+  __shared__ uint4 stage0[kBlockSlots * SLOT];
+  __shared__ uint4 stage1[kBlockSlots * SLOT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  int m_tile, n_tile;
+  tile_of(xcd_remap(blockIdx.x, m_tiles * n_tiles), m_tiles, n_tiles, m_tile, n_tile);
+  const int split = blockIdx.y;
+
+  const int row0 = m_tile * (4 * WM) + wave * WM;
+  const int ob0 = n_tile * NB;
+  const int fb_begin = split * fb_per_split;
+  const int fb_end = min(nfb_total, fb_begin + fb_per_split);
+  const int KP = bp.K + has_base;
+  if (fb_end <= fb_begin) return;  // uniform per workgroup (empty split)
+
+  // ---- weights: global -> LDS DMA ------------------------------------------
+  // Slot s, column block nb of block fb is W'[fb][s][ob0 + nb][lane]: 64 lanes x
+  // 16 B contiguous, one DMA instruction.  Instruction j = s*NB + nb of a block
+  // is issued by wave j % 4 and lands at stage[j * 64 + lane].
+  const uint4* wtile = Wt + (long)ob0 * 64 + lane;
+  auto dma = [&](int fb, uint4* stage) {
+    const uint4* src = wtile + (long)fb * KP * nob_pad * 64;
+    for (int j = wave; j < KP * NB; j += 4) {
+      const int s = j / NB, nb = j - s * NB;
+      __builtin_amdgcn_global_load_lds(src + ((long)s * nob_pad + nb) * 64,
+                                       (__attribute__((address_space(3))) void*)(stage + j * 64), 16, 0, 0);
+    }
+  };
+  auto bread = [&](frag (&b)[NB], const uint4* stage, int s) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      uint4 u = stage[(s * NB + nb) * 64 + lane];
+      b[nb] = *reinterpret_cast<frag*>(&u);
+    }
+  };
+
+  // ---- inputs: lane holds x[row0 + rb*32 + lane%32][fb*16 + 8*(lane/32) + j] --
+  uint4 xr[RB][CPX];
+  auto xload = [&](int fbx) {
+    const int f0 = fbx * 16 + 8 * (lane >> 5);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = row0 + rb * 32 + (lane & 31);
+      const bool ok = (row < B) && (f0 < D_in);
+      const uint4* p = reinterpret_cast<const uint4*>(X + (long)row * ldx + f0);
+#pragma unroll
+      for (int c = 0; c < CPX; ++c) xr[rb][c] = ok ? p[c] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // unpack to fp32; inputs at or beyond D_in read as 0 whatever the padding holds
+  auto xunpack = [&](int fbx, float* xf) {
+    const int f0 = fbx * 16 + 8 * (lane >> 5);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int c = 0; c < CPX; ++c) {
+        const uint4 u = xr[rb][c];
+        if constexpr (sizeof(TX) == 4) {
+          xf[rb * 8 + c * 4 + 0] = __uint_as_float(u.x);
+          xf[rb * 8 + c * 4 + 1] = __uint_as_float(u.y);
+          xf[rb * 8 + c * 4 + 2] = __uint_as_float(u.z);
+          xf[rb * 8 + c * 4 + 3] = __uint_as_float(u.w);
+        } else {
+          const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            TX lo, hi;
+            const unsigned short l16 = (unsigned short)(w[q] & 0xffffu), h16 = (unsigned short)(w[q] >> 16);
+            __builtin_memcpy(&lo, &l16, 2);
+            __builtin_memcpy(&hi, &h16, 2);
+            xf[rb * 8 + 2 * q] = to_f32(lo);
+            xf[rb * 8 + 2 * q + 1] = to_f32(hi);
+          }
+        }
+      }
+    if (f0 + 8 > D_in) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (f0 + (j & 7) >= D_in) xf[j] = 0.0f;
+    }
+  };
+  auto pack = [&](frag (&a)[RB], const float* v) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[rb][j] = from_f32<T>(v[rb * 8 + j]);
+  };
+
+  floatx16 acc[RB][NB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
+
+  // ---- prologue: block fb_begin in stage0 and registers ----------------------
+  dma(fb_begin, stage0);
+  xload(fb_begin);
+  __syncthreads();
+
+  BasisGen<BASIS, NV> gen;
+  frag af[2][RB], bf[NB];
+  // One slot s of parity P, a single basic block: the MFMAs of slot s (on
+  // af[P], bf) are interleaved with the basis values of slot s+1 (into
+  // af[P^1]; the last slot of a block computes one unused extra) and the
+  // B-fragment reads of slot s+1 (clamped to the block).  Each bf[nb] is
+  // re-read as soon as its last MFMA has issued.
+  auto slot = [&](const uint4* cur, int s, auto PP) {
+    constexpr int P = decltype(PP)::value;
+    {
+      float v[NV];
+      gen.template step<P ^ 1>(s + 1 - has_base, bp, v);
+      pack(af[P ^ 1], v);
+    }
+    const int sn = min(s + 1, KP - 1);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = Mfma<T>::mma(af[P][rb], bf[nb], acc[rb][nb]);
+      uint4 u = cur[(sn * NB + nb) * 64 + lane];
+      bf[nb] = *reinterpret_cast<frag*>(&u);
+    }
+    // issue order: per column block, RB MFMAs each followed by a share of the
+    // basis-generation VALU work, then that block's next B-fragment read.
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma<BASIS, NV, RB * NB>, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                     // DS read
+    }
+  };
+  auto block = [&](int fb, const uint4* cur, uint4* nxt) {
+    float xf[NV];
+    xunpack(fb, xf);
+    if (fb + 1 < fb_end) {
+      xload(fb + 1);
+      dma(fb + 1, nxt);
+    }
+    bread(bf, cur, 0);
+    // basis k is emitted at slot k + has_base: basis 0 lands at parity has_base
+    gen.begin(xf, bp, has_base != 0);
+    {
+      float v[NV];
+      if (has_base) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = silu_f32(xf[i]);
+      } else {
+        gen.template step<0>(0, bp, v);
+      }
+      pack(af[0], v);
+    }
+    // slot pairs as one branch-free basic block; an odd last slot is peeled
+    int s = 0;
+    for (; s + 1 < KP; s += 2) {
+      slot(cur, s, std::integral_constant<int, 0>{});
+      slot(cur, s + 1, std::integral_constant<int, 1>{});
+    }
+    if (s < KP) slot(cur, s, std::integral_constant<int, 0>{});
+    __syncthreads();
+  };
+  for (int fb = fb_begin; fb < fb_end; fb += 2) {
+    block(fb, stage0, stage1);
+    if (fb + 1 < fb_end) block(fb + 1, stage1, stage0);
+  }
+
+  // ---- epilogue -------------------------------------------------------------
+  // acc register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  const int rbase = row0 + 4 * (lane >> 5);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = (ob0 + nb) * 32 + (lane & 31);
+    if (col < D_out) {
+      if (Ypart != nullptr) {
+        float* out = Ypart + ((long)split * B + rbase) * D_out + col;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = rb * 32 + 8 * (r >> 2) + (r & 3);
+            if (rbase + dr < B) out[(long)dr * D_out] = acc[rb][nb][r];
+          }
+      } else {
+        const float bcol = bias != nullptr ? to_f32(bias[col]) : 0.0f;
+        TY* out = Y + (long)rbase * ldy + col;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = rb * 32 + 8 * (r >> 2) + (r & 3);
+            if (rbase + dr < B) out[(long)dr * ldy] = from_f32<TY>(acc[rb][nb][r] + bcol);
+          }
+      }
+    }
+  }
+}
+
 // Split reduction: y = sum_split part[split] + bias, converted to T.
 template <typename T, typename TY>
 __global__ void kan_split_finalize(const float* __restrict__ part, int splits, const T* __restrict__ bias,
@@ -363,9 +630,26 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   const int splits = (L.nfb + fbps - 1) / fbps;
   dim3 grid(m_tiles * n_tiles, splits);
   float* part = splits > 1 ? L.part : nullptr;
-  hipLaunchKernelGGL((kan_fused_dense<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
-                     L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
-                     L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+  // fp16 / bf16 Chebyshev layers and RBF layers on uniform centres whose feature
+  // block fits one LDS stage take the block-pipelined kernel; B-spline (whose
+  // generator state does not fit beside the double A-fragment), RBF on
+  // arbitrary centres and fp32 take the per-slot kernel.
+  constexpr bool kBlockable = sizeof(T) == 2 && (BASIS == BASIS_CHEBY || BASIS == BASIS_RBF);
+  bool use_block = false;
+  if constexpr (kBlockable)
+    use_block = L.bp.K + L.has_base <= kBlockSlots && (BASIS == BASIS_CHEBY || L.bp.rbf_uniform != 0);
+  if (use_block) {
+    if constexpr (kBlockable) {
+      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_UNIFORM : BASIS;
+      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
+                         L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
+                         L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+    }
+  } else {
+    hipLaunchKernelGGL((kan_fused_dense<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
+                       L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
+                       L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (splits > 1) {

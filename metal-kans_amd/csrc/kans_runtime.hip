@@ -24,6 +24,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <cmath>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -146,12 +147,29 @@ struct kans_layer {
   int basis, dtype, D_in, D_out, K, has_base, has_bias;
   int D_in8, nfb, nob_pad;
   BasisParams bp{};
-  std::vector<float> centers;
-  DevBuf centers_d, Wt, bias_d, part, x_d, y_d, raw_w, raw_wb;
+  DevBuf Wt, bias_d, part, x_d, y_d, raw_w, raw_wb;
   bool have_weights = false;
   int forced_wm = 0, forced_nb = 0, forced_splits = 0;  // tuning overrides (0 = heuristic)
   unsigned gen = 0;  // bumped whenever a buffer captured by a graph may have moved
 };
+
+// Uniform-centre form of the RBF basis: when c_k = c_0 + k*h holds to 1e-6 of
+// the grid's magnitude, the kernels may evaluate exp2(-(s*x - s*c_0 - k*s*h)^2)
+// with s = sqrt(-neg_l) instead of loading c_k per slot.
+static void set_rbf_uniform(BasisParams& bp) {
+  const int K = bp.K;
+  const double c0 = bp.centers[0];
+  const double h = K > 1 ? ((double)bp.centers[K - 1] - c0) / (K - 1) : 0.0;
+  double mag = std::fabs(c0);
+  for (int k = 0; k < K; ++k) mag = std::max(mag, (double)std::fabs(bp.centers[k]));
+  bool uni = bp.neg_l < 0.0f && std::isfinite(bp.neg_l);
+  for (int k = 0; k < K && uni; ++k) uni = std::fabs((double)bp.centers[k] - (c0 + k * h)) <= 1e-6 * mag;
+  const double sq = uni ? std::sqrt(-(double)bp.neg_l) : 0.0;
+  bp.rbf_uniform = uni ? 1 : 0;
+  bp.rbf_s = (float)sq;
+  bp.rbf_sc0 = (float)(sq * c0);
+  bp.rbf_sh = (float)(sq * h);
+}
 
 static int validate_dims(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias) {
   if (basis < 0 || basis > 2) return kans_fail(KANS_ERR_ARG, "unknown basis %d", basis);
@@ -202,14 +220,11 @@ int kans_layer_set_rbf(kans_layer* L, const float* centers, float inv_den) {
   if (!L || !centers) return kans_fail(KANS_ERR_ARG, "null argument");
   if (L->basis != BASIS_RBF) return kans_fail(KANS_ERR_ARG, "layer basis is not RBF");
   std::lock_guard<std::mutex> lk(g_mu);
-  L->centers.assign(centers, centers + L->K);
-  void* old = L->centers_d.p;
-  int rc = L->centers_d.reserve(sizeof(float) * kMaxK);
-  if (rc) return rc;
-  if (old != L->centers_d.p) ++L->gen;
-  HIP_TRY(hipMemcpy(L->centers_d.p, L->centers.data(), sizeof(float) * L->K, hipMemcpyHostToDevice));
-  L->bp.centers = (const float*)L->centers_d.p;
+  for (int k = 0; k < L->K; ++k) L->bp.centers[k] = centers[k];
+  L->bp.have_centers = 1;
   L->bp.neg_l = -inv_den * kLog2e;
+  set_rbf_uniform(L->bp);
+  ++L->gen;  // the kernel arguments captured by a chain graph change
   return 0;
 }
 
@@ -366,7 +381,7 @@ static int layer_launch_locked(kans_layer* L, const void* X, long ldx, void* Y, 
   if ((x_dtype != L->dtype && x_dtype != DT_F32) || (y_dtype != L->dtype && y_dtype != DT_F32))
     return kans_fail(KANS_ERR_ARG, "input/output dtype must be the layer dtype or fp32");
   if (!L->have_weights) return kans_fail(KANS_ERR_STATE, "layer has no weights loaded");
-  if (L->basis == BASIS_RBF && !L->bp.centers) return kans_fail(KANS_ERR_STATE, "RBF centres not set");
+  if (L->basis == BASIS_RBF && !L->bp.have_centers) return kans_fail(KANS_ERR_STATE, "RBF centres not set");
   if (L->basis == BASIS_BSPLINE && L->bp.grid_size <= 0) return kans_fail(KANS_ERR_STATE, "B-spline grid not set");
   if (B <= 0) return 0;
   if (ldx < L->D_in8 || (ldx % 8) != 0)
@@ -633,11 +648,10 @@ static int sig_layer(int basis, int dtype, int D_in, int D_out, int K, int has_b
   L->nob_pad = round_up((D_out + 31) / 32, kObPad);
   L->bp.K = K;
   if (basis == BASIS_RBF) {
-    L->centers.assign(params.begin(), params.begin() + K);
-    if ((rc = L->centers_d.reserve(sizeof(float) * kMaxK))) return rc;
-    HIP_TRY(hipMemcpy(L->centers_d.p, L->centers.data(), sizeof(float) * K, hipMemcpyHostToDevice));
-    L->bp.centers = (const float*)L->centers_d.p;
+    for (int k = 0; k < K; ++k) L->bp.centers[k] = params[k];
+    L->bp.have_centers = 1;
     L->bp.neg_l = -params[K] * kLog2e;
+    set_rbf_uniform(L->bp);
   } else if (basis == BASIS_BSPLINE) {
     L->bp.grid_size = K - 3;
     L->bp.grid_min = params[0];

@@ -8,6 +8,7 @@ library is loaded once into a module global, every export gets explicit
 Differences by design: the library (``libkans_hip.so``) is built ahead of time
 for gfx950 (``python metal-kans_amd/build.py``) instead of on import, and there
 is no CPU fallback -- without the library or a gfx950 GPU the layers raise.
+``KANS_LIB_PATH`` selects another build of the library.
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ import os
 from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkans_hip.so")
+LIB_PATH = os.environ.get("KANS_LIB_PATH") or os.path.join(_HERE, "libkans_hip.so")
 
 _lib: Optional[ctypes.CDLL] = None
 _initialised = False
