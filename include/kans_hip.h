@@ -136,6 +136,13 @@ int metal_kan_dequantize_ternary(const uint32_t* packed, const float* scales, fl
 /* replaces metal_kan_swiglu_forward (device.py:431-434, metal_kan_bridge.mm:4846-4875) */
 int metal_kan_swiglu_forward(const float* gate, const float* up, float* out, int n);
 
+/* replaces metal_kan_forward_ternary_cheby (device.py:381-385, metal_kan_bridge.mm:4684-4733,
+ * fused_kan.metal:2167-2223): fp32 X [B][D_in], ternary W [D_out][D_in*degree] in the packed format
+ * above, no base branch, optional fp32 bias; fp32 arithmetic on the exact dequantized weights. */
+int metal_kan_forward_ternary_cheby(const float* X, const uint32_t* W_packed, const float* scales,
+                                    const float* bias, float* Y, int B, int D_in, int D_out, int degree,
+                                    int group_size, int has_bias);
+
 /* replaces metal_kan_chain_pipeline_cheby (device.py:116-122, metal_kan_bridge.mm:1168-1248):
  * fp32 Chebyshev layers dims[0] -> ... -> dims[num_layers], any K per layer (the reference
  * hard-codes K = 4); W_bases[l] / biases[l] may be NULL to disable that branch.  Runs as one
@@ -203,6 +210,48 @@ int kans_dequantize_affine_device(const void* qweight, const float* scales, cons
                                   long num_groups, int group_size, int bits, void* stream);
 int kans_dequantize_ternary_device(const uint32_t* packed, const float* scales, float* out, int D_out, int K_dim,
                                    int group_size, void* stream);
+
+/* ----------------------------------------------------------------------- *
+ * Quantized Chebyshev layers and the GatedKAN block, decode path (B <= 32).  *
+ * Built from the reference's packed formats (quantization.py:13-99 INT4,     *
+ * :191-246 ternary); no reference counterpart for the fused forward with the *
+ * base branch (the reference dequantizes to fp32, quantization.py:152-178,   *
+ * gated_kan.py:86-138).  Activations are evaluated in fp32 and fed to the    *
+ * MFMAs in fp16; results are accumulated in fp32.                            *
+ * ----------------------------------------------------------------------- */
+typedef struct kans_qlayer kans_qlayer;
+/* INT4, group_size 64: qweight [D_out * pad/64][32] uint8, scales / biases [D_out * pad/64] fp32,
+ * pad = D_in*K rounded up to 64 (W) or D_in rounded up to 64 (W_base); bias [D_out] of bias_dtype */
+int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                            const void* qweight, const float* scales, const float* biases,
+                            const void* qweight_base, const float* scales_base, const float* biases_base,
+                            const void* bias, int bias_dtype, kans_qlayer** out);
+/* ternary, group_size 32: w_packed [D_out][ceil(D_in*K/16)] uint32, scales [D_out][ceil(D_in*K/32)]
+ * (base: the same with D_in) */
+int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                               const uint32_t* w_packed, const float* scales, const uint32_t* w_packed_base,
+                               const float* scales_base, const void* bias, int bias_dtype, kans_qlayer** out);
+int kans_qlayer_destroy(kans_qlayer* layer);
+/* device pointers; x_dtype / y_dtype any of KANS_DT_* */
+int kans_qlayer_forward(kans_qlayer* layer, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy,
+                        int B, void* stream);
+int kans_qlayer_forward_host(kans_qlayer* layer, const void* X, int x_dtype, void* Y, int y_dtype, int B);
+
+/* GatedKAN block out = down(SiLU(gate(x)) * up(x)) (gated_kan.py:86-138); the layers are borrowed and
+ * must outlive the block.  round16: 1 (fp16) / 2 (bf16) rounds the gate, up and hidden activations as a
+ * 16-bit model does, 0 keeps them fp32. */
+typedef struct kans_gated kans_gated;
+int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out);
+int kans_gated_destroy(kans_gated* block);
+int kans_gated_forward(kans_gated* block, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy,
+                       int B, int round16, void* stream);
+int kans_gated_forward_host(kans_gated* block, const void* X, int x_dtype, void* Y, int y_dtype, int B,
+                            int round16);
+/* mean ms per block forward on device X / Y (use_graph: replay one captured HIP graph) */
+int kans_gated_time(kans_gated* block, const void* X, int x_dtype, void* Y, int y_dtype, int B, int warmup,
+                    int iters, int use_graph, float* ms);
+/* algorithmic bytes of one block forward: packed weights + group parameters + x and y (fp16) */
+long long kans_gated_stream_bytes(const kans_gated* block, int B);
 
 /* device memory helpers; kans_copy_device is a plain copy kernel (16-byte multiples) used to
  * calibrate hardware byte counters */

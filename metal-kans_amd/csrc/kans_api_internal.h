@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include "kans_common.h"
 #include "../../include/kans_hip.h"
+#include <mutex>
 
 namespace kans {
 
@@ -24,3 +25,54 @@ struct DenseLaunch {
 
 int kans_fail(int code, const char* fmt, ...);
 hipStream_t kans_default_stream();
+
+// Library lock (serialises every entry point that touches device state), lazy
+// device initialisation (call with the lock held) and the grow-only pinned
+// staging buffers of the synchronous host-pointer entry points (which = 0 in,
+// 1 out; lock held).
+std::mutex& kans_mutex();
+int kans_ensure_init();
+int kans_pinned_stage(int which, size_t bytes, void** p);
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t _e = (expr);                                                                 \
+    if (_e != hipSuccess)                                                                   \
+      return kans_fail(KANS_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                       __FILE__, __LINE__);                                                 \
+  } while (0)
+
+// Grow-only device buffer.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { if (p) (void)hipFree(p); }
+  int reserve(size_t bytes) {
+    if (bytes <= cap) return 0;
+    if (p) HIP_TRY(hipFree(p));
+    p = nullptr;
+    cap = 0;
+    HIP_TRY(hipMalloc(&p, bytes));
+    cap = bytes;
+    return 0;
+  }
+};
+
+// Grow-only pinned host buffer.
+struct Pinned {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+inline int pinned_reserve(Pinned& b, size_t bytes) {
+  if (bytes <= b.cap) return 0;
+  if (b.p) HIP_TRY(hipHostFree(b.p));
+  b.p = nullptr;
+  b.cap = 0;
+  size_t cap = bytes + bytes / 4;
+  HIP_TRY(hipHostMalloc(&b.p, cap, hipHostMallocDefault));
+  b.cap = cap;
+  return 0;
+}

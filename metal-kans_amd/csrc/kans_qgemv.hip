@@ -1,0 +1,642 @@
+// Fused decode (small-batch) forward of Chebyshev KAN layers whose weights are
+// kept in the reference's packed INT4 or ternary formats, and of the GatedKAN
+// block built from three such layers.
+//
+//   y[b,o] = bias[o] + sum_i SiLU(v[b,i]) Wb[o,i] + sum_{i,k} T_k(clamp v[b,i]) W[o,i*K+k]
+//   W  = q*s + b per group of 64 (INT4, quantization.py:13-99), or
+//        t*s, t in {-1,0,+1} per group of 32 (ternary, quantization.py:191-246)
+//
+// Replaces metal_kan_forward_ternary_cheby (metal_kan_bridge.mm:4684-4733,
+// fused_kan.metal:2167-2223), which has no base branch and no INT4 variant, and
+// the reference GatedKAN forward on dequantized weights (gated_kan.py:86-138).
+//
+// At B <= 32 the layer is HBM-bound: the job is to stream the packed weights
+// once at full bandwidth.  Design:
+//   * the packed weights are re-tiled once on upload into MFMA B-fragment order:
+//     one "superchunk" = 16 output rows x 128 reduction indices, one 16-byte
+//     (INT4) or 8-byte (ternary) load per lane, 1 KB / 512 B per wave, fully
+//     coalesced; the per-group affine parameters are re-tiled alongside;
+//   * INT4 nibbles become fp16 with the 0x6400|q trick (the fp16 value 1024+q,
+//     exact), two per v_and_or_b32; ternary codes become +-1/0 fp16 through a
+//     v_perm_b32 byte table.  The group scale is applied to the fp32 MFMA
+//     accumulator once per group: y += s * sum(phi*(1024+q)) + (b - 1024 s) *
+//     sum(phi) for INT4, y += s * sum(phi*t) for ternary;
+//   * the activation basis phi (T_k and SiLU of the layer input, fp16, permuted
+//     to match the unpack order) and its per-group sums are computed once per
+//     layer into a small buffer that stays in L2; every wave reads its A
+//     fragments (v_mfma_f32_16x16x32_f16, 16 batch rows per tile) from there;
+//   * one wave owns 4 row blocks (64 output rows) and a contiguous range of
+//     superchunks (split-K over waves for memory-level parallelism); partial
+//     sums go to an fp32 workspace that a small kernel reduces (+ bias), in
+//     the GatedKAN block together with SwiGLU(gate, up).
+#include "kans_common.h"
+#include "kans_api_internal.h"
+#include "kans_qgemv.h"
+#include <algorithm>
+
+namespace kans {
+
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Re-tiling of the wire formats (run once per layer).
+//
+// Tile order: [row group of nw row blocks][superchunk][row block in group]:
+// the nw tiles one decode wave reads per superchunk are contiguous, and each
+// wave's superchunk range is one contiguous stream.  nw is chosen per layer
+// (kans_qgemv.h: qrow_blocks).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ long qtile_index(int rb, int c, int C_tot, int nw) {
+  return ((long)(rb / nw) * C_tot + c) * nw + rb % nw;
+}
+
+// INT4 qweight: row n is `rowbytes` bytes (groups of 64 nibbles contiguous,
+// even index in the low nibble).  Q[rb][c][lane], lane = (q = l/16, r = l%16):
+// dword t holds the 8 nibbles of row 16*rb + r at reduction indices
+// 128c + 32t + 8q .. +7, i.e. bytes 64c + 16t + 4q .. +3 of the row.
+__global__ void k_tile_int4(const unsigned char* __restrict__ qw, long rowbytes, int D_out, int nrb, int C,
+                            int c_off, int C_tot, int nw, uint4* __restrict__ Q) {
+  const long total = (long)nrb * C * 64;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    const long r2 = idx >> 6;
+    const int c = (int)(r2 % C);
+    const int rb = (int)(r2 / C);
+    const int q = lane >> 4, r = lane & 15;
+    const int n = rb * 16 + r;
+    unsigned w[4] = {0u, 0u, 0u, 0u};
+    if (n < D_out) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const long off = 64L * c + 16 * t + 4 * q;
+        if (off < rowbytes) {
+          const unsigned char* p = qw + (long)n * rowbytes + off;
+          w[t] = (unsigned)p[0] | ((unsigned)p[1] << 8) | ((unsigned)p[2] << 16) | ((unsigned)p[3] << 24);
+        }
+      }
+    }
+    Q[qtile_index(rb, c_off + c, C_tot, nw) * 64 + lane] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// INT4 group parameters: SB[rb][c][r] = (s0, s0', s1, s1') for the groups
+// 2c, 2c+1 of row 16*rb + r, s' = b - 1024 s (zero past the row / matrix).
+__global__ void k_tile_int4_params(const float* __restrict__ scales, const float* __restrict__ biases, int gpr,
+                                   int D_out, int nrb, int C, int c_off, int C_tot, int nw, float4* __restrict__ SB) {
+  const long total = (long)nrb * C * 16;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int r = (int)(idx & 15);
+    const long r2 = idx >> 4;
+    const int c = (int)(r2 % C);
+    const int rb = (int)(r2 / C);
+    const int n = rb * 16 + r;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (n < D_out) {
+#pragma unroll
+      for (int gs = 0; gs < 2; ++gs) {
+        const int g = 2 * c + gs;
+        if (g < gpr) {
+          const float s = scales[(long)n * gpr + g], b = biases[(long)n * gpr + g];
+          v[2 * gs] = s;
+          v[2 * gs + 1] = b - 1024.0f * s;
+        }
+      }
+    }
+    SB[qtile_index(rb, c_off + c, C_tot, nw) * 16 + r] = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// Ternary w_packed: row n is `wpr` uint32 words, code of index j at bits
+// 2*(j%16) of word j/16.  T[rb][c][lane] (uint2): word u in {0,1} covers steps
+// 2u ("A") and 2u+1 ("B"); the 8 codes of step t for lane (q, r) are those of
+// row 16*rb + r at indices j0 = 128c + 32t + 8q .. +7.  Code e of step A sits at
+// bit 2p (e = 2p) or 16 + 2p (e = 2p+1); of step B at bit 8 + 2p or 24 + 2p,
+// so that one shift aligns the two codes of an fp16 pair at bits 8 and 24.
+__global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim, int D_out, int nrb, int C,
+                            int c_off, int C_tot, int nw, uint2* __restrict__ T) {
+  const long total = (long)nrb * C * 64;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    const long r2 = idx >> 6;
+    const int c = (int)(r2 % C);
+    const int rb = (int)(r2 / C);
+    const int q = lane >> 4, r = lane & 15;
+    const int n = rb * 16 + r;
+    unsigned out[2] = {0u, 0u};
+    if (n < D_out) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const long j0 = 128L * c + 32 * t + 8 * q;
+        unsigned h = 0u;  // 8 codes, code e at bits 2e
+        if (j0 < K_dim) {
+          const unsigned word = wp[(long)n * wpr + j0 / 16];
+          h = (word >> (2 * (j0 % 16))) & 0xffffu;
+          const long valid = K_dim - j0;  // codes past K_dim read as 1 (zero weight)
+          if (valid < 8) h = (h & ((1u << (2 * valid)) - 1u)) | (0x5555u & ~((1u << (2 * valid)) - 1u));
+        } else {
+          h = 0x5555u;
+        }
+        const int base = (t & 1) ? 8 : 0;
+        unsigned v = 0u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          v |= ((h >> (4 * p)) & 3u) << (base + 2 * p);           // e = 2p
+          v |= ((h >> (4 * p + 2)) & 3u) << (base + 16 + 2 * p);  // e = 2p + 1
+        }
+        out[t >> 1] |= v;
+      }
+    }
+    T[qtile_index(rb, c_off + c, C_tot, nw) * 64 + lane] = make_uint2(out[0], out[1]);
+  }
+}
+
+// Ternary scales: SB[rb][c][r] = scales of the four 32-groups of superchunk c.
+__global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, int D_out, int nrb, int C, int c_off,
+                                   int C_tot, int nw, float4* __restrict__ SB) {
+  const long total = (long)nrb * C * 16;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int r = (int)(idx & 15);
+    const long r2 = idx >> 4;
+    const int c = (int)(r2 % C);
+    const int rb = (int)(r2 / C);
+    const int n = rb * 16 + r;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (n < D_out) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int g = 4 * c + t;
+        if (g < gpr) v[t] = scales[(long)n * gpr + g];
+      }
+    }
+    SB[qtile_index(rb, c_off + c, C_tot, nw) * 16 + r] = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation basis.  Phi[m][p] (fp16, m < MP, p < C_tot*128): the basis segment
+// (p < Cb*128) holds T_k(clamp v[m][i]) at reduction index j = i*K + k, the base
+// segment SiLU(v[m][i]) at j = i; within each 8-block the order is the unpack
+// order pi of the weight format (INT4: 0,4,1,5,2,6,3,7; ternary: identity).
+// S[c][m] = (sum over group 2c, sum over group 2c+1) of the fp16-rounded values
+// (INT4 only).  Indices past the segment's length are 0.
+// ---------------------------------------------------------------------------
+template <int QT>
+__device__ __forceinline__ int unpack_order(int e) {
+  if constexpr (QT == Q_INT4) return (e >> 1) + 4 * (e & 1);
+  return e;
+}
+
+__device__ __forceinline__ float cheb_k(float t, int k) {
+  // T_k(t) by the recurrence, as the reference (fused_kan.metal:216-236).
+  float a = 1.0f, b = t;
+  if (k == 0) return a;
+  for (int i = 1; i < k; ++i) {
+    const float c = __builtin_fmaf(2.0f * t, b, -a);
+    a = b;
+    b = c;
+  }
+  return b;
+}
+
+// SiLU with the reference's clip of the exponent argument (gated_kan.py:15-21).
+__device__ __forceinline__ float silu_clip(float g) {
+  const float c = fminf(fmaxf(g, -20.0f), 20.0f);
+  return g / (1.0f + __expf(-c));
+}
+
+__device__ __forceinline__ float load_any(const void* p, long i, int dt) {
+  if (dt == DT_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dt == DT_F16) return (float)reinterpret_cast<const _Float16*>(p)[i];
+  return to_f32(reinterpret_cast<const __bf16*>(p)[i]);
+}
+
+// Layer input v[m][i] of k_prep.
+struct PrepIn {
+  const void* X;
+  int x_dtype;
+  long ldx;
+};
+
+__device__ __forceinline__ float prep_input(const PrepIn& in, int m, int i) {
+  return load_any(in.X, (long)m * in.ldx + i, in.x_dtype);
+}
+
+// One thread per (m, 8-block of the concatenated reduction axis).  Block = 256
+// threads = 16 superchunks' worth of 8-blocks for one m (8-blocks of a
+// superchunk are 16 consecutive threads, so group sums reduce within 8 lanes).
+template <int QT>
+__global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in, int K, int has_base, int Cb,
+                                              int C_tot, _Float16* __restrict__ Phi, float2* __restrict__ S) {
+  const int m = blockIdx.y;
+  const long blk = (long)blockIdx.x * 256 + threadIdx.x;  // 8-block index over C_tot*16
+  const bool live = blk < (long)C_tot * 16;
+  const long p0 = blk * 8;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  if (live && m < B) {
+    const long Jb = (long)D_in * K;
+    if (p0 < (long)Cb * 128) {
+      // the 8 indices cover features i0 .. i0 + 8/K (+1); each input read once
+      const long i0 = p0 / K;
+      float xin[9];
+      const int nf = (int)((p0 + 7) / K - i0) + 1;
+#pragma unroll
+      for (int f = 0; f < 9; ++f)
+        if (f < nf && (i0 + f) * K < Jb) xin[f] = fminf(fmaxf(prep_input(in, m, (int)(i0 + f)), -1.0f), 1.0f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const long j = p0 + unpack_order<QT>(e);
+        if (j < Jb) {
+          const long i = j / K;
+          v[e] = cheb_k(xin[i - i0], (int)(j - i * K));
+        }
+      }
+    } else if (has_base) {
+      const long i0 = p0 - (long)Cb * 128;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const long i = i0 + unpack_order<QT>(e);
+        if (i < D_in) v[e] = silu_f32(prep_input(in, m, (int)i));
+      }
+    }
+  }
+  _Float16 hv[8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hv[e] = (_Float16)v[e];
+    sum += (float)hv[e];
+  }
+  if (live && m < MP) *reinterpret_cast<uint4*>(Phi + (long)m * C_tot * 128 + p0) = *reinterpret_cast<uint4*>(hv);
+  if constexpr (QT == Q_INT4) {
+    // group of 64 = 8 consecutive 8-blocks = 8 consecutive lanes
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    const float other = __shfl_xor(sum, 8);
+    if (live && m < MP && (threadIdx.x & 15) == 0) S[(blk >> 4) * MP + m] = make_float2(sum, other);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV.
+// ---------------------------------------------------------------------------
+// Unpack constants held in VGPRs: with two literal constants the compiler
+// splits (a & mask) | orv into v_and + v_or (a VOP3 instruction here encodes no
+// literal and reads at most one SGPR); as opaque register values it selects
+// one v_and_or_b32.  The empty asm only hides the values from constant folding.
+struct UnpackConsts {
+  unsigned nib_mask, nib_magic, tsel_mask, tsel_zero;
+  __device__ __forceinline__ void init() {
+    nib_mask = 0x000F000Fu;
+    nib_magic = 0x64006400u;
+    tsel_mask = 0x03000300u;
+    tsel_zero = 0x000C000Cu;
+    asm volatile("" : "+v"(nib_mask), "+v"(nib_magic), "+v"(tsel_mask), "+v"(tsel_zero));
+  }
+};
+
+// INT4: 8 nibbles -> 8 fp16 values 1024+q in the order 0,4,1,5,2,6,3,7.
+__device__ __forceinline__ half8v unpack_int4(unsigned w, const UnpackConsts& k) {
+  unsigned o[4];
+  o[0] = (w & k.nib_mask) | k.nib_magic;
+  o[1] = ((w >> 4) & k.nib_mask) | k.nib_magic;
+  o[2] = ((w >> 8) & k.nib_mask) | k.nib_magic;
+  o[3] = ((w >> 12) & k.nib_mask) | k.nib_magic;
+  return *reinterpret_cast<half8v*>(o);
+}
+
+// Ternary: the 8 codes of one step (layout of k_tile_tern) -> 8 fp16 in
+// {-1, 0, +1}.  v_perm_b32 picks each value's high byte from the table
+// {0xBC, 0x00, 0x3C, 0x00} (code 0 -> -1.0, 1 -> 0, 2 -> +1.0, 3 -> 0) with the
+// code as selector; selector 12 yields the zero low bytes.
+template <int B_STEP>
+__device__ __forceinline__ half8v unpack_tern(unsigned w, const UnpackConsts& k) {
+  constexpr unsigned kTable = 0x003C00BCu;
+  unsigned o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const unsigned v = B_STEP ? (w >> (2 * p)) : (w << (8 - 2 * p));
+    const unsigned sel = (v & k.tsel_mask) | k.tsel_zero;  // codes in bytes 1, 3; 12 (= 0x00) in bytes 0, 2
+    o[p] = __builtin_amdgcn_perm(0u, kTable, sel);
+  }
+  return *reinterpret_cast<half8v*>(o);
+}
+
+struct QMatDev {
+  const void* q;        // INT4: uint4 [nrb_pad][C_tot][64]; ternary: uint2
+  const float4* sb;     // [nrb_pad][C_tot][16]
+  int D_out;
+  int col_off;          // column offset of this matrix in the output / workspace
+};
+
+// One wave = kQNW row blocks (64 output rows) x one contiguous superchunk range
+// (split-K over waves for memory-level parallelism); 4 independent waves per
+// workgroup.  part[ks][m][col] (m < B) receives the wave's partial sums.
+// SMALL (B <= kSmallB): batch row m lives only in accumulator register m of
+// lanes 0-15, so the per-group epilogue updates just those registers.
+constexpr int kSmallB = 2;
+constexpr int kQNW = 4;
+
+template <int QT, int MT, bool SMALL>
+__global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
+                                               int C_tot, const _Float16* __restrict__ Phi,
+                                               const float2* __restrict__ S, int B, int MP,
+                                               float* __restrict__ part, int N_total) {
+  constexpr int NW = kQNW;
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int rg = item / ksplit;
+  const int ks = item - rg * ksplit;
+  if (rg >= n_rg) return;  // uniform per wave
+  const QMatDev& M = rg < rg_split ? m0 : m1;
+  const int rg_loc = rg < rg_split ? rg : rg - rg_split;
+  const int rb0 = rg_loc * NW;
+  const int c_lo = (int)((long)C_tot * ks / ksplit);
+  const int c_hi = (int)((long)C_tot * (ks + 1) / ksplit);
+  const int q = lane >> 4, r = lane & 15;
+  const long ldphi = (long)C_tot * 128;
+  UnpackConsts uk;
+  uk.init();
+
+  floatx4 acc[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc[mt][w] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  bool arow[MT];
+  const _Float16* arow_p[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    arow[mt] = mt * 16 + r < B;
+    arow_p[mt] = Phi + (long)(mt * 16 + r) * ldphi + 8 * q;
+  }
+
+  typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
+  const QWord* qbase = reinterpret_cast<const QWord*>(M.q);
+
+  // operands of one superchunk.  The weights / group parameters of superchunk
+  // c+1 are loaded while c is consumed; the activation fragments of c (L2
+  // resident) are loaded just before that prefetch is issued, so waiting for
+  // them (vmcnt counts in issue order) never waits for the prefetch.
+  struct Wts {
+    QWord qw[NW];
+    float4 sb[NW];
+  };
+  struct Acts {
+    half8v a[MT][4];
+    float2 sg[MT][4];  // INT4: group sums of rows m = 16mt + 4q + i
+  };
+  struct Ops {
+    Wts w;
+    Acts x;
+  };
+  auto load_w = [&](int c, Wts& o) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const long tile = ((long)rg_loc * C_tot + c) * NW + w;
+      o.qw[w] = qbase[tile * 64 + lane];
+      // the four lanes of a row (q = 0..3) share its group parameters; with
+      // SMALL only lanes 0-15 (q = 0) hold live accumulators, so only they load
+      // (16 distinct 16-byte requests instead of 64 duplicated ones)
+      if (!SMALL || q == 0) o.sb[w] = M.sb[tile * 16 + r];
+      else o.sb[w] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto load_x = [&](int c, Acts& o) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (arow[mt]) u = *reinterpret_cast<const uint4*>(arow_p[mt] + (long)c * 128 + 32 * t);
+        o.a[mt][t] = *reinterpret_cast<half8v*>(&u);
+      }
+    if constexpr (QT == Q_INT4) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
+          const int mm = mt * 16 + 4 * q + i;
+          o.sg[mt][i] = mm < B ? S[(long)c * MP + mm] : make_float2(0.f, 0.f);
+        }
+    }
+  };
+  auto compute = [&](const Wts& ow, const Acts& ox) {
+    if constexpr (QT == Q_INT4) {
+#pragma unroll
+      for (int gs = 0; gs < 2; ++gs) {
+        floatx4 g[MT][NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const half8v b0 = unpack_int4(dw[2 * gs], uk);
+          const half8v b1 = unpack_int4(dw[2 * gs + 1], uk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][2 * gs + 1], b1, g[mt][w], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float s = gs ? ow.sb[w].z : ow.sb[w].x;
+          const float s2 = gs ? ow.sb[w].w : ow.sb[w].y;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
+              const float S_ = gs ? ox.sg[mt][i].y : ox.sg[mt][i].x;
+              acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
+            }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        floatx4 g[MT][NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const half8v bf = (t & 1) ? unpack_tern<1>(dw[t >> 1], uk) : unpack_tern<0>(dw[t >> 1], uk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][t], bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float s = t == 0 ? ow.sb[w].x : t == 1 ? ow.sb[w].y : t == 2 ? ow.sb[w].z : ow.sb[w].w;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], acc[mt][w][i]);
+        }
+      }
+    }
+  };
+
+  Wts w0, w1;
+  if (c_lo < c_hi) load_w(c_lo, w0);
+  for (int c = c_lo; c < c_hi; c += 2) {
+    Acts x;
+    load_x(c, x);
+    if (c + 1 < c_hi) load_w(c + 1, w1);
+    compute(w0, x);
+    if (c + 1 >= c_hi) break;
+    load_x(c + 1, x);
+    if (c + 2 < c_hi) load_w(c + 2, w0);
+    compute(w1, x);
+  }
+
+  // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int n = (rb0 + w) * 16 + r;
+    if (n < M.D_out) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
+          const int mm = mt * 16 + 4 * q + i;
+          if (mm < B) part[((long)ks * B + mm) * N_total + M.col_off + n] = acc[mt][w][i];
+        }
+    }
+  }
+}
+
+// y[m][col] = sum_ks part[ks][m][col] + bias.  Block = 64 columns x 4 split
+// lanes: lane g sums the splits ks = g, g+4, ... in order, then the four
+// partial sums are added in order (deterministic).
+template <typename TY>
+__global__ void __launch_bounds__(256) k_qreduce(const float* __restrict__ part, int ksplit, int B, int N,
+                                                 const void* bias, int bias_dtype, TY* __restrict__ Y, long ldy) {
+  __shared__ float red[4][64];
+  const int col = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int m = blockIdx.y;
+  const int n = blockIdx.x * 64 + col;
+  const long total = (long)B * N;
+  float sum = 0.0f;
+  if (n < N) {
+    const float* p = part + (long)m * N + n;
+    for (int k = g; k < ksplit; k += 4) sum += p[(long)k * total];
+  }
+  red[g][col] = sum;
+  __syncthreads();
+  if (g == 0 && n < N) {
+    float t = bias ? load_any(bias, n, bias_dtype) : 0.0f;
+    t += red[0][col];
+    t += red[1][col];
+    t += red[2][col];
+    t += red[3][col];
+    Y[(long)m * ldy + n] = from_f32<TY>(t);
+  }
+}
+
+// GatedKAN hidden state from the gate / up partial sums (columns [0, h) and
+// [h, 2h) of part[ks][m][.]): hidden = SiLU(gate) * up (gated_kan.py:86-138,
+// swiglu_forward_f32 fused_kan.metal:2284-2296, with the +-20 clip).  With
+// round16 the gate and up layer outputs and the hidden state are rounded to
+// fp16 (1) / bf16 (2), as the layer dtype does in the unfused path.
+__global__ void k_qswiglu(const float* __restrict__ part, int ksplit, int B, int h, const void* bias_g,
+                          const void* bias_u, int bias_dtype, int round16, float* __restrict__ hidden) {
+  const long total = (long)B * h;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int m = (int)(idx / h), i = (int)(idx - (long)m * h);
+    float g = bias_g ? load_any(bias_g, i, bias_dtype) : 0.0f;
+    float u = bias_u ? load_any(bias_u, i, bias_dtype) : 0.0f;
+    const float* p = part + (long)m * 2 * h;
+    for (int k = 0; k < ksplit; ++k) {
+      g += p[(long)k * B * 2 * h + i];
+      u += p[(long)k * B * 2 * h + h + i];
+    }
+    auto rnd = [&](float v) { return round16 == 2 ? to_f32(from_f32<__bf16>(v)) : (float)(_Float16)v; };
+    if (round16) {
+      g = rnd(g);
+      u = rnd(u);
+    }
+    float hv = silu_clip(g) * u;
+    if (round16) hv = rnd(hv);
+    hidden[idx] = hv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers.
+// ---------------------------------------------------------------------------
+static int grid_for(long n) { return (int)std::min<long>((n + 255) / 256, 8192); }
+
+hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
+                      int gpr, int nrb, int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st) {
+  hipLaunchKernelGGL(k_tile_int4, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, qw, rowbytes, D_out, nrb, C,
+                     c_off, C_tot, nw, (uint4*)Q);
+  hipLaunchKernelGGL(k_tile_int4_params, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales, biases, gpr,
+                     D_out, nrb, C, c_off, C_tot, nw, SB);
+  return hipGetLastError();
+}
+
+hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wpr, long K_dim, int gpr, int nrb,
+                      int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st) {
+  hipLaunchKernelGGL(k_tile_tern, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, wp, wpr, K_dim, D_out, nrb,
+                     C, c_off, C_tot, nw, (uint2*)Q);
+  hipLaunchKernelGGL(k_tile_tern_params, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales, gpr, D_out,
+                     nrb, C, c_off, C_tot, nw, SB);
+  return hipGetLastError();
+}
+
+hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
+  dim3 grid((unsigned)((P.C_tot * 16 + 255) / 256), (unsigned)P.MP);
+  PrepIn in{P.X, P.x_dtype, P.ldx};
+  if (qt == Q_INT4)
+    hipLaunchKernelGGL((k_prep<Q_INT4>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
+                       P.C_tot, P.Phi, P.S);
+  else
+    hipLaunchKernelGGL((k_prep<Q_TERN>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
+                       P.C_tot, P.Phi, P.S);
+  return hipGetLastError();
+}
+
+hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
+  QMatDev a{G.q0, G.sb0, G.D_out0, 0};
+  QMatDev b{G.q1 ? G.q1 : G.q0, G.q1 ? G.sb1 : G.sb0, G.D_out1, G.D_out0};
+  const int items = G.n_rg * G.ksplit;
+  dim3 grid((unsigned)((items + 3) / 4));
+#define KQ_GEMV(QTV, MTV, SM)                                                                                       \
+  hipLaunchKernelGGL((k_qgemv<QTV, MTV, SM>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit, G.C_tot, \
+                     G.Phi, G.S, G.B, G.MP, G.part, G.N_total)
+  const int mt = G.MP / 16;
+  const bool small = G.B <= kSmallB;
+  if (qt == Q_INT4) {
+    if (small) KQ_GEMV(Q_INT4, 1, true); else if (mt == 1) KQ_GEMV(Q_INT4, 1, false); else KQ_GEMV(Q_INT4, 2, false);
+  } else {
+    if (small) KQ_GEMV(Q_TERN, 1, true); else if (mt == 1) KQ_GEMV(Q_TERN, 1, false); else KQ_GEMV(Q_TERN, 2, false);
+  }
+#undef KQ_GEMV
+  return hipGetLastError();
+}
+
+hipError_t qreduce(const float* part, int ksplit, int B, int N, const void* bias, int bias_dtype, void* Y, int y_dtype,
+                   long ldy, hipStream_t st) {
+  const dim3 blocks((unsigned)((N + 63) / 64), (unsigned)B);
+  if (y_dtype == DT_F16)
+    hipLaunchKernelGGL((k_qreduce<_Float16>), blocks, dim3(256), 0, st, part, ksplit, B, N, bias, bias_dtype,
+                       (_Float16*)Y, ldy);
+  else if (y_dtype == DT_BF16)
+    hipLaunchKernelGGL((k_qreduce<__bf16>), blocks, dim3(256), 0, st, part, ksplit, B, N, bias, bias_dtype,
+                       (__bf16*)Y, ldy);
+  else
+    hipLaunchKernelGGL((k_qreduce<float>), blocks, dim3(256), 0, st, part, ksplit, B, N, bias, bias_dtype, (float*)Y,
+                       ldy);
+  return hipGetLastError();
+}
+
+hipError_t qswiglu(const float* part, int ksplit, int B, int h, const void* bias_g, const void* bias_u, int bias_dtype,
+                   int round16, float* hidden, hipStream_t st) {
+  hipLaunchKernelGGL(k_qswiglu, dim3(grid_for((long)B * h)), dim3(256), 0, st, part, ksplit, B, h, bias_g, bias_u,
+                     bias_dtype, round16, hidden);
+  return hipGetLastError();
+}
+
+}  // namespace kans

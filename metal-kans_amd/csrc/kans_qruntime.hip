@@ -1,0 +1,516 @@
+// Runtime objects of the quantized decode path: a Chebyshev KAN layer held in
+// the reference's packed INT4 / ternary formats (kans_qlayer) and the GatedKAN
+// block of three such layers (kans_gated), plus the reference-named fused
+// ternary entry point.  Kernels: kans_qgemv.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "kans_api_internal.h"
+#include "kans_qgemv.h"
+
+using namespace kans;
+
+namespace kans {
+int dequant_ternary_device(const uint32_t* p, const float* s, float* out, int D_out, int K_dim, int gs,
+                           hipStream_t st);
+}
+
+struct kans_qlayer {
+  int quant;                 // Q_INT4 / Q_TERN
+  int D_in, D_out, K, has_base, has_bias, group;
+  int Cb, Cw, C_tot;         // superchunks: basis, base, total
+  int nw;                    // 16-row blocks per decode row group (qrow_blocks)
+  int nrb_pad;               // 16-row blocks, padded to a multiple of nw
+  DevBuf Q, SB, bias;        // re-tiled weights, group parameters, bias (bias_dtype)
+  int bias_dtype = DT_F32;
+  // decode workspace: activation basis, its group sums, split-K partials
+  DevBuf Phi, S, part;
+};
+
+struct kans_gated {
+  kans_qlayer *gate, *up, *down;
+  DevBuf hidden;  // SwiGLU(gate, up) [B][h] fp32
+};
+
+namespace {
+
+constexpr int kMaxDecodeB = 32;
+
+int mp_of(int B) { return B <= 16 ? 16 : 32; }
+
+// Superchunk ranges per row group: ~10 work items (waves) per CU, at least 4
+// superchunks per item.
+int choose_ksplit(int n_rg, int C_tot) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+      cus = prop.multiProcessorCount;
+    if (cus <= 0) cus = 256;
+  }
+  int ks = (10 * cus + n_rg - 1) / n_rg;
+  ks = std::min(ks, std::max(1, C_tot / 4));
+  return std::max(ks, 1);
+}
+
+int layer_geometry(kans_qlayer* L) {
+  const long Jb = (long)L->D_in * L->K;
+  if (L->quant == Q_INT4) {
+    const long pb = (Jb + L->group - 1) / L->group * L->group;
+    const long pw = ((long)L->D_in + L->group - 1) / L->group * L->group;
+    L->Cb = (int)((pb + kQSuper - 1) / kQSuper);
+    L->Cw = L->has_base ? (int)((pw + kQSuper - 1) / kQSuper) : 0;
+  } else {
+    L->Cb = (int)((Jb + kQSuper - 1) / kQSuper);
+    L->Cw = L->has_base ? (int)(((long)L->D_in + kQSuper - 1) / kQSuper) : 0;
+  }
+  L->C_tot = L->Cb + L->Cw;
+  L->nw = qrow_blocks(L->D_out);
+  L->nrb_pad = round_up((L->D_out + 15) / 16, L->nw);
+  return 0;
+}
+
+int validate_q(int D_in, int D_out, int K, int has_base, int has_bias, int group, int quant) {
+  if (D_in <= 0 || D_out <= 0 || K <= 0 || K > kMaxK)
+    return kans_fail(KANS_ERR_ARG, "bad dims D_in=%d D_out=%d K=%d", D_in, D_out, K);
+  if ((has_base != 0 && has_base != 1) || (has_bias != 0 && has_bias != 1))
+    return kans_fail(KANS_ERR_ARG, "has_base/has_bias must be 0 or 1");
+  if (quant == Q_INT4 && group != 64)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "fused INT4 path needs group_size 64 (got %d)", group);
+  if (quant == Q_TERN && group != 32)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "fused ternary path needs group_size 32 (got %d)", group);
+  return 0;
+}
+
+// Upload host bytes to a temporary device buffer.
+int upload_tmp(DevBuf& d, const void* src, size_t bytes, hipStream_t st) {
+  int rc = d.reserve(bytes ? bytes : 16);
+  if (rc) return rc;
+  if (bytes) HIP_TRY(hipMemcpyAsync(d.p, src, bytes, hipMemcpyHostToDevice, st));
+  return 0;
+}
+
+int alloc_tiles(kans_qlayer* L) {
+  const size_t tiles = (size_t)L->nrb_pad * L->C_tot;
+  int rc = L->Q.reserve(tiles * 64 * (L->quant == Q_INT4 ? 16 : 8));
+  if (rc) return rc;
+  rc = L->SB.reserve(tiles * 16 * sizeof(float4));
+  if (rc) return rc;
+  HIP_TRY(hipMemsetAsync(L->Q.p, 0, tiles * 64 * (L->quant == Q_INT4 ? 16 : 8), kans_default_stream()));
+  HIP_TRY(hipMemsetAsync(L->SB.p, 0, tiles * 16 * sizeof(float4), kans_default_stream()));
+  return 0;
+}
+
+int upload_bias(kans_qlayer* L, const void* bias, int bias_dtype) {
+  if (!L->has_bias) return 0;
+  if (!bias) return kans_fail(KANS_ERR_ARG, "has_bias set but bias is null");
+  if (bias_dtype < DT_F32 || bias_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad bias dtype %d", bias_dtype);
+  const size_t bytes = (size_t)L->D_out * (bias_dtype == DT_F32 ? 4 : 2);
+  int rc = L->bias.reserve(bytes);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(L->bias.p, bias, bytes, hipMemcpyHostToDevice, kans_default_stream()));
+  L->bias_dtype = bias_dtype;
+  return 0;
+}
+
+int reserve_decode(kans_qlayer* L, int B, int ksplit, int N_total) {
+  const int MP = mp_of(B);
+  int rc = L->Phi.reserve((size_t)MP * L->C_tot * kQSuper * sizeof(_Float16));
+  if (rc) return rc;
+  rc = L->S.reserve((size_t)L->C_tot * MP * sizeof(float2));
+  if (rc) return rc;
+  return L->part.reserve((size_t)ksplit * B * N_total * sizeof(float));
+}
+
+int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hipStream_t st) {
+  QPrep P;
+  P.X = X;
+  P.x_dtype = x_dtype;
+  P.ldx = ldx;
+  P.B = B;
+  P.MP = mp_of(B);
+  P.D_in = L->D_in;
+  P.K = L->K;
+  P.has_base = L->has_base;
+  P.Cb = L->Cb;
+  P.C_tot = L->C_tot;
+  P.Phi = (_Float16*)L->Phi.p;
+  P.S = (float2*)L->S.p;
+  HIP_TRY(qprep(L->quant, P, st));
+  return 0;
+}
+
+// GEMV of layer a (and b, sharing a's activations): split-K partial sums in
+// a->part ([ksplit][B][a.D_out + b.D_out]).
+int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, hipStream_t st) {
+  QGemv G;
+  G.q0 = a->Q.p;
+  G.sb0 = (const float4*)a->SB.p;
+  G.D_out0 = a->D_out;
+  G.q1 = b ? b->Q.p : nullptr;
+  G.sb1 = b ? (const float4*)b->SB.p : nullptr;
+  G.D_out1 = b ? b->D_out : 0;
+  G.nw = a->nw;
+  G.rg_split = a->nrb_pad / a->nw;
+  G.n_rg = G.rg_split + (b ? b->nrb_pad / b->nw : 0);
+  G.ksplit = ksplit;
+  G.C_tot = a->C_tot;
+  G.Phi = (const _Float16*)a->Phi.p;
+  G.S = (const float2*)a->S.p;
+  G.B = B;
+  G.MP = mp_of(B);
+  G.part = (float*)a->part.p;
+  G.N_total = a->D_out + (b ? b->D_out : 0);
+  HIP_TRY(qgemv(a->quant, G, st));
+  return 0;
+}
+
+int check_x(const void* X, int x_dtype, long ldx, int D_in, int B) {
+  if (!X) return kans_fail(KANS_ERR_ARG, "null X");
+  if (x_dtype < DT_F32 || x_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad x dtype %d", x_dtype);
+  if (ldx < D_in) return kans_fail(KANS_ERR_ARG, "ldx=%ld < D_in=%d", ldx, D_in);
+  if (B <= 0 || B > kMaxDecodeB) return kans_fail(KANS_ERR_ARG, "decode path takes 1 <= B <= %d (got %d)", kMaxDecodeB, B);
+  return 0;
+}
+
+int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                          hipStream_t st) {
+  int rc = check_x(X, x_dtype, ldx, L->D_in, B);
+  if (rc) return rc;
+  if (!Y || ldy < L->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
+  if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
+  const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot);
+  if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
+  if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
+  if ((rc = gemv_locked(L, nullptr, B, ks, st))) return rc;
+  HIP_TRY(qreduce((const float*)L->part.p, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y,
+                  y_dtype, ldy, st));
+  return 0;
+}
+
+int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                         int round16, hipStream_t st) {
+  kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
+  int rc = check_x(X, x_dtype, ldx, g->D_in, B);
+  if (rc) return rc;
+  if (!Y || ldy < d->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
+  if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
+  const int h = g->D_out;
+  const int ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot);
+  const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot);
+  if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
+  if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
+  if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
+  if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
+  if ((rc = gemv_locked(g, u, B, ks1, st))) return rc;
+  HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr,
+                  u->has_bias ? u->bias.p : nullptr, g->bias_dtype, round16, (float*)G->hidden.p, st));
+  if ((rc = prep_locked(d, G->hidden.p, DT_F32, h, B, st))) return rc;
+  if ((rc = gemv_locked(d, nullptr, B, ks2, st))) return rc;
+  HIP_TRY(qreduce((const float*)d->part.p, ks2, B, d->D_out, d->has_bias ? d->bias.p : nullptr, d->bias_dtype, Y,
+                  y_dtype, ldy, st));
+  return 0;
+}
+
+size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+}  // namespace
+
+extern "C" {
+
+int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                            const void* qweight, const float* scales, const float* biases, const void* qweight_base,
+                            const float* scales_base, const float* biases_base, const void* bias, int bias_dtype,
+                            kans_qlayer** out) {
+  if (!out || !qweight || !scales || !biases) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (has_base && (!qweight_base || !scales_base || !biases_base))
+    return kans_fail(KANS_ERR_ARG, "has_base set but base arrays are null");
+  int rc = validate_q(D_in, D_out, K, has_base, has_bias, group_size, Q_INT4);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  if ((rc = kans_ensure_init())) return rc;
+  hipStream_t st = kans_default_stream();
+  auto* L = new kans_qlayer();
+  L->quant = Q_INT4;
+  L->D_in = D_in;
+  L->D_out = D_out;
+  L->K = K;
+  L->has_base = has_base;
+  L->has_bias = has_bias;
+  L->group = group_size;
+  layer_geometry(L);
+  auto fail = [&](int code) { delete L; return code; };
+  if ((rc = alloc_tiles(L))) return fail(rc);
+  // basis matrix W (D_out x D_in*K): padded rows of pad_b nibbles
+  const long pad_b = ((long)D_in * K + group_size - 1) / group_size * group_size;
+  const long gpr_b = pad_b / group_size;
+  DevBuf tq, ts, tb;
+  if ((rc = upload_tmp(tq, qweight, (size_t)D_out * pad_b / 2, st))) return fail(rc);
+  if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
+  if ((rc = upload_tmp(tb, biases, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
+  hipError_t e = qtile_int4((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, pad_b / 2,
+                            (int)gpr_b, L->nrb_pad, L->Cb, 0, L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+  if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
+  if (has_base) {
+    const long pad_w = ((long)D_in + group_size - 1) / group_size * group_size;
+    const long gpr_w = pad_w / group_size;
+    DevBuf wq, ws, wb;
+    if ((rc = upload_tmp(wq, qweight_base, (size_t)D_out * pad_w / 2, st))) return fail(rc);
+    if ((rc = upload_tmp(ws, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
+    if ((rc = upload_tmp(wb, biases_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
+    e = qtile_int4((const unsigned char*)wq.p, (const float*)ws.p, (const float*)wb.p, D_out, pad_w / 2, (int)gpr_w,
+                   L->nrb_pad, L->Cw, L->Cb, L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+    if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
+    if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
+    HIP_TRY(hipStreamSynchronize(st));  // temporaries die here
+  } else {
+    if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
+    HIP_TRY(hipStreamSynchronize(st));
+  }
+  *out = L;
+  return 0;
+}
+
+int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                               const uint32_t* w_packed, const float* scales, const uint32_t* w_packed_base,
+                               const float* scales_base, const void* bias, int bias_dtype, kans_qlayer** out) {
+  if (!out || !w_packed || !scales) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (has_base && (!w_packed_base || !scales_base))
+    return kans_fail(KANS_ERR_ARG, "has_base set but base arrays are null");
+  int rc = validate_q(D_in, D_out, K, has_base, has_bias, group_size, Q_TERN);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  if ((rc = kans_ensure_init())) return rc;
+  hipStream_t st = kans_default_stream();
+  auto* L = new kans_qlayer();
+  L->quant = Q_TERN;
+  L->D_in = D_in;
+  L->D_out = D_out;
+  L->K = K;
+  L->has_base = has_base;
+  L->has_bias = has_bias;
+  L->group = group_size;
+  layer_geometry(L);
+  auto fail = [&](int code) { delete L; return code; };
+  if ((rc = alloc_tiles(L))) return fail(rc);
+  const long kb = (long)D_in * K;
+  const int wpr_b = (int)((kb + 15) / 16), gpr_b = (int)((kb + group_size - 1) / group_size);
+  DevBuf tw, ts;
+  if ((rc = upload_tmp(tw, w_packed, (size_t)D_out * wpr_b * 4, st))) return fail(rc);
+  if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
+  hipError_t e = qtile_tern((const unsigned*)tw.p, (const float*)ts.p, D_out, wpr_b, kb, gpr_b, L->nrb_pad, L->Cb, 0,
+                            L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+  if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
+  DevBuf bw, bs;
+  if (has_base) {
+    const long kw = D_in;
+    const int wpr_w = (int)((kw + 15) / 16), gpr_w = (int)((kw + group_size - 1) / group_size);
+    if ((rc = upload_tmp(bw, w_packed_base, (size_t)D_out * wpr_w * 4, st))) return fail(rc);
+    if ((rc = upload_tmp(bs, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
+    e = qtile_tern((const unsigned*)bw.p, (const float*)bs.p, D_out, wpr_w, kw, gpr_w, L->nrb_pad, L->Cw, L->Cb,
+                   L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+    if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
+  }
+  if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
+  HIP_TRY(hipStreamSynchronize(st));
+  *out = L;
+  return 0;
+}
+
+int kans_qlayer_destroy(kans_qlayer* L) {
+  if (!L) return 0;
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  if (kans_default_stream()) (void)hipStreamSynchronize(kans_default_stream());
+  delete L;
+  return 0;
+}
+
+int kans_qlayer_forward(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                        void* stream) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = stream ? (hipStream_t)stream : kans_default_stream();
+  return qlayer_forward_locked(L, X, x_dtype, ldx, Y, y_dtype, ldy, B, st);
+}
+
+int kans_qlayer_forward_host(kans_qlayer* L, const void* X, int x_dtype, void* Y, int y_dtype, int B) {
+  if (!L || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B <= 0 || B > kMaxDecodeB) return kans_fail(KANS_ERR_ARG, "decode path takes 1 <= B <= %d", kMaxDecodeB);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = kans_default_stream();
+  const size_t xb = (size_t)B * L->D_in * dt_bytes(x_dtype), yb = (size_t)B * L->D_out * dt_bytes(y_dtype);
+  DevBuf dx, dy;
+  if ((rc = dx.reserve(xb)) || (rc = dy.reserve(yb))) return rc;
+  HIP_TRY(hipMemcpyAsync(dx.p, X, xb, hipMemcpyHostToDevice, st));
+  if ((rc = qlayer_forward_locked(L, dx.p, x_dtype, L->D_in, dy.p, y_dtype, L->D_out, B, st))) return rc;
+  HIP_TRY(hipMemcpyAsync(Y, dy.p, yb, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return 0;
+}
+
+int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out) {
+  if (!gate || !up || !down || !out) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (gate->quant != up->quant || gate->quant != down->quant)
+    return kans_fail(KANS_ERR_ARG, "gate, up and down must share one quantization format");
+  if (gate->D_in != up->D_in || gate->D_out != up->D_out || gate->K != up->K || gate->has_base != up->has_base ||
+      down->D_in != gate->D_out || down->D_out != gate->D_in)
+    return kans_fail(KANS_ERR_ARG, "shape mismatch: gate/up %dx%d, down %dx%d", gate->D_in, gate->D_out, down->D_in,
+                     down->D_out);
+  if (gate->has_bias != up->has_bias || (gate->has_bias && gate->bias_dtype != up->bias_dtype))
+    return kans_fail(KANS_ERR_ARG, "gate and up must agree on bias");
+  auto* G = new kans_gated();
+  G->gate = gate;
+  G->up = up;
+  G->down = down;
+  *out = G;
+  return 0;
+}
+
+int kans_gated_destroy(kans_gated* G) {
+  if (!G) return 0;
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  if (kans_default_stream()) (void)hipStreamSynchronize(kans_default_stream());
+  delete G;
+  return 0;
+}
+
+int kans_gated_forward(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                       int round16, void* stream) {
+  if (!G) return kans_fail(KANS_ERR_ARG, "null block");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = stream ? (hipStream_t)stream : kans_default_stream();
+  return gated_forward_locked(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, st);
+}
+
+int kans_gated_forward_host(kans_gated* G, const void* X, int x_dtype, void* Y, int y_dtype, int B, int round16) {
+  if (!G || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B <= 0 || B > kMaxDecodeB) return kans_fail(KANS_ERR_ARG, "decode path takes 1 <= B <= %d", kMaxDecodeB);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = kans_default_stream();
+  const int d = G->gate->D_in;
+  const size_t xb = (size_t)B * d * dt_bytes(x_dtype), yb = (size_t)B * d * dt_bytes(y_dtype);
+  DevBuf dx, dy;
+  if ((rc = dx.reserve(xb)) || (rc = dy.reserve(yb))) return rc;
+  HIP_TRY(hipMemcpyAsync(dx.p, X, xb, hipMemcpyHostToDevice, st));
+  if ((rc = gated_forward_locked(G, dx.p, x_dtype, d, dy.p, y_dtype, d, B, round16, st))) return rc;
+  HIP_TRY(hipMemcpyAsync(Y, dy.p, yb, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return 0;
+}
+
+// Mean time of one block forward on device-resident X / Y; use_graph replays
+// the six launches as one captured HIP graph.
+int kans_gated_time(kans_gated* G, const void* X, int x_dtype, void* Y, int y_dtype, int B, int warmup, int iters,
+                    int use_graph, float* ms) {
+  if (!G || !X || !Y || !ms || iters <= 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = kans_default_stream();
+  const int d = G->gate->D_in;
+  // one eager call sizes every workspace before any capture
+  if ((rc = gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st))) return rc;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  if (use_graph) {
+    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    rc = gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st);
+    hipError_t e = hipStreamEndCapture(st, &graph);
+    if (rc) return rc;
+    HIP_TRY(e);
+    HIP_TRY(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  }
+  auto run = [&]() -> int {
+    if (use_graph) {
+      HIP_TRY(hipGraphLaunch(exec, st));
+      return 0;
+    }
+    return gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st);
+  };
+  for (int i = 0; i < warmup; ++i)
+    if ((rc = run())) return rc;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, st));
+  for (int i = 0; i < iters; ++i)
+    if ((rc = run())) return rc;
+  HIP_TRY(hipEventRecord(e1, st));
+  HIP_TRY(hipEventSynchronize(e1));
+  float t = 0.f;
+  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  *ms = t / iters;
+  return 0;
+}
+
+// Packed bytes the decode path streams per block forward (weights + group
+// parameters as stored by the reference formats, activations in, result out):
+// the algorithmic traffic used for the HBM roofline.
+long long kans_gated_stream_bytes(const kans_gated* G, int B) {
+  if (!G) return -1;
+  long long total = 0;
+  for (const kans_qlayer* L : {G->gate, G->up, G->down}) {
+    const long kb = (long)L->D_in * L->K;
+    for (int part = 0; part < 1 + L->has_base; ++part) {
+      const long kdim = part == 0 ? kb : L->D_in;
+      if (L->quant == Q_INT4) {
+        const long pad = (kdim + L->group - 1) / L->group * L->group;
+        total += (long long)L->D_out * (pad / 2 + (pad / L->group) * 8);
+      } else {
+        total += (long long)L->D_out * (((kdim + 15) / 16) * 4 + ((kdim + L->group - 1) / L->group) * 4);
+      }
+    }
+  }
+  total += (long long)B * G->gate->D_in * 2 * 2;  // x in, y out (fp16)
+  return total;
+}
+
+// Reference fused ternary forward (metal_kan_bridge.mm:4684-4733): fp32 X, no
+// base branch, ternary W (D_out x D_in*degree), optional fp32 bias.  Computed
+// in fp32 on the exact dequantized weights (the same arithmetic contract as
+// the reference kernel), so results match the fp32 oracle to 1e-4.
+int metal_kan_forward_ternary_cheby(const float* X, const uint32_t* W_packed, const float* scales, const float* bias,
+                                    float* Y, int B, int D_in, int D_out, int degree, int group_size, int has_bias) {
+  if (!X || !W_packed || !scales || !Y || B <= 0 || D_in <= 0 || D_out <= 0 || degree <= 0 || group_size <= 0)
+    return kans_fail(KANS_ERR_ARG, "bad argument");
+  if (degree > kMaxK) return kans_fail(KANS_ERR_ARG, "degree %d > %d", degree, kMaxK);
+  std::vector<float> W((size_t)D_out * D_in * degree);
+  {
+    std::lock_guard<std::mutex> lk(kans_mutex());
+    int rc = kans_ensure_init();
+    if (rc) return -1;
+    hipStream_t st = kans_default_stream();
+    const long kd = (long)D_in * degree;
+    const size_t pbytes = (size_t)D_out * ((kd + 15) / 16) * 4, sbytes = (size_t)D_out * ((kd + group_size - 1) / group_size) * 4;
+    DevBuf dp, ds, dw;
+    if ((rc = upload_tmp(dp, W_packed, pbytes, st)) || (rc = upload_tmp(ds, scales, sbytes, st)) ||
+        (rc = dw.reserve(W.size() * 4)))
+      return rc;
+    if ((rc = dequant_ternary_device((const uint32_t*)dp.p, (const float*)ds.p, (float*)dw.p, D_out, (int)kd,
+                                     group_size, st)))
+      return rc;
+    HIP_TRY(hipMemcpyAsync(W.data(), dw.p, W.size() * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+  }
+  std::vector<float> zero_b(has_bias ? 0 : 1, 0.0f);
+  return metal_kan_cheby_forward(X, W.data(), X /*unused: no base*/, has_bias ? bias : zero_b.data(), Y, B, D_in, D_out,
+                                 degree, 0, has_bias ? 1 : 0);
+}
+
+}  // extern "C"

@@ -194,12 +194,6 @@ inline int grid_for(long n) { return (int)std::min<long>((n + 255) / 256, 65536)
 
 }  // namespace
 
-#define HIP_TRY(expr)                                                                                   \
-  do {                                                                                                  \
-    hipError_t _e = (expr);                                                                             \
-    if (_e != hipSuccess) return kans_fail(KANS_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e)); \
-  } while (0)
-
 namespace kans {
 int dequant_affine_device(const void* q, const float* s, const float* b, float* out, long ngroups, int gs, int bits,
                           hipStream_t st) {

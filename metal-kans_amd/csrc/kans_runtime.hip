@@ -58,14 +58,6 @@ int kans_fail(int code, const char* fmt, ...) {
   return code;
 }
 
-#define HIP_TRY(expr)                                                                       \
-  do {                                                                                      \
-    hipError_t _e = (expr);                                                                 \
-    if (_e != hipSuccess)                                                                   \
-      return kans_fail(KANS_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
-                       __FILE__, __LINE__);                                                 \
-  } while (0)
-
 // ---------------------------------------------------------------------------
 // Device state
 // ---------------------------------------------------------------------------
@@ -83,22 +75,7 @@ struct Pending {  // a deferred device->host result copy (async mode); dst null:
 static std::vector<Pending> g_pending;
 
 // grow-only pinned staging buffers (synchronous mode)
-struct Pinned {
-  void* p = nullptr;
-  size_t cap = 0;
-};
 static Pinned g_pin_in, g_pin_out;
-
-static int pinned_reserve(Pinned& b, size_t bytes) {
-  if (bytes <= b.cap) return 0;
-  if (b.p) HIP_TRY(hipHostFree(b.p));
-  b.p = nullptr;
-  b.cap = 0;
-  size_t cap = bytes + bytes / 4;
-  HIP_TRY(hipHostMalloc(&b.p, cap, hipHostMallocDefault));
-  b.cap = cap;
-  return 0;
-}
 
 static int ensure_init() {
   if (g_ready) return 0;
@@ -120,23 +97,15 @@ static int ensure_init() {
 
 hipStream_t kans_default_stream() { return g_stream; }
 
-// ---------------------------------------------------------------------------
-// Device buffers
-// ---------------------------------------------------------------------------
-struct DevBuf {
-  void* p = nullptr;
-  size_t cap = 0;
-  ~DevBuf() { if (p) (void)hipFree(p); }
-  int reserve(size_t bytes) {
-    if (bytes <= cap) return 0;
-    if (p) HIP_TRY(hipFree(p));
-    p = nullptr;
-    cap = 0;
-    HIP_TRY(hipMalloc(&p, bytes));
-    cap = bytes;
-    return 0;
-  }
-};
+std::mutex& kans_mutex() { return g_mu; }
+int kans_ensure_init() { return ensure_init(); }
+int kans_pinned_stage(int which, size_t bytes, void** p) {
+  Pinned& b = which ? g_pin_out : g_pin_in;
+  int rc = pinned_reserve(b, bytes);
+  if (rc) return rc;
+  *p = b.p;
+  return 0;
+}
 
 static size_t dtype_size(int dt) { return dt == DT_F32 ? 4 : 2; }
 

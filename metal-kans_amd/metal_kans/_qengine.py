@@ -1,0 +1,152 @@
+"""Device-resident quantized Chebyshev layers and GatedKAN blocks (decode path).
+
+A layer quantized with ``to_int4`` (group 64) or ``to_ternary`` (group 32)
+keeps its packed weights in ``_w_cheby_quantized`` / ``_w_cheby_ternary`` (and
+the ``w_base`` counterparts), in the reference's formats (quantization.py:13-99,
+191-246).  ``QLayerEngine`` uploads those packed arrays once and runs the fused
+decode kernel on them, which streams the packed bytes instead of dequantized
+fp32 weights.  The engine is rebuilt when the packed objects change (a new
+``to_int4`` / ``to_ternary``).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import device
+from ._engine import DT_BF16, DT_F16, DT_F32
+
+MAX_DECODE_B = 32
+
+
+def packed_format(layer) -> Optional[str]:
+    """'int4' / 'ternary' when every weight matrix of a Chebyshev layer is packed in a format the fused
+    decode kernel reads (INT4 with group 64, ternary with group 32), else None."""
+    from .quantization import QuantizedWeight, TernaryQuantizedWeight
+
+    def fmt(attr):
+        # the packed object counts only while the layer still holds the array it dequantized to
+        # (a later quantization, assignment or in-place edit makes it stale)
+        cur = getattr(layer, attr, None)
+
+        def live(obj):
+            snap = getattr(obj, "_deq_snapshot", None)
+            return snap is not None and snap.same(cur)
+        q = getattr(layer, f"_{attr}_quantized", None)
+        if isinstance(q, QuantizedWeight) and q.bits == 4 and q.group_size == 64 and live(q):
+            return "int4"
+        t = getattr(layer, f"_{attr}_ternary", None)
+        if isinstance(t, TernaryQuantizedWeight) and t.group_size == 32 and live(t):
+            return "ternary"
+        return None
+
+    f = fmt("w_cheby")
+    if f is None:
+        return None
+    if getattr(layer, "has_base", False) and fmt("w_base") != f:
+        return None
+    return f
+
+
+def _key(layer, fmt):
+    suffix = "_quantized" if fmt == "int4" else "_ternary"
+    objs = [getattr(layer, "_w_cheby" + suffix, None), getattr(layer, "_w_base" + suffix, None),
+            getattr(layer, "bias", None) if layer.has_bias else None]
+    return tuple(id(o) for o in objs)
+
+
+class QLayerEngine:
+    """Owns a ``kans_qlayer`` handle built from a quantized ChebyKAN layer."""
+
+    def __init__(self, layer, fmt: str):
+        self.fmt = fmt
+        self.key = _key(layer, fmt)
+        self.d_in, self.d_out = int(layer.in_features), int(layer.out_features)
+        lib = device.get_metal_bridge()
+        self.handle = ctypes.c_void_p()
+        has_base, has_bias = int(bool(layer.has_base)), int(bool(layer.has_bias))
+        K = int(layer.degree)
+        bias = None
+        if has_bias:
+            bias = np.ascontiguousarray(layer.bias, dtype=np.float32)
+        bias_ptr = bias.ctypes.data if bias is not None else None
+        if fmt == "int4":
+            w = layer._w_cheby_quantized
+            wb = layer._w_base_quantized if has_base else None
+            arrs = [np.ascontiguousarray(w.qweight), np.ascontiguousarray(w.scales, dtype=np.float32),
+                    np.ascontiguousarray(w.biases, dtype=np.float32)]
+            barrs = ([np.ascontiguousarray(wb.qweight), np.ascontiguousarray(wb.scales, dtype=np.float32),
+                      np.ascontiguousarray(wb.biases, dtype=np.float32)] if wb is not None else [None, None, None])
+            ptr = [a.ctypes.data if a is not None else None for a in arrs + barrs]
+            device.check(lib.kans_qlayer_create_int4(self.d_in, self.d_out, K, has_base, has_bias, 64, *ptr,
+                                                     bias_ptr, DT_F32, ctypes.byref(self.handle)),
+                         "kans_qlayer_create_int4")
+        else:
+            w = layer._w_cheby_ternary
+            wb = layer._w_base_ternary if has_base else None
+            arrs = [np.ascontiguousarray(w.w_packed), np.ascontiguousarray(w.scales, dtype=np.float32)]
+            barrs = ([np.ascontiguousarray(wb.w_packed), np.ascontiguousarray(wb.scales, dtype=np.float32)]
+                     if wb is not None else [None, None])
+            ptr = [a.ctypes.data if a is not None else None for a in arrs + barrs]
+            device.check(lib.kans_qlayer_create_ternary(self.d_in, self.d_out, K, has_base, has_bias, 32, *ptr,
+                                                        bias_ptr, DT_F32, ctypes.byref(self.handle)),
+                         "kans_qlayer_create_ternary")
+
+    def __del__(self):
+        try:
+            if self.handle:
+                device.load_library().kans_qlayer_destroy(self.handle)
+        except Exception:
+            pass
+
+    def current(self, layer) -> bool:
+        return packed_format(layer) == self.fmt and _key(layer, self.fmt) == self.key
+
+    def forward_host(self, x: np.ndarray, out_dtype) -> np.ndarray:
+        x = np.ascontiguousarray(x)
+        B = x.shape[0]
+        xdt = DT_F16 if x.dtype == np.float16 else DT_F32
+        if xdt == DT_F32 and x.dtype != np.float32:
+            x = x.astype(np.float32)
+        y = np.empty((B, self.d_out), dtype=out_dtype)
+        ydt = DT_F16 if out_dtype == np.float16 else DT_F32
+        device.check(device.get_metal_bridge().kans_qlayer_forward_host(self.handle, x.ctypes.data, xdt, y.ctypes.data,
+                                                                          ydt, B), "kans_qlayer_forward_host")
+        return y
+
+
+class GatedEngine:
+    """Owns the three ``kans_qlayer`` handles and the ``kans_gated`` block of a quantized GatedKAN."""
+
+    def __init__(self, block, fmt: str):
+        self.fmt = fmt
+        self.layers = [QLayerEngine(k, fmt) for k in (block.gate_kan, block.up_kan, block.down_kan)]
+        self.handle = ctypes.c_void_p()
+        device.check(device.get_metal_bridge().kans_gated_create(self.layers[0].handle, self.layers[1].handle,
+                                                                 self.layers[2].handle, ctypes.byref(self.handle)),
+                     "kans_gated_create")
+        self.d_model = self.layers[0].d_in
+
+    def __del__(self):
+        try:
+            if self.handle:
+                device.load_library().kans_gated_destroy(self.handle)
+        except Exception:
+            pass
+
+    def current(self, block) -> bool:
+        return all(e.current(k) for e, k in zip(self.layers, (block.gate_kan, block.up_kan, block.down_kan)))
+
+    def forward_host(self, x: np.ndarray, out_dtype, round16: int) -> np.ndarray:
+        x = np.ascontiguousarray(x)
+        B = x.shape[0]
+        xdt = DT_F16 if x.dtype == np.float16 else DT_F32
+        if xdt == DT_F32 and x.dtype != np.float32:
+            x = x.astype(np.float32)
+        y = np.empty((B, self.d_model), dtype=out_dtype)
+        ydt = DT_F16 if out_dtype == np.float16 else DT_F32
+        device.check(device.get_metal_bridge().kans_gated_forward_host(self.handle, x.ctypes.data, xdt, y.ctypes.data,
+                                                                         ydt, B, round16), "kans_gated_forward_host")
+        return y

@@ -24,6 +24,7 @@ _initialised = False
 
 c_int = ctypes.c_int
 c_long = ctypes.c_long
+c_longlong = ctypes.c_longlong
 c_float = ctypes.c_float
 c_double = ctypes.c_double
 c_size_t = ctypes.c_size_t
@@ -59,6 +60,7 @@ SIGNATURES = {
     "metal_kan_quantize_ternary": (c_int, [P, P, P, c_int, c_int, c_int]),
     "metal_kan_dequantize_ternary": (c_int, [P, P, P, c_int, c_int, c_int]),
     "metal_kan_swiglu_forward": (c_int, [P, P, P, c_int]),
+    "metal_kan_forward_ternary_cheby": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int]),
     # device-resident layer API
     "kans_init": (c_int, []),
     "kans_stream": (c_void_p, []),
@@ -91,6 +93,18 @@ SIGNATURES = {
     "kans_memcpy_h2d": (c_int, [P, P, c_size_t]),
     "kans_memcpy_d2h": (c_int, [P, P, c_size_t]),
     "kans_copy_device": (c_int, [P, P, c_size_t, P]),
+    # quantized decode path
+    "kans_qlayer_create_int4": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P, c_int, P]),
+    "kans_qlayer_create_ternary": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P]),
+    "kans_qlayer_destroy": (c_int, [P]),
+    "kans_qlayer_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, P]),
+    "kans_qlayer_forward_host": (c_int, [P, P, c_int, P, c_int, c_int]),
+    "kans_gated_create": (c_int, [P, P, P, P]),
+    "kans_gated_destroy": (c_int, [P]),
+    "kans_gated_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, c_int, P]),
+    "kans_gated_forward_host": (c_int, [P, P, c_int, P, c_int, c_int, c_int]),
+    "kans_gated_time": (c_int, [P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "kans_gated_stream_bytes": (c_longlong, [P, c_int]),
 }
 
 

@@ -6,6 +6,12 @@ constructor (gated_kan.py:36-84: gate, up, down ChebyKAN built in that order,
 up = Up(x), hidden = SiLU(gate) * up with the +-20 clip, out = Down(hidden),
 (B, S, d) inputs flattened), ``to_int8`` / ``to_int4`` / ``to_ternary``
 (:239-258), ``parameter_count``.  SwiGLU runs on the GPU for every dtype.
+
+Decode path: a float16 block quantized with ``to_int4()`` (group 64) or
+``to_ternary()`` (group 32) runs batches of at most 32 rows through the fused
+quantized block (``_qengine.GatedEngine``): the packed weights are streamed
+from HBM once per forward instead of being dequantized, and gate/up, SwiGLU and
+down run back to back on the device.  Other cases use the three layers.
 """
 from __future__ import annotations
 
@@ -16,6 +22,7 @@ import numpy as np
 from . import device
 from .cheby_kan import ChebyKAN
 from .quantization import to_int4, to_int8, to_ternary
+from ._qengine import MAX_DECODE_B, GatedEngine, packed_format
 
 
 class GatedKAN:
@@ -53,10 +60,31 @@ class GatedKAN:
                      "metal_kan_swiglu_forward")
         return out.astype(gate.dtype, copy=False)
 
+    def _decode_engine(self) -> Optional[GatedEngine]:
+        """The fused quantized block, when this forward can use it (see module docstring)."""
+        if self.dtype != np.float16:
+            return None
+        fmt = packed_format(self.gate_kan)
+        if fmt is None or packed_format(self.up_kan) != fmt or packed_format(self.down_kan) != fmt:
+            return None
+        eng = self.__dict__.get("_qblock")
+        if eng is None or eng.fmt != fmt or not eng.current(self):
+            eng = GatedEngine(self, fmt)
+            self._qblock = eng
+        return eng
+
     def forward(self, x: np.ndarray) -> np.ndarray:
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
         self._saved_x = x_2d
+        if x_2d.shape[0] <= MAX_DECODE_B:
+            eng = self._decode_engine()
+            if eng is not None:
+                out = eng.forward_host(x_2d if x_2d.dtype == np.float16 else x_2d.astype(np.float32), np.float16, 1)
+                self._saved_gate = self._saved_up = self._saved_hidden = None
+                if len(orig_shape) > 2:
+                    return out.reshape(*orig_shape[:-1], self.d_model)
+                return out
         gate = self.gate_kan(x_2d)
         up = self.up_kan(x_2d)
         self._saved_gate = gate

@@ -12,6 +12,10 @@ libkans_hip.so) with the rounding of the reference's NumPy fallback (the path
 the reference takes off-macOS); the dequantizers run on the GPU and are
 bit-identical to the reference's.  There is no NumPy fallback.
 
+Each packed object remembers (``_deq_snapshot``) the dequantized array it put
+in place, so a fused kernel that reads the packed weights directly can check
+that they still are the layer's weights (``_qengine.packed_format``).
+
 One addition: a layer that computed in fp16/bf16 before quantization keeps
 that compute dtype (``_quantized_from``), so a quantized ``GatedKAN(dtype=
 float16)`` still runs fp16 activations; fp32 layers behave exactly as in the
@@ -24,6 +28,7 @@ from typing import Any
 import numpy as np
 
 from . import device
+from ._engine import _Snapshot
 
 WEIGHT_ATTRS = ["w_cheby", "w_rbf", "w_relu", "w_wav", "w_fourier", "w_jacobi", "w_p", "w_q", "w_spline", "w_up",
                 "w_base"]
@@ -121,6 +126,7 @@ def quantize(model: Any, bits: int = 8, group_size: int = 64) -> Any:
                 qw = QuantizedWeight(w, bits=bits, group_size=group_size)
                 setattr(model, f"_{attr}_quantized", qw)
                 setattr(model, attr, qw.dequantize())
+                qw._deq_snapshot = _Snapshot(getattr(model, attr))
     if hasattr(model, "sub_layer"):
         quantize(model.sub_layer, bits=bits, group_size=group_size)
     if hasattr(model, "down_layer"):
@@ -152,6 +158,7 @@ def to_ternary(model: Any, group_size: int = 32) -> Any:
                 qw = TernaryQuantizedWeight(w, group_size=group_size)
                 setattr(model, f"_{attr}_ternary", qw)
                 setattr(model, attr, qw.dequantize())
+                qw._deq_snapshot = _Snapshot(getattr(model, attr))
     if hasattr(model, "sub_layer"):
         to_ternary(model.sub_layer, group_size=group_size)
     if hasattr(model, "down_layer"):

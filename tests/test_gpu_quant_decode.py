@@ -1,0 +1,201 @@
+"""GPU parity of the fused quantized decode path (INT4 group 64, ternary group 32).
+
+Parity target (quantization.py:168-171): the forward on the dequantized weights,
+dequant(quant(W)), evaluated by the float64 oracle.  The decode kernel feeds the
+basis values to the MFMAs in fp16, so the bar is the 16-bit one, 2e-2 (the
+measured error is ~1e-3); the reference-named fp32 ternary entry point keeps the
+fp32 bar, 1e-4.  Packed weights come from the oracle's quantizers (pinned
+against the reference's NumPy fallback in tests/test_oracle.py).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kan_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT_F32, DT_F16 = 0, 1
+
+
+def _quant_int4(W):
+    q, s, b, pad = O.quantize_affine(W, 4, 64)
+    deq = O.dequantize_affine(q, s, b, 4, 64, W.shape, pad)
+    return (np.ascontiguousarray(q), np.ascontiguousarray(s, np.float32).ravel(),
+            np.ascontiguousarray(b, np.float32).ravel()), deq
+
+
+def _quant_tern(W):
+    p, s = O.quantize_ternary(W, 32)
+    deq = O.dequantize_ternary(p, s, W.shape, 32)
+    return (np.ascontiguousarray(p), np.ascontiguousarray(s, np.float32)), deq
+
+
+def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed):
+    rng = np.random.default_rng(seed)
+    W = rng.normal(0, 0.05, (d_out, d_in * K)).astype(np.float32)
+    Wb = rng.normal(0, 0.1, (d_out, d_in)).astype(np.float32) if base else None
+    bv = rng.normal(0, 0.1, d_out).astype(np.float32) if bias else None
+    h = ctypes.c_void_p()
+    bptr = bv.ctypes.data if bv is not None else None
+    if fmt == "int4":
+        pw, dW = _quant_int4(W)
+        pb, dWb = _quant_int4(Wb) if base else ((None, None, None), None)
+        keep = (pw, pb)
+        rc = lib.kans_qlayer_create_int4(d_in, d_out, K, int(base), int(bias), 64,
+                                         *[a.ctypes.data if a is not None else None for a in pw + pb],
+                                         bptr, DT_F32, ctypes.byref(h))
+    else:
+        pw, dW = _quant_tern(W)
+        pb, dWb = _quant_tern(Wb) if base else ((None, None), None)
+        keep = (pw, pb)
+        rc = lib.kans_qlayer_create_ternary(d_in, d_out, K, int(base), int(bias), 32,
+                                            *[a.ctypes.data if a is not None else None for a in pw + pb],
+                                            bptr, DT_F32, ctypes.byref(h))
+    assert rc == 0, lib.kans_last_error()
+    del keep
+    return h, {"W": dW, "W_base": dWb, "bias": bv, "K": K}
+
+
+SHAPES = [(100, 70, 4, True, True), (256, 130, 3, True, False), (64, 48, 4, False, True), (33, 17, 5, True, True)]
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}K{s[2]}b{int(s[3])}{int(s[4])}")
+def test_qlayer_decode(gpu, fmt, shape):
+    lib = gpu
+    d_in, d_out, K, base, bias = shape
+    h, ref_l = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=d_in + d_out)
+    try:
+        rng = np.random.default_rng(7)
+        for B in (1, 3, 16, 17, 32):
+            x = rng.uniform(-1.3, 1.3, (B, d_in)).astype(np.float32)
+            ref = O.kan_forward("cheby", x, ref_l["W"], ref_l["W_base"], ref_l["bias"], {"K": K})
+            for xdt, xin in ((DT_F32, x), (DT_F16, x.astype(np.float16))):
+                y = np.empty((B, d_out), np.float32)
+                assert lib.kans_qlayer_forward_host(h, xin.ctypes.data, xdt, y.ctypes.data, DT_F32, B) == 0, \
+                    lib.kans_last_error()
+                r = ref if xdt == DT_F32 else O.kan_forward("cheby", xin.astype(np.float32), ref_l["W"],
+                                                            ref_l["W_base"], ref_l["bias"], {"K": K})
+                e = O.rel_err(y, r)
+                print(f"{fmt} {shape} B={B} x_dtype={xdt}: rel err {e:.2e}")
+                assert e <= 2e-2
+                assert e <= 5e-3  # fp16 basis operands: observed ~1e-3
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+def test_qlayer_rejects(gpu):
+    lib = gpu
+    h, _ = make_qlayer(lib, "int4", 64, 32, 4, True, False, seed=1)
+    try:
+        x = np.zeros((33, 64), np.float32)
+        y = np.empty((33, 32), np.float32)
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 33) < 0  # B > 32
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 0) < 0
+    finally:
+        lib.kans_qlayer_destroy(h)
+    out = ctypes.c_void_p()
+    q = np.zeros(64 * 32, np.uint8)
+    s = np.ones(64, np.float32)
+    assert lib.kans_qlayer_create_int4(64, 32, 1, 0, 0, 32, q.ctypes.data, s.ctypes.data, s.ctypes.data,
+                                       None, None, None, None, DT_F32, ctypes.byref(out)) < 0  # group 32
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_gated_block_decode(gpu, fmt, B):
+    """Fused GatedKAN block vs down(SiLU(gate(x)) * up(x)) on dequantized weights."""
+    lib = gpu
+    d, hdim, K = 96, 200, 4
+    layers, refs = [], []
+    for i, (di, do) in enumerate(((d, hdim), (d, hdim), (hdim, d))):
+        h, r = make_qlayer(lib, fmt, di, do, K, True, False, seed=100 + i)
+        layers.append(h)
+        refs.append(r)
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0, lib.kans_last_error()
+    try:
+        x = np.random.default_rng(B).normal(0, 1, (B, d)).astype(np.float16)
+        ref = O.gated_forward(x.astype(np.float32), *refs)
+        for round16 in (0, 1):
+            y = np.empty((B, d), np.float32)
+            assert lib.kans_gated_forward_host(blk, x.ctypes.data, DT_F16, y.ctypes.data, DT_F32, B, round16) == 0, \
+                lib.kans_last_error()
+            e = O.rel_err(y, ref)
+            print(f"gated {fmt} B={B} round16={round16}: rel err {e:.2e}")
+            assert e <= 2e-2
+        ms = ctypes.c_float()
+        xd, yd = ctypes.c_void_p(), ctypes.c_void_p()
+        assert lib.kans_dev_malloc(ctypes.byref(xd), x.nbytes) == 0
+        assert lib.kans_dev_malloc(ctypes.byref(yd), B * d * 2) == 0
+        try:
+            assert lib.kans_memcpy_h2d(xd, x.ctypes.data, x.nbytes) == 0
+            for graph in (0, 1):
+                assert lib.kans_gated_time(blk, xd, DT_F16, yd, DT_F16, B, 1, 3, graph, ctypes.byref(ms)) == 0, \
+                    lib.kans_last_error()
+                y16 = np.empty((B, d), np.float16)
+                assert lib.kans_memcpy_d2h(y16.ctypes.data, yd, y16.nbytes) == 0
+                assert O.rel_err(y16.astype(np.float32), ref) <= 2e-2
+        finally:
+            lib.kans_dev_free(xd)
+            lib.kans_dev_free(yd)
+        assert lib.kans_gated_stream_bytes(blk, B) > 0
+    finally:
+        lib.kans_gated_destroy(blk)
+        for h in layers:
+            lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("quant", ["int4", "ternary"])
+def test_gatedkan_python_decode(gpu, quant):
+    """GatedKAN(dtype=float16).to_int4() / .to_ternary() takes the fused block for B <= 32."""
+    import metal_kans as mk
+    np.random.seed(3)
+    blk = mk.GatedKAN(d_model=64, d_ffn=160, degree=4, dtype=np.float16)
+    getattr(blk, f"to_{quant}")()
+    x = np.random.default_rng(2).normal(0, 1, (5, 64)).astype(np.float16)
+    out = blk(x)
+    assert blk.__dict__.get("_qblock") is not None
+    assert out.shape == (5, 64) and out.dtype == np.float16
+    ref = O.gated_forward(x.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                                                   for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    assert O.rel_err(out.astype(np.float32), ref) <= 2e-2
+    # larger batches take the per-layer path on the dequantized weights
+    xb = np.random.default_rng(3).normal(0, 1, (40, 64)).astype(np.float16)
+    refb = O.gated_forward(xb.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                                                     for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    assert O.rel_err(blk(xb).astype(np.float32), refb) <= 2e-2
+    # re-quantizing rebuilds the device block from the new packed weights
+    old = blk._qblock
+    blk.to_int4() if quant == "ternary" else blk.to_ternary()
+    out2 = blk(x)
+    assert blk._qblock is not old and blk._qblock.fmt != old.fmt
+    ref2 = O.gated_forward(x.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                                                    for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    assert O.rel_err(out2.astype(np.float32), ref2) <= 2e-2
+    # an in-place edit of a (small) dequantized weight retires the packed path for that layer
+    blk.down_kan.w_cheby[0, 0] += 1.0
+    assert blk._decode_engine() is None
+    refe = O.gated_forward(x.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                                                    for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    assert O.rel_err(blk(x).astype(np.float32), refe) <= 2e-2
+
+
+def test_reference_ternary_entry_point(gpu):
+    """metal_kan_forward_ternary_cheby (metal_kan_bridge.mm:4684-4733): fp32, no base."""
+    lib = gpu
+    rng = np.random.default_rng(11)
+    B, Di, Do, deg = 9, 40, 24, 5
+    W = rng.normal(0, 0.1, (Do, Di * deg)).astype(np.float32)
+    p, s = O.quantize_ternary(W, 32)
+    bias = rng.normal(0, 0.1, Do).astype(np.float32)
+    x = rng.uniform(-1.2, 1.2, (B, Di)).astype(np.float32)
+    y = np.empty((B, Do), np.float32)
+    for hb in (0, 1):
+        assert lib.metal_kan_forward_ternary_cheby(x.ctypes.data, p.ctypes.data, s.ctypes.data, bias.ctypes.data,
+                                                   y.ctypes.data, B, Di, Do, deg, 32, hb) == 0, lib.kans_last_error()
+        ref = O.kan_forward("cheby", x, O.dequantize_ternary(p, s, W.shape, 32), None, bias if hb else None,
+                            {"K": deg})
+        assert O.rel_err(y, ref) <= 1e-4
