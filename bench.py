@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the fused KAN layer forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--quick]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 100] [--quick] [--only cfg5,...]
 
 Prints ONE JSON line.  A "step" is one fused forward over one batch with the
 inputs already resident in HBM.  The headline workload is BASELINE config 3
@@ -30,6 +30,13 @@ sys.path.insert(0, os.path.join(ROOT, "metal-kans_amd"))
 sys.path.insert(0, ROOT)
 
 PEAK = {"f16": 2516.6, "bf16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s (MI355X datasheet)
+# Committed summary of the headline kernel's two
+# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) scaled by a copy-kernel
+# calibration: the source of roofline.traffic (PMC counters cannot be read
+# from inside the timed process).
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_kan_fused_dense_cfg3_fastkan_fp16.txt")
+SECONDARY = ("ns_cheby_fp16", "ns_bspline_fp16", "cfg4_bspline_bf16", "cfg4_bspline_fp32", "cfg1_cheby_fp32",
+             "cfg2", "cfg5")
 HBM_PEAK_GBS = 8000.0
 METRIC = "fused KAN fwd TFLOP/s + % MFMA peak; quantized-weight HBM GB/s (1 MI355X)"
 
@@ -136,6 +143,23 @@ def run_layer_workload(lib, mk, name, kind, B, d_in, d_out, K, dtype, seed, x_fn
     return out, state
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed PMC summary (``key: value`` lines), or None
+    when the summary is missing or was measured on another kernel."""
+    try:
+        kv = {}
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                k, sep, v = line.partition(":")
+                if sep and not line.startswith((" ", "#", "|")):
+                    kv[k.strip()] = v.strip()
+        if kv.get("kernel") != kernel:
+            return None
+        return int(float(kv["traffic_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline_cfg3(x, L, budget_s=12.0):
     """Oracle fp32 four-stage forward (reference stage order) on a row sample of cfg 3."""
     from oracle import kan_oracle as O
@@ -216,16 +240,116 @@ def run_chain_cfg2(lib, mk, warmup, iters):
     return out
 
 
+def _quantized_layer(lib, fmt, W, Wb, K):
+    """kans_qlayer from a float32 (W, W_base) pair packed in the reference format (native quantizers)."""
+    d_out, d_in = Wb.shape
+    h = ctypes.c_void_p()
+    if fmt == "int4":
+        arrs = []
+        for A in (W, Wb):
+            ng = A.size // 64
+            q = np.empty((ng, 32), np.uint8)
+            s_ = np.empty(ng, np.float32)
+            b_ = np.empty(ng, np.float32)
+            assert lib.metal_kan_quantize_int4(A.ctypes.data, q.ctypes.data, s_.ctypes.data, b_.ctypes.data, ng, 64) == 0
+            arrs += [q, s_, b_]
+        rc = lib.kans_qlayer_create_int4(d_in, d_out, K, 1, 0, 64, *[a.ctypes.data for a in arrs], None, 0,
+                                         ctypes.byref(h))
+    else:
+        arrs = []
+        for A in (W, Wb):
+            kd = A.shape[1]
+            p_ = np.zeros((A.shape[0], (kd + 15) // 16), np.uint32)
+            s_ = np.zeros((A.shape[0], (kd + 31) // 32), np.float32)
+            assert lib.metal_kan_quantize_ternary(A.ctypes.data, p_.ctypes.data, s_.ctypes.data, A.shape[0], kd, 32) == 0
+            arrs += [p_, s_]
+        rc = lib.kans_qlayer_create_ternary(d_in, d_out, K, 1, 0, 32, *[a.ctypes.data for a in arrs], None, 0,
+                                            ctypes.byref(h))
+    if rc:
+        raise RuntimeError(lib.kans_last_error().decode())
+    return h
+
+
+def run_cfg5(lib, warmup, iters):
+    """GatedKAN d=4096, h=11008, K=4 (base on, no bias), all six weight matrices
+    ~N(0, 0.02) then INT4 (group 64) or ternary (group 32); x ~ N(0,1) fp16.  Decode B in {1, 32}
+    through the fused quantized block (one HIP graph, packed weights streamed from HBM): GB/s =
+    algorithmic bytes (packed codes + group parameters + x + y) / time.  Prefill B = 8192 through the
+    per-layer fused kernel on the dequantized weights (fp16): TFLOP/s."""
+    d, hdim, K = 4096, 11008, 4
+    rng = np.random.default_rng(1005)
+    t0 = time.perf_counter()
+    xs = {B: rng.standard_normal((B, d), dtype=np.float32).astype(np.float16) for B in (1, 32)}
+    mats = []
+    for (di, do) in ((d, hdim), (d, hdim), (hdim, d)):
+        W = rng.standard_normal((do, di * K), dtype=np.float32) * np.float32(0.02)
+        Wb = rng.standard_normal((do, di), dtype=np.float32) * np.float32(0.02)
+        mats.append((W, Wb))
+    out = {}
+    for fmt in ("int4", "ternary"):
+        layers = [_quantized_layer(lib, fmt, W, Wb, K) for (W, Wb) in mats]
+        blk = ctypes.c_void_p()
+        assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0
+        for B, x in xs.items():
+            xd, yd = DevBuf(lib, x.nbytes), DevBuf(lib, x.nbytes)
+            xd.upload(x)
+            ms = ctypes.c_float()
+            rc = lib.kans_gated_time(blk, xd.p, 1, yd.p, 1, B, warmup, iters, 1, ctypes.byref(ms))
+            if rc:
+                raise RuntimeError(lib.kans_last_error().decode())
+            nbytes = lib.kans_gated_stream_bytes(blk, B)
+            gbs = nbytes / ms.value / 1e6
+            out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
+                                              "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                              "bytes": int(nbytes), "batch": B}
+            xd.free()
+            yd.free()
+        lib.kans_gated_destroy(blk)
+        for hnd in layers:
+            lib.kans_qlayer_destroy(hnd)
+    # prefill: per-layer fused fp16 kernel on the INT4-dequantized weights
+    B = 8192
+    import metal_kans as mk
+    tot_ms, flops = 0.0, 0.0
+    for i, (W, Wb) in enumerate(mats):
+        do, di = Wb.shape
+        L = mk.ChebyKAN(di, do, degree=K, bias=False)
+        L.w_cheby, L.w_base = W, Wb
+        mk.to_int4(L)
+        L.half()
+        eng = L._engine()
+        from metal_kans._engine import DT_F16
+        eng.prepare(DT_F16, L.w_cheby, L.w_base, None, ())
+        xd, yd = DevBuf(lib, B * di * 2), DevBuf(lib, B * do * 2)
+        xd.upload(rng.standard_normal((B, di), dtype=np.float32).astype(np.float16))
+        tot_ms += time_layer(lib, eng, xd, yd, B, di, do, warmup, iters)
+        flops += 2.0 * B * do * di * (K + 1)
+        xd.free()
+        yd.free()
+        del L, eng
+    out["cfg5_int4_prefill_b8192"] = {"ms_three_layers": round(tot_ms, 4), "tflops": round(flops / tot_ms / 1e9, 2),
+                                      "frac_mfma_peak": round(flops / tot_ms / 1e9 / PEAK["f16"], 4),
+                                      "path": "per-layer fused fp16 kernel on dequantized INT4 weights"}
+    log(f"[bench] cfg5 ({time.perf_counter() - t0:.1f} s): {out}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary workloads / CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", metavar="NAMES",
+                    help="comma-separated secondary workloads to run (default all): " + ",".join(SECONDARY))
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run kans_copy_device over MIB MiB, 5 times (byte-counter calibration)")
     a = ap.parse_args()
+    only = set(filter(None, a.only.split(",")))
+    if only - set(SECONDARY):
+        ap.error(f"unknown workloads {sorted(only - set(SECONDARY))}")
+    want = lambda name: not only or name in only  # noqa: E731
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only (the fused KAN forward is single-GPU; "
                                    "multi-GPU sharding is a design note, see DESIGN.md)", "n_gpus": a.gpus}))
@@ -252,6 +376,11 @@ def main():
                                   steps=iters)
     F = st["flops"]
     wall_ms = st["wall_ms"]
+    # RBF layers always take the per-slot kernel; its tile is the library's choice for this batch
+    tile = [ctypes.c_int() for _ in range(3)]
+    assert lib.kans_layer_describe(st["eng"].handle, 16384, *[ctypes.byref(v) for v in tile]) == 0
+    head_kernel = (f"kans::kan_fused_dense<_Float16, _Float16, _Float16, BASIS_RBF, {tile[0].value}, "
+                   f"{tile[1].value}>" + (f" x {tile[2].value} feature splits" if tile[2].value > 1 else ""))
     value = F / wall_ms / 1e9
     kernel_ms = head["ms"]
     achieved = F / kernel_ms / 1e9
@@ -273,9 +402,8 @@ def main():
                    "batch": 16384, "d_in": 1024, "d_out": 1024, "K": 8, "has_base": 1,
                    "flops_per_step": F},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["f16"], "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK["f16"], 4), "traffic": None,
-                     "kernel": "kans::kan_fused_dense<_Float16, BASIS_RBF, 64, 4>",
-                     "kernel_ms": kernel_ms},
+                     "frac": round(achieved / PEAK["f16"], 4), "traffic": measured_traffic(head_kernel),
+                     "traffic_unit": "bytes per launch", "kernel": head_kernel, "kernel_ms": kernel_ms},
     }
     workloads = {"cfg3_fastkan_fp16": head}
     if not a.quick:
@@ -287,12 +415,17 @@ def main():
             ("cfg4_bspline_fp32", "bspline", 8192, 1024, 4096, 8, "f32", 1004, unif(-1.2, 1.2), np.sqrt(1 / (1024 * 8))),
             ("cfg1_cheby_fp32", "cheby", 256, 64, 64, 9, "f32", 1001, lambda rng, B, d: np.tanh(rng.uniform(-1, 1, (B, d))).astype(np.float32), np.sqrt(1 / (64 * 9))),
         ]:
+            if not want(name):
+                continue
             out, s2 = run_layer_workload(lib, mk, name, kind, B, di, do, K, dt, seed, xf, ws, a.warmup, iters)
             workloads[name] = out
             s2["xd"].free()
             s2["yd"].free()
             del s2
-        workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters)
+        if want("cfg2"):
+            workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters)
+        if want("cfg5"):
+            workloads.update(run_cfg5(lib, a.warmup, iters))
     result["workloads"] = workloads
     if not (a.quick or a.no_cpu):
         result["cpu_baseline"] = cpu_baseline_cfg3(st["x"], st["L"])

@@ -167,7 +167,7 @@ int kans_layer_destroy(kans_layer* layer);
 /* RBF: K centres (fp32) and 1/(2h^2); B-spline: G (K = G + 3), grid_min, inv_h */
 int kans_layer_set_rbf(kans_layer* layer, const float* centers, float inv_denominator);
 int kans_layer_set_bspline(kans_layer* layer, int grid_size, float grid_min, float inv_h);
-/* tiling override for tuning: (wm, nb) in {(64,4),(32,4),(32,1)} or (0,0) = automatic; splits >= 0 */
+/* tiling override for tuning: (wm, nb) in {(64,4),(32,8),(32,4),(32,1)} or (0,0) = automatic; splits >= 0 */
 int kans_layer_set_tiling(kans_layer* layer, int wm, int nb, int splits);
 int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
 /* weights in the layer dtype: W [D_out][D_in*K] (k fastest), W_base [D_out][D_in], bias [D_out] */

@@ -16,9 +16,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 enum Basis { BASIS_CHEBY = 0, BASIS_RBF = 1, BASIS_BSPLINE = 2 };
-// Kernel-only basis id: Gaussian RBF on uniformly spaced centres (see
-// BasisGen<BASIS_RBF_UNIFORM>); the public API never sees it.
-constexpr int BASIS_RBF_UNIFORM = 3;
 enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -33,14 +30,12 @@ struct BasisParams {
   float inv_h;        // B-spline: G / (max - min)
   float neg_l;        // RBF: -inv_den * log2(e)
   int have_centers;   // RBF: centres set
-  int rbf_uniform;    // RBF: centres are c_0 + k*h (to 1e-6 relative)
   float rbf_s;        // RBF: sqrt(-neg_l), so phi_k = exp2(-(s*x - s*c_k)^2)
-  float rbf_sc0;      // RBF: s * c_0
-  float rbf_sh;       // RBF: s * h
-  // RBF centres c_k, by value: the kernels read them with scalar loads from the
-  // argument segment, which do not wait on the vector-memory counter that the
-  // weight / input prefetch uses.
-  float centers[kMaxK];
+  float centers[kMaxK];  // RBF centres c_k (host copy)
+  // RBF scaled centres s * c_k, by value: the kernels read them with scalar
+  // loads from the argument segment, which do not wait on the vector-memory
+  // counter that the weight / input prefetch uses.
+  float rbf_sc[kMaxK];
 };
 
 // ---------------------------------------------------------------------------
@@ -135,8 +130,10 @@ template <int NV> struct BasisGen<BASIS_CHEBY, NV> {
   }
 };
 
-// Gaussian RBF exp(-(x - c_k)^2 * inv_den) = exp2(neg_l * (x - c_k)^2)
-// (reference: fused_kan.metal:140-166, fast_kan.py:40-42).
+// Gaussian RBF exp(-(x - c_k)^2 * inv_den) = exp2(-(s*x - s*c_k)^2) with
+// s = sqrt(inv_den * log2(e)) (reference: fused_kan.metal:140-166,
+// fast_kan.py:40-42): one fma, one multiply and one exp2 per value; s*c_k
+// comes precomputed in BasisParams::rbf_sc (a kernel argument).
 template <int NV> struct BasisGen<BASIS_RBF, NV> {
   float xv[NV];
   template <int P>
@@ -146,38 +143,16 @@ template <int NV> struct BasisGen<BASIS_RBF, NV> {
     for (int v = 0; v < NV; ++v) xv[v] = x[v];
   }
   __device__ __forceinline__ void one(int k, const BasisParams& bp, float* v0) {
-    const float c = bp.centers[k];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const float d = xv[v] - c;
-      v0[v] = __builtin_amdgcn_exp2f(bp.neg_l * d * d);
-    }
-  }
-  __device__ __forceinline__ void pair(int k, const BasisParams& bp, float* v0, float* v1) {
-    one(k, bp, v0);
-    one(k + 1, bp, v1);
-  }
-};
-
-// Gaussian RBF on uniform centres c_k = c_0 + k*h:
-//   phi_k = exp2(-t_k^2),  t_k = s*x - (s*c_0 + k*s*h),  s = sqrt(-neg_l)
-// one fma, one multiply and one exp2 per value, and no per-slot centre load
-// (s*c_k is formed from two kernel arguments).  Same function as the direct
-// form exp2(neg_l * (x - c_k)^2) up to fp32 rounding of t_k.
-template <int NV> struct BasisGen<BASIS_RBF_UNIFORM, NV> {
-  float xv[NV];
-  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool = false) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) xv[v] = x[v];
-  }
-  template <int P>
-  __device__ __forceinline__ void step(int k, const BasisParams& bp, float* v0) {
-    const float sck = __builtin_fmaf((float)k, bp.rbf_sh, bp.rbf_sc0);
+    const float sck = bp.rbf_sc[k];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const float t = __builtin_fmaf(xv[v], bp.rbf_s, -sck);
       v0[v] = __builtin_amdgcn_exp2f(-(t * t));
     }
+  }
+  __device__ __forceinline__ void pair(int k, const BasisParams& bp, float* v0, float* v1) {
+    one(k, bp, v0);
+    one(k + 1, bp, v1);
   }
 };
 

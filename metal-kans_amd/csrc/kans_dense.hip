@@ -24,11 +24,11 @@
 //     kernel reduces (used when the output tile count alone cannot fill the GPU).
 //
 // Two kernels share this decomposition:
-//   kan_fused_block  fp16/bf16 Chebyshev and uniform-centre RBF with K+base <= 10:
+//   kan_fused_block  fp16/bf16 Chebyshev with K+base <= 10:
 //                    one barrier per feature block, global->LDS DMA of the next
 //                    block's weights, basis generation interleaved with the MFMAs;
-//   kan_fused_dense  everything else (fp32, B-spline, arbitrary RBF centres,
-//                    larger K): one barrier per slot, register-staged weights.
+//   kan_fused_dense  everything else (fp32, RBF, B-spline, larger K): one
+//                    barrier per slot, register-staged weights.
 #include "kans_common.h"
 #include "kans_api_internal.h"
 #include <algorithm>
@@ -126,18 +126,27 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
   // resident workgroup).
   const uint4* wbase = Wt + (long)ob0 * (64 * CPL) + tid;
   const long slot_stride = (long)nob_pad * (64 * CPL);
-  uint4 rg[LPT];
+  // The staged chunks live in one vector value, not a uint4 array: an array of
+  // more than one uint4 was left in private (scratch) memory by the compiler.
+  typedef unsigned RegVec __attribute__((ext_vector_type(4 * LPT)));
+  RegVec rg;
   auto gload = [&](int t) {
     const uint4* src = wbase + ((long)fb_begin * KP + t) * slot_stride;
 #pragma unroll
     for (int q = 0; q < LPT; ++q)
-      if (q * kThreads + tid < SU) rg[q] = src[q * kThreads];
+      if (q * kThreads + tid < SU) {
+        const uint4 u = src[q * kThreads];
+        rg[4 * q + 0] = u.x;
+        rg[4 * q + 1] = u.y;
+        rg[4 * q + 2] = u.z;
+        rg[4 * q + 3] = u.w;
+      }
   };
   auto lstore = [&](int t) {
     uint4* dst = lds[t % kStages] + tid;
 #pragma unroll
     for (int q = 0; q < LPT; ++q)
-      if (q * kThreads + tid < SU) dst[q * kThreads] = rg[q];
+      if (q * kThreads + tid < SU) dst[q * kThreads] = make_uint4(rg[4 * q], rg[4 * q + 1], rg[4 * q + 2], rg[4 * q + 3]);
   };
 
   // ---- input rows ---------------------------------------------------------
@@ -340,10 +349,10 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 constexpr int kBlockSlots = 10;
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
-// (scheduling hint): Chebyshev 1 fma per value, uniform RBF fma + mul + exp2,
-// plus the fp32 -> 16-bit packing.
+// (scheduling hint): Chebyshev 1 fma per value, plus the fp32 -> 16-bit
+// packing.
 template <int BASIS, int NV, int MFMAS>
-constexpr int kValuPerMfma = ((BASIS == BASIS_CHEBY ? 1 : 3) * NV + NV / 2 + MFMAS - 1) / MFMAS;
+constexpr int kValuPerMfma = (NV + NV / 2 + MFMAS - 1) / MFMAS;
 
 template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
 __global__ void __launch_bounds__(kThreads, 2)
@@ -630,18 +639,18 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   const int splits = (L.nfb + fbps - 1) / fbps;
   dim3 grid(m_tiles * n_tiles, splits);
   float* part = splits > 1 ? L.part : nullptr;
-  // fp16 / bf16 Chebyshev layers and RBF layers on uniform centres whose feature
-  // block fits one LDS stage take the block-pipelined kernel; B-spline (whose
-  // generator state does not fit beside the double A-fragment), RBF on
-  // arbitrary centres and fp32 take the per-slot kernel.
-  constexpr bool kBlockable = sizeof(T) == 2 && (BASIS == BASIS_CHEBY || BASIS == BASIS_RBF);
+  // fp16 / bf16 Chebyshev layers whose feature block fits one LDS stage take the
+  // block-pipelined kernel.  Everything else takes the per-slot kernel: fp32;
+  // B-spline, whose generator state does not fit beside the double A-fragment;
+  // and RBF, whose exp2-heavy generation measured faster there (two waves per
+  // SIMD alternate VALU and MFMA phases; the block kernel interleaves them in
+  // one wave and runs a few percent slower on the BASELINE shape).
+  constexpr bool kBlockable = sizeof(T) == 2 && BASIS == BASIS_CHEBY && NB <= 4;
   bool use_block = false;
-  if constexpr (kBlockable)
-    use_block = L.bp.K + L.has_base <= kBlockSlots && (BASIS == BASIS_CHEBY || L.bp.rbf_uniform != 0);
+  if constexpr (kBlockable) use_block = L.bp.K + L.has_base <= kBlockSlots;
   if (use_block) {
     if constexpr (kBlockable) {
-      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_UNIFORM : BASIS;
-      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
+      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
                          L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
                          L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
     }
@@ -663,19 +672,21 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
 }
 
 // Instantiated tile configurations (WM rows per wave, NB 32-column blocks):
-// (64,4) (32,4) (32,1); at most 128 fp32 accumulators per lane so two
-// workgroups (8 waves) stay resident per CU.  Keep in sync with
+// (64,4) (32,8) (32,4) (32,1); at most 128 fp32 accumulators per lane so two
+// workgroups (8 waves) stay resident per CU.  (32,8) halves the basis values a
+// lane generates per MFMA relative to (64,4).  Keep in sync with
 // dense_config_supported().
 template <typename T, typename TX, typename TY, int BASIS>
 static hipError_t launch_dense_cfg(const DenseLaunch& L, hipStream_t st) {
   if (L.wm == 64 && L.nb == 4) return launch_dense_t<T, TX, TY, BASIS, 64, 4>(L, st);
+  if (L.wm == 32 && L.nb == 8) return launch_dense_t<T, TX, TY, BASIS, 32, 8>(L, st);
   if (L.wm == 32 && L.nb == 4) return launch_dense_t<T, TX, TY, BASIS, 32, 4>(L, st);
   if (L.wm == 32 && L.nb == 1) return launch_dense_t<T, TX, TY, BASIS, 32, 1>(L, st);
   return hipErrorInvalidValue;
 }
 
 bool dense_config_supported(int wm, int nb) {
-  return (wm == 64 && nb == 4) || (wm == 32 && (nb == 4 || nb == 1));
+  return (wm == 64 && nb == 4) || (wm == 32 && (nb == 8 || nb == 4 || nb == 1));
 }
 
 template <typename T, typename TX, typename TY>

@@ -122,22 +122,16 @@ struct kans_layer {
   unsigned gen = 0;  // bumped whenever a buffer captured by a graph may have moved
 };
 
-// Uniform-centre form of the RBF basis: when c_k = c_0 + k*h holds to 1e-6 of
-// the grid's magnitude, the kernels may evaluate exp2(-(s*x - s*c_0 - k*s*h)^2)
-// with s = sqrt(-neg_l) instead of loading c_k per slot.
-static void set_rbf_uniform(BasisParams& bp) {
-  const int K = bp.K;
-  const double c0 = bp.centers[0];
-  const double h = K > 1 ? ((double)bp.centers[K - 1] - c0) / (K - 1) : 0.0;
-  double mag = std::fabs(c0);
-  for (int k = 0; k < K; ++k) mag = std::max(mag, (double)std::fabs(bp.centers[k]));
-  bool uni = bp.neg_l < 0.0f && std::isfinite(bp.neg_l);
-  for (int k = 0; k < K && uni; ++k) uni = std::fabs((double)bp.centers[k] - (c0 + k * h)) <= 1e-6 * mag;
-  const double sq = uni ? std::sqrt(-(double)bp.neg_l) : 0.0;
-  bp.rbf_uniform = uni ? 1 : 0;
+// Scaled-centre table of the RBF basis: phi_k = exp2(-(s*x - s*c_k)^2) with
+// s = sqrt(-neg_l), the form BasisGen<BASIS_RBF> evaluates.
+// Reference layers derive inv_denominator = 1 / (2 h^2) >= 0 (fast_kan.py:42);
+// a negative one (a growing "Gaussian") has no real scale s and is rejected.
+static bool rbf_inv_den_ok(float inv_den) { return inv_den >= 0.0f && std::isfinite(inv_den); }
+
+static void set_rbf_table(BasisParams& bp) {
+  const double sq = bp.neg_l < 0.0f ? std::sqrt(-(double)bp.neg_l) : 0.0;
   bp.rbf_s = (float)sq;
-  bp.rbf_sc0 = (float)(sq * c0);
-  bp.rbf_sh = (float)(sq * h);
+  for (int k = 0; k < bp.K; ++k) bp.rbf_sc[k] = (float)(sq * (double)bp.centers[k]);
 }
 
 static int validate_dims(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias) {
@@ -188,11 +182,12 @@ int kans_layer_destroy(kans_layer* L) {
 int kans_layer_set_rbf(kans_layer* L, const float* centers, float inv_den) {
   if (!L || !centers) return kans_fail(KANS_ERR_ARG, "null argument");
   if (L->basis != BASIS_RBF) return kans_fail(KANS_ERR_ARG, "layer basis is not RBF");
+  if (!rbf_inv_den_ok(inv_den)) return kans_fail(KANS_ERR_ARG, "RBF inv_denominator must be finite and >= 0");
   std::lock_guard<std::mutex> lk(g_mu);
   for (int k = 0; k < L->K; ++k) L->bp.centers[k] = centers[k];
   L->bp.have_centers = 1;
   L->bp.neg_l = -inv_den * kLog2e;
-  set_rbf_uniform(L->bp);
+  set_rbf_table(L->bp);
   ++L->gen;  // the kernel arguments captured by a chain graph change
   return 0;
 }
@@ -214,7 +209,7 @@ int kans_layer_set_tiling(kans_layer* L, int wm, int nb, int splits) {
   if (wm != 0 && wm != 32 && wm != 64) return kans_fail(KANS_ERR_ARG, "wm must be 0, 32 or 64");
   if ((wm == 0) != (nb == 0)) return kans_fail(KANS_ERR_ARG, "wm and nb must both be 0 or both set");
   if (wm != 0 && !dense_config_supported(wm, nb))
-    return kans_fail(KANS_ERR_ARG, "tile (wm=%d, nb=%d) not instantiated; use (64,4) (32,4) (32,1)", wm, nb);
+    return kans_fail(KANS_ERR_ARG, "tile (wm=%d, nb=%d) not instantiated; use (64,4) (32,8) (32,4) (32,1)", wm, nb);
   if (splits < 0) return kans_fail(KANS_ERR_ARG, "splits must be >= 0");
   L->forced_wm = wm;
   L->forced_nb = nb;
@@ -299,16 +294,29 @@ int kans_layer_load_weights_device(kans_layer* L, const void* W, const void* W_b
 
 }  // extern "C"
 
-// Tile configuration: among the instantiated (WM, NB) shapes, take the first
-// (largest tile first: basis generation and LDS traffic amortised best) that
-// gives every CU its two resident workgroups; otherwise the one with the most
-// tiles, then split the feature blocks until ~512 workgroups exist.
+// Tile configuration: among the instantiated (WM, NB) shapes, in the order of
+// preference for the layer's dtype and basis, take the first that gives every
+// CU its two resident workgroups; otherwise the one with the most tiles, then
+// split the feature blocks until ~512 workgroups exist.  Preference orders
+// come from MI355X timings at 16384 x 1024 -> 1024 (16-bit) and 8192 x 1024 ->
+// {1024, 4096} (fp32):
+//   16-bit Chebyshev  (64,4) -- the block-pipelined kernel;
+//   16-bit RBF        (32,8) -- 8 basis values per lane feed 8 MFMAs (exp2-bound
+//                               generation amortised over twice the columns);
+//   16-bit B-spline   (32,8) -- also keeps the generator state small;
+//   fp32 Chebyshev/RBF (32,4); fp32 B-spline (32,8).
 static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
-  static const int cand[3][2] = {{64, 4}, {32, 4}, {32, 1}};  // largest tile first
+  static const int pref_wide[4][2] = {{64, 4}, {32, 8}, {32, 4}, {32, 1}};
+  static const int pref_n8[4][2] = {{32, 8}, {64, 4}, {32, 4}, {32, 1}};
+  static const int pref_n4[4][2] = {{32, 4}, {64, 4}, {32, 8}, {32, 1}};
+  const bool f32 = L->dtype == DT_F32;
+  const int(*cand)[2] = (L->basis == BASIS_BSPLINE || (!f32 && L->basis == BASIS_RBF)) ? pref_n8
+                        : f32 ? pref_n4 : pref_wide;
   const int nob = (L->D_out + 31) / 32;
   auto tiles = [&](int ww, int nn) { return ((B + 4 * ww - 1) / (4 * ww)) * ((nob + nn - 1) / nn); };
   int bw = 32, bn = 1, bt = tiles(32, 1);  // (32, 1) always fits
-  for (auto& c : cand) {
+  for (int i = 0; i < 4; ++i) {
+    const int* c = cand[i];
     const int padded = ((nob + c[1] - 1) / c[1]) * c[1];
     if (c[1] > 1 && 2 * nob < padded) continue;  // over half of the N-tile would be padding
     const int t = tiles(c[0], c[1]);
@@ -596,6 +604,8 @@ static std::map<SigKey, std::unique_ptr<kans_layer>> g_sig_layers;
 
 static int sig_layer(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias,
                      const std::vector<float>& params, kans_layer** out) {
+  if (basis == BASIS_RBF && !rbf_inv_den_ok(params[K]))
+    return kans_fail(KANS_ERR_ARG, "RBF inv_denominator must be finite and >= 0");
   SigKey key(basis, dtype, D_in, D_out, K, has_base, has_bias, params);
   auto it = g_sig_layers.find(key);
   if (it != g_sig_layers.end()) {
@@ -620,7 +630,7 @@ static int sig_layer(int basis, int dtype, int D_in, int D_out, int K, int has_b
     for (int k = 0; k < K; ++k) L->bp.centers[k] = params[k];
     L->bp.have_centers = 1;
     L->bp.neg_l = -params[K] * kLog2e;
-    set_rbf_uniform(L->bp);
+    set_rbf_table(L->bp);
   } else if (basis == BASIS_BSPLINE) {
     L->bp.grid_size = K - 3;
     L->bp.grid_min = params[0];

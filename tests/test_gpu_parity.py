@@ -87,11 +87,13 @@ def test_branch_flags(gpu, kind, K, base, bias):
     assert O.rel_err(L(x), oracle_of(L, x)) <= 1e-4
 
 
-@pytest.mark.parametrize("wm,nb,splits", [(64, 4, 1), (32, 4, 1), (32, 1, 1), (64, 4, 3), (32, 4, 5)])
+@pytest.mark.parametrize("wm,nb,splits", [(64, 4, 1), (32, 8, 1), (32, 4, 1), (32, 1, 1), (64, 4, 3), (32, 4, 5),
+                                          (32, 8, 4)])
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
-def test_tilings_and_splits(gpu, wm, nb, splits, dtype):
+@pytest.mark.parametrize("kind,K", [("cheby", 6), ("rbf", 8)])
+def test_tilings_and_splits(gpu, wm, nb, splits, dtype, kind, K):
     import metal_kans as mk
-    L = make_layer(mk, "cheby", 200, 150, 6, seed=11)
+    L = make_layer(mk, kind, 200, 150, K, seed=11)
     L.set_tiling(wm, nb, splits)
     x = np.random.default_rng(2).uniform(-1, 1, (333, 200)).astype(np.float32)
     y_ref = oracle_of(L, x)
@@ -104,6 +106,10 @@ def test_rbf_arbitrary_centres(gpu):
     L.grid = np.array([-1.7, -0.2, 0.0, 0.9, 2.4], np.float32)   # non-uniform centres
     x = np.random.default_rng(3).normal(0, 1, (90, 48)).astype(np.float32)
     assert O.rel_err(L(x), oracle_of(L, x)) <= 1e-4
+    # reference layers always carry inv_denominator = 1/(2h^2) >= 0; a negative one is refused loudly
+    L.inv_denominator = -1.0
+    with pytest.raises(RuntimeError, match="inv_denominator"):
+        L(x)
 
 
 def test_inputs_outside_grid_and_extremes(gpu):
