@@ -34,7 +34,7 @@ PEAK = {"f16": 2516.6, "bf16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s (MI3
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) scaled by a copy-kernel
 # calibration: the source of roofline.traffic (PMC counters cannot be read
 # from inside the timed process).
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_kan_fused_dense_cfg3_fastkan_fp16.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_kan_fused_block_cfg3_fastkan_fp16.txt")
 SECONDARY = ("ns_cheby_fp16", "ns_bspline_fp16", "cfg4_bspline_bf16", "cfg4_bspline_fp32", "cfg1_cheby_fp32",
              "cfg2", "cfg5")
 HBM_PEAK_GBS = 8000.0
@@ -376,11 +376,9 @@ def main():
                                   steps=iters)
     F = st["flops"]
     wall_ms = st["wall_ms"]
-    # RBF layers always take the per-slot kernel; its tile is the library's choice for this batch
-    tile = [ctypes.c_int() for _ in range(3)]
-    assert lib.kans_layer_describe(st["eng"].handle, 16384, *[ctypes.byref(v) for v in tile]) == 0
-    head_kernel = (f"kans::kan_fused_dense<_Float16, _Float16, _Float16, BASIS_RBF, {tile[0].value}, "
-                   f"{tile[1].value}>" + (f" x {tile[2].value} feature splits" if tile[2].value > 1 else ""))
+    name = ctypes.create_string_buffer(160)
+    assert lib.kans_layer_kernel(st["eng"].handle, 16384, name, 160) == 0
+    head_kernel = name.value.decode()
     value = F / wall_ms / 1e9
     kernel_ms = head["ms"]
     achieved = F / kernel_ms / 1e9

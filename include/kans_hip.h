@@ -170,6 +170,8 @@ int kans_layer_set_bspline(kans_layer* layer, int grid_size, float grid_min, flo
 /* tiling override for tuning: (wm, nb) in {(64,4),(32,8),(32,4),(32,1)} or (0,0) = automatic; splits >= 0 */
 int kans_layer_set_tiling(kans_layer* layer, int wm, int nb, int splits);
 int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
+/* name of the fused kernel (and its tile) that a forward of batch B runs, NUL-terminated in name[len] */
+int kans_layer_kernel(const kans_layer* layer, int B, char* name, int len);
 /* weights in the layer dtype: W [D_out][D_in*K] (k fastest), W_base [D_out][D_in], bias [D_out] */
 int kans_layer_load_weights(kans_layer* layer, const void* W, const void* W_base, const void* bias);
 int kans_layer_load_weights_device(kans_layer* layer, const void* W, const void* W_base, const void* bias);

@@ -16,6 +16,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 enum Basis { BASIS_CHEBY = 0, BASIS_RBF = 1, BASIS_BSPLINE = 2 };
+// Kernel-only basis id: the Gaussian RBF of BASIS_RBF with its scaled centres
+// read from a table in LDS (BasisGen<BASIS_RBF_TABLE>); the public API never
+// sees it.
+constexpr int BASIS_RBF_TABLE = 3;
 enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -153,6 +157,29 @@ template <int NV> struct BasisGen<BASIS_RBF, NV> {
   __device__ __forceinline__ void pair(int k, const BasisParams& bp, float* v0, float* v1) {
     one(k, bp, v0);
     one(k + 1, bp, v1);
+  }
+};
+
+// Gaussian RBF as BasisGen<BASIS_RBF>, with the scaled centre s*c_k read from
+// `tab`, a copy of BasisParams::rbf_sc in LDS (entry K = 0 for the unused step
+// after a block's last slot).  A broadcast LDS read is counted with the LDS
+// reads of the weights (in order), where a scalar load from the argument
+// segment would force a wait for all of them.
+template <int NV> struct BasisGen<BASIS_RBF_TABLE, NV> {
+  float xv[NV];
+  const float* tab = nullptr;
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool = false) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xv[v] = x[v];
+  }
+  template <int P>
+  __device__ __forceinline__ void step(int k, const BasisParams& bp, float* v0) {
+    const float sck = tab[k];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float t = __builtin_fmaf(xv[v], bp.rbf_s, -sck);
+      v0[v] = __builtin_amdgcn_exp2f(-(t * t));
+    }
   }
 };
 

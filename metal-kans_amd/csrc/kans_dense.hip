@@ -24,10 +24,11 @@
 //     kernel reduces (used when the output tile count alone cannot fill the GPU).
 //
 // Two kernels share this decomposition:
-//   kan_fused_block  fp16/bf16 Chebyshev with K+base <= 10:
+//   kan_fused_block  fp16/bf16: Chebyshev with K+base <= 10 (4 waves), RBF and
+//                    B-spline with K+base <= 9 on the 256 x 256 tile (8 waves):
 //                    one barrier per feature block, global->LDS DMA of the next
 //                    block's weights, basis generation interleaved with the MFMAs;
-//   kan_fused_dense  everything else (fp32, RBF, B-spline, larger K): one
+//   kan_fused_dense  everything else (fp32, other tiles, larger K): one
 //                    barrier per slot, register-staged weights.
 #include "kans_common.h"
 #include "kans_api_internal.h"
@@ -344,18 +345,27 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // run.  Slots are unrolled by two so the fragment buffers and the Chebyshev
 // recurrence roles are fixed at compile time.
 //
-// Requires KP = K + has_base <= kBlockSlots (the launcher checks).
+// Two shapes: WAVES = 4 (tile 4*WM x NB*32, two workgroups per CU) and
+// WAVES = 8 with WM = 32, NB = 8 (tile 256 x 256, one workgroup of 8 waves
+// per CU).  The second halves the basis values a lane generates per MFMA
+// (8 values feed 8 MFMAs), which the exp2-based RBF and the B-spline need;
+// its two stages of 9 slots x 8 KB fill 144 KB of the 160 KB LDS.
+//
+// Requires KP = K + has_base <= block_slots(WAVES) (the launcher checks).
 // ---------------------------------------------------------------------------
-constexpr int kBlockSlots = 10;
+constexpr int kBlockSlots = 10;   // WAVES = 4
+constexpr int kBlockSlots8 = 9;   // WAVES = 8
+__host__ __device__ constexpr int block_slots(int waves) { return waves == 8 ? kBlockSlots8 : kBlockSlots; }
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
-// (scheduling hint): Chebyshev 1 fma per value, plus the fp32 -> 16-bit
-// packing.
+// (scheduling hint): per value 1 fma (Chebyshev), fma + mul + exp2 (RBF) or
+// ~6 compares / selects (B-spline), plus the fp32 -> 16-bit packing.
 template <int BASIS, int NV, int MFMAS>
-constexpr int kValuPerMfma = (NV + NV / 2 + MFMAS - 1) / MFMAS;
+constexpr int kValuPerMfma =
+    ((BASIS == BASIS_CHEBY ? 1 : BASIS == BASIS_BSPLINE ? 6 : 3) * NV + NV / 2 + MFMAS - 1) / MFMAS;
 
-template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
-__global__ void __launch_bounds__(kThreads, 2)
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64, WAVES == 4 ? 2 : 1)
 kan_fused_block(const TX* __restrict__ X, long ldx,
                 const uint4* __restrict__ Wt, int nob_pad,
                 const T* __restrict__ bias,
@@ -369,8 +379,12 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   constexpr int SLOT = NB * 64;         // uint4 per slot of the N-tile
   typedef typename Mfma<T>::frag frag;
 
-  __shared__ uint4 stage0[kBlockSlots * SLOT];
-  __shared__ uint4 stage1[kBlockSlots * SLOT];
+  constexpr int SLOTS = block_slots(WAVES);
+  __shared__ uint4 stage0[SLOTS * SLOT];
+  __shared__ uint4 stage1[SLOTS * SLOT];
+  // RBF: scaled centres s*c_k, entry K = 0 (read by the unused step after a
+  // block's last slot)
+  __shared__ float rbf_tab[BASIS == BASIS_RBF_TABLE ? kMaxK + 1 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -379,7 +393,7 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   tile_of(xcd_remap(blockIdx.x, m_tiles * n_tiles), m_tiles, n_tiles, m_tile, n_tile);
   const int split = blockIdx.y;
 
-  const int row0 = m_tile * (4 * WM) + wave * WM;
+  const int row0 = m_tile * (WAVES * WM) + wave * WM;
   const int ob0 = n_tile * NB;
   const int fb_begin = split * fb_per_split;
   const int fb_end = min(nfb_total, fb_begin + fb_per_split);
@@ -389,11 +403,11 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   // ---- weights: global -> LDS DMA ------------------------------------------
   // Slot s, column block nb of block fb is W'[fb][s][ob0 + nb][lane]: 64 lanes x
   // 16 B contiguous, one DMA instruction.  Instruction j = s*NB + nb of a block
-  // is issued by wave j % 4 and lands at stage[j * 64 + lane].
+  // is issued by wave j % WAVES and lands at stage[j * 64 + lane].
   const uint4* wtile = Wt + (long)ob0 * 64 + lane;
   auto dma = [&](int fb, uint4* stage) {
     const uint4* src = wtile + (long)fb * KP * nob_pad * 64;
-    for (int j = wave; j < KP * NB; j += 4) {
+    for (int j = wave; j < KP * NB; j += WAVES) {
       const int s = j / NB, nb = j - s * NB;
       __builtin_amdgcn_global_load_lds(src + ((long)s * nob_pad + nb) * 64,
                                        (__attribute__((address_space(3))) void*)(stage + j * 64), 16, 0, 0);
@@ -468,11 +482,15 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
 
   // ---- prologue: block fb_begin in stage0 and registers ----------------------
+  if constexpr (BASIS == BASIS_RBF_TABLE) {
+    if (tid <= bp.K) rbf_tab[tid] = tid < bp.K ? bp.rbf_sc[tid] : 0.0f;
+  }
   dma(fb_begin, stage0);
   xload(fb_begin);
   __syncthreads();
 
   BasisGen<BASIS, NV> gen;
+  if constexpr (BASIS == BASIS_RBF_TABLE) gen.tab = rbf_tab;
   frag af[2][RB], bf[NB];
   // One slot s of parity P, a single basic block: the MFMAs of slot s (on
   // af[P], bf) are interleaved with the basis values of slot s+1 (into
@@ -630,6 +648,8 @@ __global__ void kan_convert(const S* __restrict__ src, T* __restrict__ dst, long
 // ---------------------------------------------------------------------------
 
 
+int block_waves(bool half, int basis, int wm, int nb, int KP);
+
 template <typename T, typename TX, typename TY, int BASIS, int WM, int NB>
 static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   const int m_tiles = (L.B + 4 * WM - 1) / (4 * WM);
@@ -639,20 +659,26 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   const int splits = (L.nfb + fbps - 1) / fbps;
   dim3 grid(m_tiles * n_tiles, splits);
   float* part = splits > 1 ? L.part : nullptr;
-  // fp16 / bf16 Chebyshev layers whose feature block fits one LDS stage take the
-  // block-pipelined kernel.  Everything else takes the per-slot kernel: fp32;
-  // B-spline, whose generator state does not fit beside the double A-fragment;
-  // and RBF, whose exp2-heavy generation measured faster there (two waves per
-  // SIMD alternate VALU and MFMA phases; the block kernel interleaves them in
-  // one wave and runs a few percent slower on the BASELINE shape).
-  constexpr bool kBlockable = sizeof(T) == 2 && BASIS == BASIS_CHEBY && NB <= 4;
-  bool use_block = false;
-  if constexpr (kBlockable) use_block = L.bp.K + L.has_base <= kBlockSlots;
-  if (use_block) {
-    if constexpr (kBlockable) {
-      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
+  // Kernel choice for 16-bit layers whose feature block fits one LDS stage:
+  //   Chebyshev, tiles up to NB = 4        -> block kernel, 4 waves;
+  //   RBF / B-spline, tile (32,8)          -> block kernel, 8 waves (256 x 256);
+  // everything else (fp32, other tiles, larger K) -> the per-slot kernel.
+  const int waves = block_waves(sizeof(T) == 2, BASIS, WM, NB, L.bp.K + L.has_base);
+  constexpr bool kBlock4 = sizeof(T) == 2 && BASIS == BASIS_CHEBY && NB <= 4;
+  constexpr bool kBlock8 = sizeof(T) == 2 && (BASIS == BASIS_RBF || BASIS == BASIS_BSPLINE) && WM == 32 && NB == 8;
+  if (waves == 4) {
+    if constexpr (kBlock4) {
+      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BASIS, WM, NB, 4>), grid, dim3(256), 0, st, (const TX*)L.X,
                          L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
                          L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+    }
+  } else if (waves == 8) {
+    if constexpr (kBlock8) {
+      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_TABLE : BASIS;
+      const int m_tiles8 = (L.B + 8 * WM - 1) / (8 * WM);
+      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8>), dim3(m_tiles8 * n_tiles, splits), dim3(512), 0,
+                         st, (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy,
+                         part, L.B, L.D_in, L.D_out, m_tiles8, n_tiles, L.nfb, fbps, L.has_base, L.bp);
     }
   } else {
     hipLaunchKernelGGL((kan_fused_dense<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,
@@ -669,6 +695,14 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
     e = hipGetLastError();
   }
   return e;
+}
+
+// Workgroup waves of the block kernel for this configuration, 0 when the
+// per-slot kernel runs (the routing of launch_dense_t).
+int block_waves(bool half, int basis, int wm, int nb, int KP) {
+  if (half && basis == BASIS_CHEBY && nb <= 4 && KP <= kBlockSlots) return 4;
+  if (half && (basis == BASIS_RBF || basis == BASIS_BSPLINE) && wm == 32 && nb == 8 && KP <= kBlockSlots8) return 8;
+  return 0;
 }
 
 // Instantiated tile configurations (WM rows per wave, NB 32-column blocks):

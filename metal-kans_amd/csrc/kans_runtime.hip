@@ -38,6 +38,7 @@ using namespace kans;
 namespace kans {
 hipError_t launch_dense(const DenseLaunch& L, hipStream_t st);
 bool dense_config_supported(int wm, int nb);
+int block_waves(bool half, int basis, int wm, int nb, int KP);
 hipError_t launch_repack(int src_dtype, int dtype, const void* W, const void* Wb, void* Wt, int D_in, int D_out,
                          int K, int has_base, int nfb, int nob_pad, hipStream_t st);
 hipError_t launch_convert(int src_dtype, int dtype, const void* src, void* dst, long n, hipStream_t st);
@@ -495,6 +496,23 @@ int kans_layer_forward_host_ex(kans_layer* L, const void* X, int x_dtype, void* 
 int kans_layer_describe(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
   if (!L || !wm || !nb || !splits) return kans_fail(KANS_ERR_ARG, "null argument");
   choose_tiling(L, B, wm, nb, splits);
+  return 0;
+}
+
+int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
+  if (!L || !name || len <= 0) return kans_fail(KANS_ERR_ARG, "null argument");
+  int wm, nb, splits;
+  choose_tiling(L, B, &wm, &nb, &splits);
+  static const char* dt[] = {"float", "_Float16", "__bf16"};
+  static const char* bs[] = {"BASIS_CHEBY", "BASIS_RBF", "BASIS_BSPLINE"};
+  const int waves = block_waves(L->dtype != DT_F32, L->basis, wm, nb, L->K + L->has_base);
+  int n;
+  if (waves)
+    n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves>", dt[L->dtype],
+                 L->basis == BASIS_RBF ? "BASIS_RBF_TABLE" : bs[L->basis], wm, nb, waves);
+  else
+    n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", dt[L->dtype], bs[L->basis], wm, nb);
+  if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);
   return 0;
 }
 

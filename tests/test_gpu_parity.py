@@ -90,7 +90,7 @@ def test_branch_flags(gpu, kind, K, base, bias):
 @pytest.mark.parametrize("wm,nb,splits", [(64, 4, 1), (32, 8, 1), (32, 4, 1), (32, 1, 1), (64, 4, 3), (32, 4, 5),
                                           (32, 8, 4)])
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
-@pytest.mark.parametrize("kind,K", [("cheby", 6), ("rbf", 8)])
+@pytest.mark.parametrize("kind,K", [("cheby", 6), ("rbf", 8), ("bspline", 8), ("rbf", 12)])
 def test_tilings_and_splits(gpu, wm, nb, splits, dtype, kind, K):
     import metal_kans as mk
     L = make_layer(mk, kind, 200, 150, K, seed=11)
@@ -98,6 +98,26 @@ def test_tilings_and_splits(gpu, wm, nb, splits, dtype, kind, K):
     x = np.random.default_rng(2).uniform(-1, 1, (333, 200)).astype(np.float32)
     y_ref = oracle_of(L, x)
     assert O.rel_err(cast(L, dtype)(x), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("kind,K", [("rbf", 8), ("bspline", 8), ("rbf", 5), ("bspline", 6)])
+@pytest.mark.parametrize("base,bias", [(True, True), (False, False), (False, True)])
+def test_block_kernel_256x256_tile(gpu, dtype, kind, K, base, bias):
+    """16-bit RBF / B-spline on the (32, 8) tile take the 8-wave block kernel (K + base <= 9): ragged
+    rows, a feature count that is not a multiple of 16, output columns that end inside an N-tile,
+    with and without a feature split."""
+    import metal_kans as mk
+    L = make_layer(mk, kind, 200, 150, K, bias=bias, base=base, seed=21, grid_range=(-1.5, 1.5))
+    x = np.random.default_rng(5).uniform(-1.7, 1.7, (300, 200)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    for splits in (1, 3):
+        L.set_tiling(32, 8, splits)
+        assert O.rel_err(L(x), y_ref) <= TOL[dtype]
+        name = ctypes.create_string_buffer(160)
+        assert gpu.kans_layer_kernel(L._engine().handle, 300, name, 160) == 0
+        assert name.value.startswith(b"kans::kan_fused_block<") and b"32, 8, 8 waves>" in name.value, name.value
 
 
 def test_rbf_arbitrary_centres(gpu):
