@@ -10,9 +10,26 @@ enum QuantKind { Q_INT4 = 0, Q_TERN = 1 };
 // Reduction indices per superchunk (one wave load of a 16-row block).
 constexpr int kQSuper = 128;
 
+// Batches up to kSmallB take the small-batch GEMV (live accumulator rows only,
+// three-deep prefetch ring at two waves per SIMD); larger ones up to 32 the
+// general one (three waves per SIMD at MT = 1, one superchunk in flight).
+constexpr int kSmallB = 2;
+// Work items (waves) per CU the split-K aims for: the small-batch kernel's
+// resident waves per CU (INT4 two, ternary three per SIMD: its register
+// footprint), the general kernel's ~10.
+inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 12) : 10; }
+
 // 16-row blocks per decode wave (64 output rows: each activation fragment
-// serves 4 weight tiles, and a wave reads 4 KB of weights per superchunk).
-inline int qrow_blocks(int /*D_out*/) { return 4; }
+// serves 4 weight tiles, and a wave reads 4 KB of INT4 codes per superchunk).
+constexpr int kQNW = 4;
+inline int qrow_blocks(int /*D_out*/) { return kQNW; }
+
+// Bytes of one 16-row x 128-index code tile, and of one record: the kQNW code
+// tiles a decode wave reads for one superchunk followed by their group
+// parameters (kQNW x 16 rows x float4), so the wave's whole input is one
+// contiguous stream.
+__host__ __device__ constexpr int qtile_bytes(int quant) { return quant == Q_INT4 ? 1024 : 512; }
+__host__ __device__ constexpr int qrec_bytes(int quant) { return kQNW * (qtile_bytes(quant) + 16 * 16); }
 
 // Activation basis of one layer input (see k_prep).
 struct QPrep {
@@ -29,8 +46,8 @@ struct QPrep {
 // One decode GEMV launch over one matrix or two matrices sharing the
 // activations (GatedKAN gate | up), see k_qgemv.
 struct QGemv {
-  const void* q0; const float4* sb0; int D_out0;
-  const void* q1; const float4* sb1; int D_out1;  // q1 null: single matrix
+  const void* rec0; int D_out0;
+  const void* rec1; int D_out1;  // rec1 null: single matrix
   int nw;          // 16-row blocks per row group (qrow_blocks)
   int rg_split;    // row groups of matrix 0
   int n_rg;        // row groups in total
@@ -43,10 +60,11 @@ struct QGemv {
   int N_total;
 };
 
+// Re-tile a packed matrix (C superchunks starting at superchunk c_off) into the records R.
 hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
-                      int gpr, int nrb, int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st);
+                      int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st);
 hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wpr, long K_dim, int gpr, int nrb,
-                      int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st);
+                      int C, int c_off, int C_tot, void* R, hipStream_t st);
 hipError_t qprep(int qt, const QPrep& P, hipStream_t st);
 hipError_t qgemv(int qt, const QGemv& G, hipStream_t st);
 // out[m][n] = sum_ks part[ks][m][n] + bias[n]

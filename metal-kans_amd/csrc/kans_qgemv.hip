@@ -42,13 +42,25 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------
 // Re-tiling of the wire formats (run once per layer).
 //
-// Tile order: [row group of nw row blocks][superchunk][row block in group]:
-// the nw tiles one decode wave reads per superchunk are contiguous, and each
-// wave's superchunk range is one contiguous stream.  nw is chosen per layer
-// (kans_qgemv.h: qrow_blocks).
+// Record order: one record per (row group of kQNW row blocks, superchunk),
+// records of a row group consecutive in superchunk order, so each decode
+// wave's superchunk range is one contiguous stream.  A record holds the kQNW
+// code tiles (1 KB INT4 / 512 B ternary each) followed by their group
+// parameters (kQNW x 16 rows x float4), see qrec_bytes.
 // ---------------------------------------------------------------------------
-__host__ __device__ __forceinline__ long qtile_index(int rb, int c, int C_tot, int nw) {
-  return ((long)(rb / nw) * C_tot + c) * nw + rb % nw;
+template <int QT>
+__host__ __device__ __forceinline__ long qrec_offset(int rb, int c, int C_tot) {
+  return ((long)(rb / kQNW) * C_tot + c) * qrec_bytes(QT);
+}
+// byte offset of lane `lane`'s code word of row block rb, superchunk c
+template <int QT>
+__host__ __device__ __forceinline__ long qcode_offset(int rb, int c, int C_tot, int lane) {
+  return qrec_offset<QT>(rb, c, C_tot) + (long)(rb % kQNW) * qtile_bytes(QT) + (long)lane * (qtile_bytes(QT) / 64);
+}
+// byte offset of the group parameters (float4) of row r of row block rb, superchunk c
+template <int QT>
+__host__ __device__ __forceinline__ long qparam_offset(int rb, int c, int C_tot, int r) {
+  return qrec_offset<QT>(rb, c, C_tot) + (long)kQNW * qtile_bytes(QT) + (long)((rb % kQNW) * 16 + r) * 16;
 }
 
 // INT4 qweight: row n is `rowbytes` bytes (groups of 64 nibbles contiguous,
@@ -56,7 +68,7 @@ __host__ __device__ __forceinline__ long qtile_index(int rb, int c, int C_tot, i
 // dword t holds the 8 nibbles of row 16*rb + r at reduction indices
 // 128c + 32t + 8q .. +7, i.e. bytes 64c + 16t + 4q .. +3 of the row.
 __global__ void k_tile_int4(const unsigned char* __restrict__ qw, long rowbytes, int D_out, int nrb, int C,
-                            int c_off, int C_tot, int nw, uint4* __restrict__ Q) {
+                            int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 64;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int lane = (int)(idx & 63);
@@ -76,14 +88,14 @@ __global__ void k_tile_int4(const unsigned char* __restrict__ qw, long rowbytes,
         }
       }
     }
-    Q[qtile_index(rb, c_off + c, C_tot, nw) * 64 + lane] = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(R + qcode_offset<Q_INT4>(rb, c_off + c, C_tot, lane)) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
 // INT4 group parameters: SB[rb][c][r] = (s0, s0', s1, s1') for the groups
 // 2c, 2c+1 of row 16*rb + r, s' = b - 1024 s (zero past the row / matrix).
 __global__ void k_tile_int4_params(const float* __restrict__ scales, const float* __restrict__ biases, int gpr,
-                                   int D_out, int nrb, int C, int c_off, int C_tot, int nw, float4* __restrict__ SB) {
+                                   int D_out, int nrb, int C, int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 16;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int r = (int)(idx & 15);
@@ -103,7 +115,7 @@ __global__ void k_tile_int4_params(const float* __restrict__ scales, const float
         }
       }
     }
-    SB[qtile_index(rb, c_off + c, C_tot, nw) * 16 + r] = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(R + qparam_offset<Q_INT4>(rb, c_off + c, C_tot, r)) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -114,7 +126,7 @@ __global__ void k_tile_int4_params(const float* __restrict__ scales, const float
 // bit 2p (e = 2p) or 16 + 2p (e = 2p+1); of step B at bit 8 + 2p or 24 + 2p,
 // so that one shift aligns the two codes of an fp16 pair at bits 8 and 24.
 __global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim, int D_out, int nrb, int C,
-                            int c_off, int C_tot, int nw, uint2* __restrict__ T) {
+                            int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 64;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int lane = (int)(idx & 63);
@@ -147,13 +159,13 @@ __global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim
         out[t >> 1] |= v;
       }
     }
-    T[qtile_index(rb, c_off + c, C_tot, nw) * 64 + lane] = make_uint2(out[0], out[1]);
+    *reinterpret_cast<uint2*>(R + qcode_offset<Q_TERN>(rb, c_off + c, C_tot, lane)) = make_uint2(out[0], out[1]);
   }
 }
 
 // Ternary scales: SB[rb][c][r] = scales of the four 32-groups of superchunk c.
 __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, int D_out, int nrb, int C, int c_off,
-                                   int C_tot, int nw, float4* __restrict__ SB) {
+                                   int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 16;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int r = (int)(idx & 15);
@@ -169,7 +181,7 @@ __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, in
         if (g < gpr) v[t] = scales[(long)n * gpr + g];
       }
     }
-    SB[qtile_index(rb, c_off + c, C_tot, nw) * 16 + r] = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(R + qparam_offset<Q_TERN>(rb, c_off + c, C_tot, r)) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -326,8 +338,7 @@ __device__ __forceinline__ half8v unpack_tern(unsigned w, const UnpackConsts& k)
 }
 
 struct QMatDev {
-  const void* q;        // INT4: uint4 [nrb_pad][C_tot][64]; ternary: uint2
-  const float4* sb;     // [nrb_pad][C_tot][16]
+  const char* rec;      // records [nrb_pad / kQNW][C_tot], qrec_bytes each
   int D_out;
   int col_off;          // column offset of this matrix in the output / workspace
 };
@@ -337,8 +348,6 @@ struct QMatDev {
 // workgroup.  part[ks][m][col] (m < B) receives the wave's partial sums.
 // SMALL (B <= kSmallB): batch row m lives only in accumulator register m of
 // lanes 0-15, so the per-group epilogue updates just those registers.
-constexpr int kSmallB = 2;
-constexpr int kQNW = 4;
 
 template <int QT, int MT, bool SMALL>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
@@ -376,12 +385,10 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   }
 
   typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
-  const QWord* qbase = reinterpret_cast<const QWord*>(M.q);
+  const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
 
-  // operands of one superchunk.  The weights / group parameters of superchunk
-  // c+1 are loaded while c is consumed; the activation fragments of c (L2
-  // resident) are loaded just before that prefetch is issued, so waiting for
-  // them (vmcnt counts in issue order) never waits for the prefetch.
+  // operands of one superchunk: weights / group parameters (HBM stream) and
+  // activation fragments / group sums (L2 resident).
   struct Wts {
     QWord qw[NW];
     float4 sb[NW];
@@ -395,15 +402,17 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     Acts x;
   };
   auto load_w = [&](int c, Wts& o) {
+    const char* rec = rbase + (long)c * qrec_bytes(QT);
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const long tile = ((long)rg_loc * C_tot + c) * NW + w;
-      o.qw[w] = qbase[tile * 64 + lane];
+      o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
       // the four lanes of a row (q = 0..3) share its group parameters; with
       // SMALL only lanes 0-15 (q = 0) hold live accumulators, so only they load
       // (16 distinct 16-byte requests instead of 64 duplicated ones)
-      if (!SMALL || q == 0) o.sb[w] = M.sb[tile * 16 + r];
-      else o.sb[w] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!SMALL || q == 0)
+        o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
+      else
+        o.sb[w] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   auto load_x = [&](int c, Acts& o) {
@@ -478,17 +487,50 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     }
   };
 
-  Wts w0, w1;
-  if (c_lo < c_hi) load_w(c_lo, w0);
-  for (int c = c_lo; c < c_hi; c += 2) {
-    Acts x;
-    load_x(c, x);
-    if (c + 1 < c_hi) load_w(c + 1, w1);
-    compute(w0, x);
-    if (c + 1 >= c_hi) break;
-    load_x(c + 1, x);
-    if (c + 2 < c_hi) load_w(c + 2, w0);
-    compute(w1, x);
+  if (c_lo < c_hi) {
+    if constexpr (SMALL) {
+      // Three-deep ring: superchunks c+1 and c+2 are in flight while c is
+      // consumed (~10 KB per wave: the stream needs that much in flight to
+      // cover the HBM latency at full bandwidth).  Loads past the end of the
+      // range repeat the last superchunk (an L2 hit, no extra HBM traffic), so
+      // the loop body is branch-free between the exits and compute(c) waits for
+      // exactly the operands of c (vmcnt counts in issue order).
+      Ops o0, o1, o2;
+      auto issue = [&](int c, Ops& o) {
+        const int cc = min(c, c_hi - 1);
+        load_x(cc, o.x);
+        load_w(cc, o.w);
+      };
+      issue(c_lo, o0);
+      issue(c_lo + 1, o1);
+      for (int c = c_lo; c < c_hi; c += 3) {
+        issue(c + 2, o2);
+        compute(o0.w, o0.x);
+        if (c + 1 >= c_hi) break;
+        issue(c + 3, o0);
+        compute(o1.w, o1.x);
+        if (c + 2 >= c_hi) break;
+        issue(c + 4, o1);
+        compute(o2.w, o2.x);
+      }
+    } else {
+      // Larger batches hold MT activation tiles per superchunk: one superchunk
+      // of weights in flight (a deeper ring would cost occupancy).  The
+      // activation fragments of c are loaded just before that prefetch, so
+      // waiting for them never waits for it.
+      Wts w0, w1;
+      load_w(c_lo, w0);
+      for (int c = c_lo; c < c_hi; c += 2) {
+        Acts x;
+        load_x(c, x);
+        if (c + 1 < c_hi) load_w(c + 1, w1);
+        compute(w0, x);
+        if (c + 1 >= c_hi) break;
+        load_x(c + 1, x);
+        if (c + 2 < c_hi) load_w(c + 2, w0);
+        compute(w1, x);
+      }
+    }
   }
 
   // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
@@ -569,20 +611,20 @@ __global__ void k_qswiglu(const float* __restrict__ part, int ksplit, int B, int
 static int grid_for(long n) { return (int)std::min<long>((n + 255) / 256, 8192); }
 
 hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
-                      int gpr, int nrb, int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st) {
+                      int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st) {
   hipLaunchKernelGGL(k_tile_int4, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, qw, rowbytes, D_out, nrb, C,
-                     c_off, C_tot, nw, (uint4*)Q);
+                     c_off, C_tot, (char*)R);
   hipLaunchKernelGGL(k_tile_int4_params, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales, biases, gpr,
-                     D_out, nrb, C, c_off, C_tot, nw, SB);
+                     D_out, nrb, C, c_off, C_tot, (char*)R);
   return hipGetLastError();
 }
 
 hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wpr, long K_dim, int gpr, int nrb,
-                      int C, int c_off, int C_tot, int nw, void* Q, float4* SB, hipStream_t st) {
+                      int C, int c_off, int C_tot, void* R, hipStream_t st) {
   hipLaunchKernelGGL(k_tile_tern, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, wp, wpr, K_dim, D_out, nrb,
-                     C, c_off, C_tot, nw, (uint2*)Q);
+                     C, c_off, C_tot, (char*)R);
   hipLaunchKernelGGL(k_tile_tern_params, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales, gpr, D_out,
-                     nrb, C, c_off, C_tot, nw, SB);
+                     nrb, C, c_off, C_tot, (char*)R);
   return hipGetLastError();
 }
 
@@ -599,8 +641,8 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
 }
 
 hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
-  QMatDev a{G.q0, G.sb0, G.D_out0, 0};
-  QMatDev b{G.q1 ? G.q1 : G.q0, G.q1 ? G.sb1 : G.sb0, G.D_out1, G.D_out0};
+  QMatDev a{(const char*)G.rec0, G.D_out0, 0};
+  QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
   dim3 grid((unsigned)((items + 3) / 4));
 #define KQ_GEMV(QTV, MTV, SM)                                                                                       \

@@ -24,7 +24,7 @@ struct kans_qlayer {
   int Cb, Cw, C_tot;         // superchunks: basis, base, total
   int nw;                    // 16-row blocks per decode row group (qrow_blocks)
   int nrb_pad;               // 16-row blocks, padded to a multiple of nw
-  DevBuf Q, SB, bias;        // re-tiled weights, group parameters, bias (bias_dtype)
+  DevBuf R, bias;            // re-tiled records (codes + group parameters), bias (bias_dtype)
   int bias_dtype = DT_F32;
   // decode workspace: activation basis, its group sums, split-K partials
   DevBuf Phi, S, part;
@@ -41,9 +41,9 @@ constexpr int kMaxDecodeB = 32;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
 
-// Superchunk ranges per row group: ~10 work items (waves) per CU, at least 4
-// superchunks per item.
-int choose_ksplit(int n_rg, int C_tot) {
+// Superchunk ranges per row group: about items_per_cu work items (waves) per
+// CU, at least 4 superchunks per item.
+int choose_ksplit(int n_rg, int C_tot, int B, int quant) {
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
@@ -52,7 +52,8 @@ int choose_ksplit(int n_rg, int C_tot) {
       cus = prop.multiProcessorCount;
     if (cus <= 0) cus = 256;
   }
-  int ks = (10 * cus + n_rg - 1) / n_rg;
+  const int per_cu = items_per_cu(quant, B);
+  int ks = B <= kSmallB ? per_cu * cus / n_rg : (per_cu * cus + n_rg - 1) / n_rg;
   ks = std::min(ks, std::max(1, C_tot / 4));
   return std::max(ks, 1);
 }
@@ -95,13 +96,10 @@ int upload_tmp(DevBuf& d, const void* src, size_t bytes, hipStream_t st) {
 }
 
 int alloc_tiles(kans_qlayer* L) {
-  const size_t tiles = (size_t)L->nrb_pad * L->C_tot;
-  int rc = L->Q.reserve(tiles * 64 * (L->quant == Q_INT4 ? 16 : 8));
+  const size_t bytes = (size_t)(L->nrb_pad / L->nw) * L->C_tot * qrec_bytes(L->quant);
+  int rc = L->R.reserve(bytes);
   if (rc) return rc;
-  rc = L->SB.reserve(tiles * 16 * sizeof(float4));
-  if (rc) return rc;
-  HIP_TRY(hipMemsetAsync(L->Q.p, 0, tiles * 64 * (L->quant == Q_INT4 ? 16 : 8), kans_default_stream()));
-  HIP_TRY(hipMemsetAsync(L->SB.p, 0, tiles * 16 * sizeof(float4), kans_default_stream()));
+  HIP_TRY(hipMemsetAsync(L->R.p, 0, bytes, kans_default_stream()));
   return 0;
 }
 
@@ -148,11 +146,9 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hip
 // a->part ([ksplit][B][a.D_out + b.D_out]).
 int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, hipStream_t st) {
   QGemv G;
-  G.q0 = a->Q.p;
-  G.sb0 = (const float4*)a->SB.p;
+  G.rec0 = a->R.p;
   G.D_out0 = a->D_out;
-  G.q1 = b ? b->Q.p : nullptr;
-  G.sb1 = b ? (const float4*)b->SB.p : nullptr;
+  G.rec1 = b ? b->R.p : nullptr;
   G.D_out1 = b ? b->D_out : 0;
   G.nw = a->nw;
   G.rg_split = a->nrb_pad / a->nw;
@@ -183,7 +179,7 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   if (rc) return rc;
   if (!Y || ldy < L->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
   if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
-  const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot);
+  const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
   if ((rc = gemv_locked(L, nullptr, B, ks, st))) return rc;
@@ -200,8 +196,8 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if (!Y || ldy < d->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
   if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
   const int h = g->D_out;
-  const int ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot);
-  const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot);
+  const int ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot, B, g->quant);
+  const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot, B, d->quant);
   if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
   if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
@@ -253,7 +249,7 @@ int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bi
   if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
   if ((rc = upload_tmp(tb, biases, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
   hipError_t e = qtile_int4((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, pad_b / 2,
-                            (int)gpr_b, L->nrb_pad, L->Cb, 0, L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+                            (int)gpr_b, L->nrb_pad, L->Cb, 0, L->C_tot, L->R.p, st);
   if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
   if (has_base) {
     const long pad_w = ((long)D_in + group_size - 1) / group_size * group_size;
@@ -263,7 +259,7 @@ int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bi
     if ((rc = upload_tmp(ws, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
     if ((rc = upload_tmp(wb, biases_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
     e = qtile_int4((const unsigned char*)wq.p, (const float*)ws.p, (const float*)wb.p, D_out, pad_w / 2, (int)gpr_w,
-                   L->nrb_pad, L->Cw, L->Cb, L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+                   L->nrb_pad, L->Cw, L->Cb, L->C_tot, L->R.p, st);
     if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
     if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
     HIP_TRY(hipStreamSynchronize(st));  // temporaries die here
@@ -303,7 +299,7 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
   if ((rc = upload_tmp(tw, w_packed, (size_t)D_out * wpr_b * 4, st))) return fail(rc);
   if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
   hipError_t e = qtile_tern((const unsigned*)tw.p, (const float*)ts.p, D_out, wpr_b, kb, gpr_b, L->nrb_pad, L->Cb, 0,
-                            L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+                            L->C_tot, L->R.p, st);
   if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
   DevBuf bw, bs;
   if (has_base) {
@@ -312,7 +308,7 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
     if ((rc = upload_tmp(bw, w_packed_base, (size_t)D_out * wpr_w * 4, st))) return fail(rc);
     if ((rc = upload_tmp(bs, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
     e = qtile_tern((const unsigned*)bw.p, (const float*)bs.p, D_out, wpr_w, kw, gpr_w, L->nrb_pad, L->Cw, L->Cb,
-                   L->C_tot, L->nw, L->Q.p, (float4*)L->SB.p, st);
+                   L->C_tot, L->R.p, st);
     if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
   }
   if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
