@@ -348,14 +348,14 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // Two shapes: WAVES = 4 (tile 4*WM x NB*32, two workgroups per CU) and
 // WAVES = 8 with WM = 32, NB = 8 (tile 256 x 256, one workgroup of 8 waves
 // per CU).  The second halves the basis values a lane generates per MFMA
-// (8 values feed 8 MFMAs), which the exp2-based RBF and the B-spline need;
-// its two stages of 9 slots x 8 KB fill 144 KB of the 160 KB LDS.
+// (8 values feed 8 MFMAs); its two stages of up to 10 slots x 8 KB fill the
+// 160 KB LDS (9 slots with the RBF centre table).
 //
-// Requires KP = K + has_base <= block_slots(WAVES) (the launcher checks).
+// Requires KP = K + has_base <= block_slots(WAVES, BASIS) (the launcher checks).
 // ---------------------------------------------------------------------------
-constexpr int kBlockSlots = 10;   // WAVES = 4
-constexpr int kBlockSlots8 = 9;   // WAVES = 8
-__host__ __device__ constexpr int block_slots(int waves) { return waves == 8 ? kBlockSlots8 : kBlockSlots; }
+__host__ __device__ constexpr int block_slots(int waves, int basis) {
+  return waves == 8 && (basis == BASIS_RBF || basis == BASIS_RBF_TABLE) ? 9 : 10;
+}
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
 // (scheduling hint): per value 1 fma (Chebyshev), fma + mul + exp2 (RBF) or
@@ -379,12 +379,9 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   constexpr int SLOT = NB * 64;         // uint4 per slot of the N-tile
   typedef typename Mfma<T>::frag frag;
 
-  constexpr int SLOTS = block_slots(WAVES);
+  constexpr int SLOTS = block_slots(WAVES, BASIS);
   __shared__ uint4 stage0[SLOTS * SLOT];
   __shared__ uint4 stage1[SLOTS * SLOT];
-  // RBF: scaled centres s*c_k, entry K = 0 (read by the unused step after a
-  // block's last slot)
-  __shared__ float rbf_tab[BASIS == BASIS_RBF_TABLE ? kMaxK + 1 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -482,15 +479,17 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
 
   // ---- prologue: block fb_begin in stage0 and registers ----------------------
+  BasisGen<BASIS, NV> gen;
   if constexpr (BASIS == BASIS_RBF_TABLE) {
+    // scaled centres s*c_k, entry K = 0 (read by the unused step after a
+    // block's last slot)
+    __shared__ float rbf_tab[kMaxK + 1];
     if (tid <= bp.K) rbf_tab[tid] = tid < bp.K ? bp.rbf_sc[tid] : 0.0f;
+    gen.tab = rbf_tab;
   }
   dma(fb_begin, stage0);
   xload(fb_begin);
   __syncthreads();
-
-  BasisGen<BASIS, NV> gen;
-  if constexpr (BASIS == BASIS_RBF_TABLE) gen.tab = rbf_tab;
   frag af[2][RB], bf[NB];
   // One slot s of parity P, a single basic block: the MFMAs of slot s (on
   // af[P], bf) are interleaved with the basis values of slot s+1 (into
@@ -665,7 +664,7 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   // everything else (fp32, other tiles, larger K) -> the per-slot kernel.
   const int waves = block_waves(sizeof(T) == 2, BASIS, WM, NB, L.bp.K + L.has_base);
   constexpr bool kBlock4 = sizeof(T) == 2 && BASIS == BASIS_CHEBY && NB <= 4;
-  constexpr bool kBlock8 = sizeof(T) == 2 && (BASIS == BASIS_RBF || BASIS == BASIS_BSPLINE) && WM == 32 && NB == 8;
+  constexpr bool kBlock8 = sizeof(T) == 2 && WM == 32 && NB == 8;
   if (waves == 4) {
     if constexpr (kBlock4) {
       hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BASIS, WM, NB, 4>), grid, dim3(256), 0, st, (const TX*)L.X,
@@ -700,8 +699,9 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
 // Workgroup waves of the block kernel for this configuration, 0 when the
 // per-slot kernel runs (the routing of launch_dense_t).
 int block_waves(bool half, int basis, int wm, int nb, int KP) {
-  if (half && basis == BASIS_CHEBY && nb <= 4 && KP <= kBlockSlots) return 4;
-  if (half && (basis == BASIS_RBF || basis == BASIS_BSPLINE) && wm == 32 && nb == 8 && KP <= kBlockSlots8) return 8;
+  if (!half) return 0;
+  if (basis == BASIS_CHEBY && nb <= 4 && KP <= block_slots(4, basis)) return 4;
+  if (wm == 32 && nb == 8 && KP <= block_slots(8, basis)) return 8;
   return 0;
 }
 

@@ -71,7 +71,7 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st);
 hipError_t qreduce(const float* part, int ksplit, int B, int N, const void* bias, int bias_dtype, void* Y, int y_dtype,
                    long ldy, hipStream_t st);
 // hidden[m][i] = SiLU(gate) * up from the [gate | up] partials (+ biases), see k_qswiglu
-hipError_t qswiglu(const float* part, int ksplit, int B, int h, const void* bias_g, const void* bias_u, int bias_dtype,
-                   int round16, float* hidden, hipStream_t st);
+hipError_t qswiglu(const float* part, int ksplit, int B, int h, const void* bias_g, int bias_g_dtype,
+                   const void* bias_u, int bias_u_dtype, int round16, float* hidden, hipStream_t st);
 
 }  // namespace kans

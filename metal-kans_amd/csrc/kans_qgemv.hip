@@ -583,12 +583,13 @@ __global__ void __launch_bounds__(256) k_qreduce(const float* __restrict__ part,
 // round16 the gate and up layer outputs and the hidden state are rounded to
 // fp16 (1) / bf16 (2), as the layer dtype does in the unfused path.
 __global__ void k_qswiglu(const float* __restrict__ part, int ksplit, int B, int h, const void* bias_g,
-                          const void* bias_u, int bias_dtype, int round16, float* __restrict__ hidden) {
+                          const void* bias_u, int bias_g_dtype, int bias_u_dtype, int round16,
+                          float* __restrict__ hidden) {
   const long total = (long)B * h;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int m = (int)(idx / h), i = (int)(idx - (long)m * h);
-    float g = bias_g ? load_any(bias_g, i, bias_dtype) : 0.0f;
-    float u = bias_u ? load_any(bias_u, i, bias_dtype) : 0.0f;
+    float g = bias_g ? load_any(bias_g, i, bias_g_dtype) : 0.0f;
+    float u = bias_u ? load_any(bias_u, i, bias_u_dtype) : 0.0f;
     const float* p = part + (long)m * 2 * h;
     for (int k = 0; k < ksplit; ++k) {
       g += p[(long)k * B * 2 * h + i];
@@ -674,10 +675,10 @@ hipError_t qreduce(const float* part, int ksplit, int B, int N, const void* bias
   return hipGetLastError();
 }
 
-hipError_t qswiglu(const float* part, int ksplit, int B, int h, const void* bias_g, const void* bias_u, int bias_dtype,
-                   int round16, float* hidden, hipStream_t st) {
+hipError_t qswiglu(const float* part, int ksplit, int B, int h, const void* bias_g, int bias_g_dtype,
+                   const void* bias_u, int bias_u_dtype, int round16, float* hidden, hipStream_t st) {
   hipLaunchKernelGGL(k_qswiglu, dim3(grid_for((long)B * h)), dim3(256), 0, st, part, ksplit, B, h, bias_g, bias_u,
-                     bias_dtype, round16, hidden);
+                     bias_g_dtype, bias_u_dtype, round16, hidden);
   return hipGetLastError();
 }
 

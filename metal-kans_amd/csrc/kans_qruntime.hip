@@ -203,8 +203,8 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
   if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
   if ((rc = gemv_locked(g, u, B, ks1, st))) return rc;
-  HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr,
-                  u->has_bias ? u->bias.p : nullptr, g->bias_dtype, round16, (float*)G->hidden.p, st));
+  HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr, g->bias_dtype,
+                  u->has_bias ? u->bias.p : nullptr, u->bias_dtype, round16, (float*)G->hidden.p, st));
   if ((rc = prep_locked(d, G->hidden.p, DT_F32, h, B, st))) return rc;
   if ((rc = gemv_locked(d, nullptr, B, ks2, st))) return rc;
   HIP_TRY(qreduce((const float*)d->part.p, ks2, B, d->D_out, d->has_bias ? d->bias.p : nullptr, d->bias_dtype, Y,
@@ -360,8 +360,6 @@ int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kan
       down->D_in != gate->D_out || down->D_out != gate->D_in)
     return kans_fail(KANS_ERR_ARG, "shape mismatch: gate/up %dx%d, down %dx%d", gate->D_in, gate->D_out, down->D_in,
                      down->D_out);
-  if (gate->has_bias != up->has_bias || (gate->has_bias && gate->bias_dtype != up->bias_dtype))
-    return kans_fail(KANS_ERR_ARG, "gate and up must agree on bias");
   auto* G = new kans_gated();
   G->gate = gate;
   G->up = up;

@@ -301,18 +301,14 @@ int kans_layer_load_weights_device(kans_layer* L, const void* W, const void* W_b
 // split the feature blocks until ~512 workgroups exist.  Preference orders
 // come from MI355X timings at 16384 x 1024 -> 1024 (16-bit) and 8192 x 1024 ->
 // {1024, 4096} (fp32):
-//   16-bit Chebyshev  (64,4) -- the block-pipelined kernel;
-//   16-bit RBF        (32,8) -- 8 basis values per lane feed 8 MFMAs (exp2-bound
-//                               generation amortised over twice the columns);
-//   16-bit B-spline   (32,8) -- also keeps the generator state small;
-//   fp32 Chebyshev/RBF (32,4); fp32 B-spline (32,8).
+//   16-bit, every basis (32,8) -- the 8-wave block kernel: 8 basis values per
+//                                lane feed 8 MFMAs;
+//   fp32 Chebyshev / RBF (32,4); fp32 B-spline (32,8).
 static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
-  static const int pref_wide[4][2] = {{64, 4}, {32, 8}, {32, 4}, {32, 1}};
   static const int pref_n8[4][2] = {{32, 8}, {64, 4}, {32, 4}, {32, 1}};
   static const int pref_n4[4][2] = {{32, 4}, {64, 4}, {32, 8}, {32, 1}};
   const bool f32 = L->dtype == DT_F32;
-  const int(*cand)[2] = (L->basis == BASIS_BSPLINE || (!f32 && L->basis == BASIS_RBF)) ? pref_n8
-                        : f32 ? pref_n4 : pref_wide;
+  const int(*cand)[2] = (f32 && L->basis != BASIS_BSPLINE) ? pref_n4 : pref_n8;
   const int nob = (L->D_out + 31) / 32;
   auto tiles = [&](int ww, int nn) { return ((B + 4 * ww - 1) / (4 * ww)) * ((nob + nn - 1) / nn); };
   int bw = 32, bn = 1, bt = tiles(32, 1);  // (32, 1) always fits

@@ -101,10 +101,11 @@ def test_tilings_and_splits(gpu, wm, nb, splits, dtype, kind, K):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-@pytest.mark.parametrize("kind,K", [("rbf", 8), ("bspline", 8), ("rbf", 5), ("bspline", 6)])
+@pytest.mark.parametrize("kind,K", [("rbf", 8), ("bspline", 8), ("rbf", 5), ("bspline", 6), ("cheby", 9),
+                                    ("cheby", 4)])
 @pytest.mark.parametrize("base,bias", [(True, True), (False, False), (False, True)])
 def test_block_kernel_256x256_tile(gpu, dtype, kind, K, base, bias):
-    """16-bit RBF / B-spline on the (32, 8) tile take the 8-wave block kernel (K + base <= 9): ragged
+    """16-bit layers on the (32, 8) tile take the 8-wave block kernel (K + base <= 9 for RBF, 10 otherwise): ragged
     rows, a feature count that is not a multiple of 16, output columns that end inside an N-tile,
     with and without a feature split."""
     import metal_kans as mk

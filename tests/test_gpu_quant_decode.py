@@ -32,27 +32,31 @@ def _quant_tern(W):
     return (np.ascontiguousarray(p), np.ascontiguousarray(s, np.float32)), deq
 
 
-def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed):
+def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed, bias_dtype=DT_F32):
     rng = np.random.default_rng(seed)
     W = rng.normal(0, 0.05, (d_out, d_in * K)).astype(np.float32)
     Wb = rng.normal(0, 0.1, (d_out, d_in)).astype(np.float32) if base else None
     bv = rng.normal(0, 0.1, d_out).astype(np.float32) if bias else None
     h = ctypes.c_void_p()
-    bptr = bv.ctypes.data if bv is not None else None
+    bdev = None
+    if bv is not None:
+        bdev = bv.astype(np.float16) if bias_dtype == DT_F16 else bv
+        bv = bdev.astype(np.float32)   # the values the layer holds
+    bptr = bdev.ctypes.data if bdev is not None else None
     if fmt == "int4":
         pw, dW = _quant_int4(W)
         pb, dWb = _quant_int4(Wb) if base else ((None, None, None), None)
         keep = (pw, pb)
         rc = lib.kans_qlayer_create_int4(d_in, d_out, K, int(base), int(bias), 64,
                                          *[a.ctypes.data if a is not None else None for a in pw + pb],
-                                         bptr, DT_F32, ctypes.byref(h))
+                                         bptr, bias_dtype, ctypes.byref(h))
     else:
         pw, dW = _quant_tern(W)
         pb, dWb = _quant_tern(Wb) if base else ((None, None), None)
         keep = (pw, pb)
         rc = lib.kans_qlayer_create_ternary(d_in, d_out, K, int(base), int(bias), 32,
                                             *[a.ctypes.data if a is not None else None for a in pw + pb],
-                                            bptr, DT_F32, ctypes.byref(h))
+                                            bptr, bias_dtype, ctypes.byref(h))
     assert rc == 0, lib.kans_last_error()
     del keep
     return h, {"W": dW, "W_base": dWb, "bias": bv, "K": K}
@@ -104,14 +108,16 @@ def test_qlayer_rejects(gpu):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "ternary"])
-@pytest.mark.parametrize("B", [1, 8, 32])
-def test_gated_block_decode(gpu, fmt, B):
-    """Fused GatedKAN block vs down(SiLU(gate(x)) * up(x)) on dequantized weights."""
+@pytest.mark.parametrize("B,biased", [(1, False), (8, False), (32, False), (1, True), (17, True)])
+def test_gated_block_decode(gpu, fmt, B, biased):
+    """Fused GatedKAN block vs down(SiLU(gate(x)) * up(x)) on dequantized weights; the biased case
+    gives gate an fp32 bias, up an fp16 bias and down an fp32 bias."""
     lib = gpu
     d, hdim, K = 96, 200, 4
     layers, refs = [], []
     for i, (di, do) in enumerate(((d, hdim), (d, hdim), (hdim, d))):
-        h, r = make_qlayer(lib, fmt, di, do, K, True, False, seed=100 + i)
+        h, r = make_qlayer(lib, fmt, di, do, K, True, biased, seed=100 + i,
+                           bias_dtype=DT_F16 if (biased and i == 1) else DT_F32)
         layers.append(h)
         refs.append(r)
     blk = ctypes.c_void_p()
