@@ -151,6 +151,18 @@ int metal_kan_chain_pipeline_cheby(const float* X, float* Y, int B, int num_laye
                                    const int* degrees, const float** W_chebys, const float** W_bases,
                                    const float** biases);
 
+/* Chebyshev layer backward, fp32 host arrays (dY [B][D_out], X [B][D_in], W [D_out][D_in*degree],
+ * W_base [D_out][D_in]): dW_cheby, dW_base (has_base), dbias (has_bias) and dX, without a Phi buffer.
+ * Replaces metal_kan_cheby_backward_fused (device.py:369-374, metal_kan_bridge.mm:4532-4632) and
+ * metal_kan_cheby_backward (device.py:282-287, metal_kan_bridge.mm:2715), which compute the same
+ * gradients; T'_k is 0 where |x| > 1 (the clamp), degree <= 32. */
+int metal_kan_cheby_backward_fused(const float* dY, const float* X, const float* W_cheby, const float* W_base,
+                                   float* dW_cheby, float* dW_base, float* dbias, float* dX, int B, int D_in,
+                                   int D_out, int degree, int has_base, int has_bias);
+int metal_kan_cheby_backward(const float* dY, const float* X, const float* W_cheby, const float* W_base,
+                             float* dW_cheby, float* dW_base, float* dbias, float* dX, int B, int D_in, int D_out,
+                             int degree, int has_base, int has_bias);
+
 /* ======================================================================= *
  * Device-resident layer API (no reference counterpart: the reference has   *
  * unified memory and no device-resident objects).                          *
@@ -206,6 +218,12 @@ int kans_chain_forward_host_ex(kans_chain* chain, const void* X, int x_dtype, vo
 int kans_chain_forward(kans_chain* chain, const void* X, long ldx, void* Y, long ldy, int B, void* stream);
 /* mean ms per graph replay (include_copies: also the pinned H2D/D2H copies) */
 int kans_chain_time(kans_chain* chain, int B, int warmup, int iters, int include_copies, float* ms);
+
+/* Chebyshev layer backward on device fp32 arrays (no reference counterpart for device pointers; the
+ * host form is metal_kan_cheby_backward_fused), enqueued on `stream` (NULL = kans_stream()). */
+int kans_cheby_backward(const float* dY, const float* X, const float* W, const float* W_base, float* dW,
+                        float* dW_base, float* dbias, float* dX, int B, int D_in, int D_out, int K, int has_base,
+                        int has_bias, void* stream);
 
 /* bit-exact dequantizers on device pointers (stream NULL = kans_stream()); bits = 8 or 4 */
 int kans_dequantize_affine_device(const void* qweight, const float* scales, const float* biases, float* out,

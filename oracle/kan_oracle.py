@@ -17,6 +17,7 @@ It restates, in NumPy, what the reference computes on the hot path:
 * INT8/INT4 dequantizer     -- NumPy fallback ``quantization.py:136-148``
 * ternary (de)quantizer     -- NumPy fallback ``quantization.py:196-246,275-286``
 * GatedKAN block            -- ``metal_kans/gated_kan.py:15-16,86-138``
+* Chebyshev backward        -- ``metal_kan_bridge.mm:4532-4632``, ``fused_kan.metal:2053-2163``
 * SwiGLU kernel             -- ``fused_kan.metal:2284-2296``
 
 Two accumulation modes exist for the forward: ``acc=np.float64`` (the
@@ -184,6 +185,62 @@ def chain_forward(layers: Sequence[dict], x: np.ndarray, acc=np.float64,
     for L in layers:
         h = kan_forward(L["kind"], h, L["W"], L.get("W_base"), L.get("bias"), L["params"], acc, operands)
     return h
+
+
+def cheby_basis_deriv(x: np.ndarray, K: int, dtype=np.float64) -> np.ndarray:
+    """d/dx of phi_k(x) = T_k(clamp(x, -1, 1)), k < K, shape (B, D_in, K).
+
+    As the reference backward (fused_kan.metal:2098-2162): T'_0 = 0, T'_1 = 1,
+    T'_k = 2 T_{k-1} + 2t T'_{k-1} - T'_{k-2} at t = clamp(x), and 0 wherever the
+    raw input lies outside [-1, 1] (the clamp is flat there; x = +-1 counts as
+    inside).
+    """
+    x = np.asarray(x, dtype=dtype)
+    t = np.clip(x, -1.0, 1.0)
+    T = cheby_basis(x, K, dtype)
+    d = np.zeros(x.shape + (K,), dtype=dtype)
+    if K > 1:
+        d[..., 1] = 1.0
+    for k in range(2, K):
+        d[..., k] = 2.0 * T[..., k - 1] + 2.0 * t * d[..., k - 1] - d[..., k - 2]
+    d[(x < -1.0) | (x > 1.0)] = 0.0
+    return d
+
+
+def silu_deriv(x: np.ndarray) -> np.ndarray:
+    """d/dx x*sigmoid(x) = s (1 + x (1 - s)), s = sigmoid(x) (fused_kan.metal:2152-2153)."""
+    s = 1.0 / (1.0 + np.exp(-x))
+    return s * (1.0 + x * (1.0 - s))
+
+
+def cheby_backward(dY: np.ndarray, x: np.ndarray, W: np.ndarray, W_base: Optional[np.ndarray],
+                   has_bias: bool, acc=np.float64):
+    """Gradients of y = bias + SiLU(x) W_base^T + Phi W^T for a Chebyshev layer given dL/dy.
+
+    Returns (dW [D_out, D_in*K], dW_base [D_out, D_in] or None, dbias [D_out] or None,
+    dX [B, D_in]), the quantities of metal_kan_cheby_backward_fused
+    (metal_kan_bridge.mm:4532-4632; kernels fused_kan.metal:2053-2163):
+      dW[o, i*K+k]   = sum_b dY[b,o] T_k(clamp x[b,i])
+      dW_base[o, i]  = sum_b dY[b,o] SiLU(x[b,i])
+      dbias[o]       = sum_b dY[b,o]
+      dX[b, i]       = sum_k (dY W)[b, i*K+k] T'_k(x[b,i]) + (dY W_base)[b,i] SiLU'(x[b,i])
+    """
+    dY = np.asarray(dY, dtype=acc)
+    x = np.asarray(x, dtype=acc)
+    B, D_in = x.shape
+    D_out = dY.shape[1]
+    K = W.shape[1] // D_in
+    Wa = np.asarray(W, dtype=acc)
+    Phi = cheby_basis(x, K, acc).reshape(B, D_in * K)
+    dW = dY.T @ Phi
+    dPhi = (dY @ Wa).reshape(B, D_in, K)
+    dX = np.sum(dPhi * cheby_basis_deriv(x, K, acc), axis=2)
+    dWb = None
+    if W_base is not None:
+        dWb = dY.T @ silu(x)
+        dX = dX + (dY @ np.asarray(W_base, dtype=acc)) * silu_deriv(x)
+    db = dY.sum(axis=0) if has_bias else None
+    return dW, dWb, db, dX
 
 
 def silu_clipped(x: np.ndarray) -> np.ndarray:

@@ -253,3 +253,80 @@ def test_bf16_rounding():
     bits = O.bf16_round(v)
     np.testing.assert_array_equal(bits, [0x3F80, 0xC000, 0x3F80, 0x3F82, 0x7F80])  # ties to even
     np.testing.assert_array_equal(O.bf16_to_f32(bits)[:2], [1.0, -2.0])
+
+
+# ---- Chebyshev backward --------------------------------------------------------
+
+def test_cheby_derivative_closed_form():
+    """T'_k(cos t) = k sin(k t) / sin t inside (-1, 1); T'_k(+-1) = (+-1)^(k+1) k^2; 0 outside."""
+    th = np.linspace(0.05, np.pi - 0.05, 37)
+    d = O.cheby_basis_deriv(np.cos(th), 12)
+    for k in range(12):
+        np.testing.assert_allclose(d[:, k], k * np.sin(k * th) / np.sin(th), rtol=1e-10, atol=1e-10)
+    e = O.cheby_basis_deriv(np.array([1.0, -1.0, 1.3, -2.0]), 9)
+    ks = np.arange(9)
+    np.testing.assert_allclose(e[0], ks ** 2)
+    np.testing.assert_allclose(e[1], (-1.0) ** (ks + 1) * ks ** 2)
+    assert not e[2:].any()
+
+
+def test_silu_derivative_matches_difference_quotient():
+    x = np.linspace(-8, 8, 41)
+    h = 1e-6
+    np.testing.assert_allclose(O.silu_deriv(x), (O.silu(x + h) - O.silu(x - h)) / (2 * h), rtol=1e-7, atol=1e-9)
+
+
+@pytest.mark.parametrize("base,bias", [(True, True), (False, False)])
+def test_cheby_backward_matches_finite_differences(base, bias):
+    """Every gradient of L = sum(y * dY) against central differences of the float64 forward, with
+    inputs inside (-1, 1) and outside it (where the clamp makes the basis flat)."""
+    rng = np.random.default_rng(5)
+    B, Di, Do, K = 5, 4, 3, 6
+    x = rng.uniform(-0.95, 0.95, (B, Di))
+    x[0, 1], x[3, 2] = 1.4, -1.7
+    W = rng.normal(0, 1, (Do, Di * K))
+    Wb = rng.normal(0, 1, (Do, Di)) if base else None
+    bv = rng.normal(0, 1, Do) if bias else None
+    dY = rng.normal(0, 1, (B, Do))
+    dW, dWb, db, dX = O.cheby_backward(dY, x, W, Wb, bias)
+
+    def loss(x_, W_, Wb_, b_):
+        return float(np.sum(O.kan_forward("cheby", x_, W_, Wb_, b_, {"K": K}) * dY))
+
+    def num(arr, f):
+        g = np.zeros_like(arr)
+        h = 1e-6
+        for idx in np.ndindex(arr.shape):
+            a, b = arr.copy(), arr.copy()
+            a[idx] += h
+            b[idx] -= h
+            g[idx] = (f(a) - f(b)) / (2 * h)
+        return g
+
+    np.testing.assert_allclose(dX, num(x, lambda a: loss(a, W, Wb, bv)), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(dW, num(W, lambda a: loss(x, a, Wb, bv)), rtol=1e-6, atol=1e-7)
+    if base:
+        np.testing.assert_allclose(dWb, num(Wb, lambda a: loss(x, W, a, bv)), rtol=1e-6, atol=1e-7)
+    else:
+        assert dWb is None
+    if bias:
+        np.testing.assert_allclose(db, num(bv, lambda a: loss(x, W, Wb, a)), rtol=1e-6, atol=1e-7)
+    else:
+        assert db is None
+
+
+def test_cheby_backward_brute_force_loops():
+    rng = np.random.default_rng(9)
+    B, Di, Do, K = 3, 2, 2, 4
+    x = rng.uniform(-1, 1, (B, Di))
+    W = rng.normal(0, 1, (Do, Di * K))
+    Wb = rng.normal(0, 1, (Do, Di))
+    dY = rng.normal(0, 1, (B, Do))
+    dW, dWb, db, dX = O.cheby_backward(dY, x, W, Wb, True)
+    for o in range(Do):
+        for i in range(Di):
+            for k in range(K):
+                ref = sum(dY[b, o] * np.cos(k * np.arccos(x[b, i])) for b in range(B))
+                assert abs(dW[o, i * K + k] - ref) < 1e-12
+            assert abs(dWb[o, i] - sum(dY[b, o] * x[b, i] / (1 + np.exp(-x[b, i])) for b in range(B))) < 1e-12
+        assert abs(db[o] - dY[:, o].sum()) < 1e-12
