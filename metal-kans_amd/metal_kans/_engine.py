@@ -68,6 +68,7 @@ class LayerEngine:
         self.dt = None
         self.params = None
         self.snaps: Optional[Sequence[_Snapshot]] = None
+        self.dev_key: Optional[tuple] = None
         self.tiling = (0, 0, 0)
 
     def __del__(self):
@@ -79,6 +80,7 @@ class LayerEngine:
 
     def invalidate(self) -> None:
         self.snaps = None
+        self.dev_key = None
 
     def _ensure_handle(self, dt: int) -> ctypes.CDLL:
         lib = device.get_metal_bridge()
@@ -94,6 +96,7 @@ class LayerEngine:
         self.dt = dt
         self.params = None
         self.snaps = None
+        self.dev_key = None
         if self.tiling != (0, 0, 0):
             device.check(lib.kans_layer_set_tiling(self.handle, *self.tiling), "kans_layer_set_tiling")
         return lib
@@ -109,10 +112,7 @@ class LayerEngine:
         """As ``prepare`` with float32 host arrays converted on the device to dtype ``dt``."""
         self.prepare(dt, W, W_base, bias, params, src_f32=True)
 
-    def prepare(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
-                params: tuple, src_f32: bool = False) -> None:
-        """Make the device copy current: handle for dtype, basis params, weights."""
-        lib = self._ensure_handle(dt)
+    def _set_params(self, lib, params: tuple) -> None:
         if params != self.params:
             if self.basis == "rbf":
                 centers = np.ascontiguousarray(params[0], dtype=np.float32)
@@ -122,6 +122,27 @@ class LayerEngine:
                 device.check(lib.kans_layer_set_bspline(self.handle, int(params[0]), float(params[1]),
                                                         float(params[2])), "kans_layer_set_bspline")
             self.params = params
+
+    def prepare_device(self, dt: int, W_ptr: int, W_base_ptr: Optional[int], bias_ptr: Optional[int],
+                       params: tuple, key: tuple) -> None:
+        """Make the device copy current from device arrays in dtype ``dt`` (e.g. torch tensors); ``key``
+        identifies their contents (pointers and version counters): equal keys skip the re-tiling.  The
+        caller has finished writing the arrays (the upload runs on the library's stream)."""
+        lib = self._ensure_handle(dt)
+        self._set_params(lib, params)
+        if self.snaps is None and self.dev_key == key:
+            return
+        device.check(lib.kans_layer_load_weights_device(self.handle, W_ptr, W_base_ptr, bias_ptr),
+                     "kans_layer_load_weights_device")
+        self.snaps = None
+        self.dev_key = key
+
+    def prepare(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
+                params: tuple, src_f32: bool = False) -> None:
+        """Make the device copy current: handle for dtype, basis params, weights."""
+        lib = self._ensure_handle(dt)
+        self._set_params(lib, params)
+        self.dev_key = None
         arrays = (W, W_base if self.has_base else None, bias if self.has_bias else None)
         if self.snaps is not None and all(s.same(a) for s, a in zip(self.snaps, arrays)):
             return
