@@ -20,6 +20,9 @@ enum Basis { BASIS_CHEBY = 0, BASIS_RBF = 1, BASIS_BSPLINE = 2 };
 // read from a table in LDS (BasisGen<BASIS_RBF_TABLE>); the public API never
 // sees it.
 constexpr int BASIS_RBF_TABLE = 3;
+// Kernel-only basis id: the Chebyshev basis of BASIS_CHEBY, advanced in place
+// with each step emitting the value it just computed (BasisGen<BASIS_CHEBY_POST>).
+constexpr int BASIS_CHEBY_POST = 4;
 enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -130,6 +133,46 @@ template <int NV> struct BasisGen<BASIS_CHEBY, NV> {
       v1[v] = r1[v];
       r0[v] = __builtin_fmaf(tw[v], r1[v], -r0[v]);
       r1[v] = __builtin_fmaf(tw[v], r0[v], -r1[v]);
+    }
+  }
+};
+
+// Chebyshev T_k(clamp(x,-1,1)) as BasisGen<BASIS_CHEBY>, but each step first
+// advances its register and then emits the fresh value: step<P> does
+// r_P <- 2t r_{1-P} - r_P and returns r_P, so the emitted value is the result
+// of the step's own fma and no copy of the previous value has to stay alive.
+// Before the first step the registers hold T_{-2} = T_2 = 2t^2 - 1 and
+// T_{-1} = T_1 = t (T_{-k} = T_k), which yields T_0 = 2t*t - (2t^2 - 1) and
+// T_1 = 2t*T_0 - t; both are within an fp32 rounding of 1 and t, far below
+// the 16-bit rounding of the MFMA operands this generator feeds.
+template <int NV> struct BasisGen<BASIS_CHEBY_POST, NV> {
+  float tw[NV], r0[NV], r1[NV];
+  __device__ __forceinline__ void begin(const float* x, const BasisParams&, bool swap = false) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float t = __builtin_fminf(__builtin_fmaxf(x[v], -1.0f), 1.0f);
+      tw[v] = t + t;
+      const float tm2 = __builtin_fmaf(tw[v], t, -1.0f);
+      r0[v] = swap ? t : tm2;
+      r1[v] = swap ? tm2 : t;
+    }
+  }
+  template <int P>
+  __device__ __forceinline__ void step(int, const BasisParams&, float* v0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      // the empty asm makes the fp32 result opaque, so the packing reads it
+      // instead of recomputing the fma with a 16-bit result (v_fma_mix), which
+      // would keep the previous value alive and cost a register copy per value
+      if constexpr (P == 0) {
+        r0[v] = __builtin_fmaf(tw[v], r1[v], -r0[v]);
+        asm volatile("" : "+v"(r0[v]));
+        v0[v] = r0[v];
+      } else {
+        r1[v] = __builtin_fmaf(tw[v], r0[v], -r1[v]);
+        asm volatile("" : "+v"(r1[v]));
+        v0[v] = r1[v];
+      }
     }
   }
 };

@@ -104,7 +104,10 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a scalar: the compiler cannot see that tid >> 6 is uniform
+  // per wave, and would otherwise keep wave-derived loop counters and
+  // addresses in vector registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tiles = m_tiles * n_tiles;
   const int lin = xcd_remap(blockIdx.x, tiles);
   const int n_tile = lin / m_tiles;
@@ -362,7 +365,8 @@ __host__ __device__ constexpr int block_slots(int waves, int basis) {
 // ~6 compares / selects (B-spline), plus the fp32 -> 16-bit packing.
 template <int BASIS, int NV, int MFMAS>
 constexpr int kValuPerMfma =
-    ((BASIS == BASIS_CHEBY ? 1 : BASIS == BASIS_BSPLINE ? 6 : 3) * NV + NV / 2 + MFMAS - 1) / MFMAS;
+    ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1 : BASIS == BASIS_BSPLINE ? 6 : 3) * NV + NV / 2 +
+     MFMAS - 1) / MFMAS;
 
 template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64, WAVES == 4 ? 2 : 1)
@@ -385,7 +389,10 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a scalar: the compiler cannot see that tid >> 6 is uniform
+  // per wave, and would otherwise keep wave-derived loop counters and
+  // addresses in vector registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int m_tile, n_tile;
   tile_of(xcd_remap(blockIdx.x, m_tiles * n_tiles), m_tiles, n_tiles, m_tile, n_tile);
   const int split = blockIdx.y;
@@ -457,7 +464,9 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
           }
         }
       }
-    if (f0 + 8 > D_in) {
+    // only the last feature block can reach past D_in: a wave-uniform test
+    // keeps the per-lane masking out of every other block
+    if ((fbx + 1) * 16 > D_in) {
 #pragma unroll
       for (int j = 0; j < NV; ++j)
         if (f0 + (j & 7) >= D_in) xf[j] = 0.0f;
@@ -522,6 +531,11 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       }
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                     // DS read
     }
+    // Chebyshev: nothing crosses into the next slot (otherwise the scheduler
+    // sinks this slot's B-fragment reads into the next one, which then waits
+    // on LDS latency before its MFMAs; measured 3-4 % faster).  The RBF and
+    // B-spline schedules measured better without the fence.
+    if constexpr (BASIS == BASIS_CHEBY_POST) __builtin_amdgcn_sched_barrier(0);
   };
   auto block = [&](int fb, const uint4* cur, uint4* nxt) {
     float xf[NV];
@@ -667,13 +681,14 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   constexpr bool kBlock8 = sizeof(T) == 2 && WM == 32 && NB == 8;
   if (waves == 4) {
     if constexpr (kBlock4) {
-      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BASIS, WM, NB, 4>), grid, dim3(256), 0, st, (const TX*)L.X,
+      constexpr int BB = BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS;
+      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 4>), grid, dim3(256), 0, st, (const TX*)L.X,
                          L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
                          L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
     }
   } else if (waves == 8) {
     if constexpr (kBlock8) {
-      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_TABLE : BASIS;
+      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_TABLE : BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS;
       const int m_tiles8 = (L.B + 8 * WM - 1) / (8 * WM);
       hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8>), dim3(m_tiles8 * n_tiles, splits), dim3(512), 0,
                          st, (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy,
