@@ -43,6 +43,32 @@ struct QPrep {
   float2* S;       // [C_tot][MP] (INT4 only; may be null for ternary)
 };
 
+// What a small-batch decode GEMV does after its split-K partial sums are
+// written (k_qgemv).  QEPI_PART stops there (separate kernels reduce them);
+// QEPI_SWIGLU (GatedKAN gate | up, matrices 0 / 1 with h rows each): the last
+// wave to finish output group j = gate row group j + up row group j (features
+// 64j .. 64j+63; arrivals counted in `counters`) reduces the group's partials
+// itself into hidden = SiLU(gate + bias) * (up + bias_u), as k_qswiglu, and
+// writes the down layer's activation basis Phi2 / S2 for those features, as
+// k_prep would compute it from hidden.  This replaces two kernel launches; the
+// last wave pays two memory round trips (its own stores, the arrival count)
+// before it reads 2 * ksplit partials per feature in batches of 8.
+enum QEpiKind { QEPI_PART = 0, QEPI_SWIGLU = 2 };
+constexpr int kMaxEpiSplit = 64;
+
+struct QEpi {
+  int kind = QEPI_PART;
+  int* counters = nullptr;   // one per output group, 0 between launches
+  const void* bias = nullptr;  // gate bias
+  int bias_dtype = 0;
+  const void* bias_u = nullptr;  // up bias
+  int bias_u_dtype = 0;
+  int round16 = 0;           // rounding of gate / up / hidden, as k_qswiglu
+  int K2 = 0, has_base2 = 0, Cb2 = 0, C_tot2 = 0;  // down layer's basis geometry
+  _Float16* Phi2 = nullptr;  // down layer's Phi / S (layout of QPrep)
+  float2* S2 = nullptr;
+};
+
 // One decode GEMV launch over one matrix or two matrices sharing the
 // activations (GatedKAN gate | up), see k_qgemv.
 struct QGemv {
@@ -58,6 +84,7 @@ struct QGemv {
   int B, MP;
   float* part;     // [ksplit][B][N_total] partial sums (matrix 1's columns after matrix 0's)
   int N_total;
+  QEpi epi;        // B <= kSmallB only
 };
 
 // Re-tile a packed matrix (C superchunks starting at superchunk c_off) into the records R.

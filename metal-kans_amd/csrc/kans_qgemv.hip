@@ -217,6 +217,20 @@ __device__ __forceinline__ float silu_clip(float g) {
   return g / (1.0f + __expf(-c));
 }
 
+// fp32 -> 16-bit of a value first materialised in fp32.  Without the opaque
+// register the compiler may fold the producing fma / multiply and the
+// conversion into one v_fma_mixlo_f16 (a single rounding) in one kernel and
+// not in another, and the decode kernels that must agree bit for bit
+// (k_prep / k_qswiglu and the fused GEMV epilogues) would not.
+__device__ __forceinline__ _Float16 half_of(float v) {
+  asm volatile("" : "+v"(v));
+  return (_Float16)v;
+}
+__device__ __forceinline__ float round16_of(float v, int mode) {
+  asm volatile("" : "+v"(v));
+  return mode == 2 ? to_f32(from_f32<__bf16>(v)) : (float)(_Float16)v;
+}
+
 __device__ __forceinline__ float load_any(const void* p, long i, int dt) {
   if (dt == DT_F32) return reinterpret_cast<const float*>(p)[i];
   if (dt == DT_F16) return (float)reinterpret_cast<const _Float16*>(p)[i];
@@ -278,7 +292,7 @@ __global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in
   float sum = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    hv[e] = (_Float16)v[e];
+    hv[e] = half_of(v[e]);
     sum += (float)hv[e];
   }
   if (live && m < MP) *reinterpret_cast<uint4*>(Phi + (long)m * C_tot * 128 + p0) = *reinterpret_cast<uint4*>(hv);
@@ -343,17 +357,149 @@ struct QMatDev {
   int col_off;          // column offset of this matrix in the output / workspace
 };
 
+// ---------------------------------------------------------------------------
+// Fused epilogue (QEpi).  The partial sums of the fused launches are written
+// through to memory with agent-scope atomic stores and read back with
+// agent-scope atomic loads, which bypass the per-XCD L2 caches; ordering them
+// against the arrival counter then takes only a wait for this wave's memory
+// operations, where agent-scope fences would write back / invalidate the whole
+// L2 of the XCD.
+// ---------------------------------------------------------------------------
+constexpr int kWaitVmem = 0 | (0x7 << 4) | (0xf << 8);  // s_waitcnt vmcnt(0) only
+
+__device__ __forceinline__ void part_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts this wave's arrival at counter *c; true for the last of `need`
+// arrivals, which also resets the counter for the next launch.  Every wave of
+// the group arrives exactly once per launch and none waits for another.
+__device__ __forceinline__ bool last_arrival(int* c, int need, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);  // this wave's partial stores are complete
+  int old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0);
+  if (old != need - 1) return false;
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (lane == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// Writes 8-blocks [b_lo, b_hi) of one Phi row from the staged values st (local
+// index i < n_st; 0 past it), index p0 = p_lo + 8b, in the unpack order of the
+// weight format; INT4 also writes the group sums of the fp16 values (groups of
+// 64 = 8 blocks, summed as k_prep does).
+template <int QT>
+__device__ __forceinline__ void epi_write_blocks(const _Float16* st, int n_st, long p_lo, int nblk, _Float16* phi_row,
+                                                 float* S2f, int MP, int m, int lane) {
+  for (int b0 = 0; b0 < nblk; b0 += 64) {
+    const int b = b0 + lane;
+    const bool live = b < nblk;
+    _Float16 hv[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * b + unpack_order<QT>(e);
+      hv[e] = live && i < n_st ? st[i] : (_Float16)0.0f;
+      sum += (float)hv[e];
+    }
+    const long p0 = p_lo + 8L * b;
+    if (live) *reinterpret_cast<uint4*>(phi_row + p0) = *reinterpret_cast<uint4*>(hv);
+    if constexpr (QT == Q_INT4) {
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+      if (live && (b & 7) == 0) {
+        const long G = p0 >> 6;
+        S2f[((G >> 1) * MP + m) * 2 + (G & 1)] = sum;
+      }
+    }
+  }
+}
+
+// QEPI_SWIGLU for feature group j (lane = feature 64j + lane): hidden as
+// k_qswiglu (same sum order and rounding), then T_k(clamp(hidden)) and
+// SiLU(hidden) into the next layer's Phi / S as k_prep.  The group covering
+// the last features also writes the zero padding up to each segment's end.
+template <int QT>
+__device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int ksplit, int B, int MP, int h, int j,
+                                           int n_groups, _Float16* st, int lane) {
+  const int f = j * 64 + lane;
+  const int K2 = E.K2;
+  const long total = (long)B * 2 * h;
+  const long ldphi2 = (long)E.C_tot2 * 128;
+  const bool last = j == n_groups - 1;
+  const long pb_lo = (long)j * 64 * K2;
+  const long pb_hi = last ? (long)E.Cb2 * 128 : pb_lo + 64L * K2;
+  const long pw_lo = (long)E.Cb2 * 128 + 64L * j;
+  const long pw_hi = last ? ldphi2 : pw_lo + 64;
+  float* S2f = reinterpret_cast<float*>(E.S2);
+  for (int m = 0; m < B; ++m) {
+    float hvv = 0.0f;
+    if (f < h) {
+      float g = E.bias ? load_any(E.bias, f, E.bias_dtype) : 0.0f;
+      float u = E.bias_u ? load_any(E.bias_u, f, E.bias_u_dtype) : 0.0f;
+      const float* p = part + (long)m * 2 * h + f;
+      for (int k0 = 0; k0 < ksplit; k0 += 8) {
+        float vg[8], vu[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          vg[q] = k0 + q < ksplit ? part_load(p + (long)(k0 + q) * total) : 0.f;
+          vu[q] = k0 + q < ksplit ? part_load(p + (long)(k0 + q) * total + h) : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (k0 + q < ksplit) {
+            g += vg[q];
+            u += vu[q];
+          }
+      }
+      if (E.round16) {
+        g = round16_of(g, E.round16);
+        u = round16_of(u, E.round16);
+      }
+      hvv = silu_clip(g) * u;
+      if (E.round16) hvv = round16_of(hvv, E.round16);
+    }
+    // stage T_0 .. T_{K2-1} at lane*K2 + k and SiLU at 64*K2 + lane (0 past h)
+    const float t = fminf(fmaxf(hvv, -1.0f), 1.0f);
+    float a = 1.0f, bb = t;
+    for (int k = 0; k < K2; ++k) {
+      float v = k == 0 ? a : bb;
+      if (k >= 2) {
+        const float c = __builtin_fmaf(2.0f * t, bb, -a);
+        a = bb;
+        bb = c;
+        v = c;
+      }
+      st[lane * K2 + k] = f < h ? half_of(v) : (_Float16)0.0f;
+    }
+    st[64 * K2 + lane] = f < h && E.has_base2 ? half_of(silu_f32(hvv)) : (_Float16)0.0f;
+    asm volatile("" ::: "memory");  // LDS writes before the reads below (one wave, in order)
+    _Float16* row = E.Phi2 + (long)m * ldphi2;
+    epi_write_blocks<QT>(st, 64 * K2, pb_lo, (int)((pb_hi - pb_lo) / 8), row, S2f, MP, m, lane);
+    if (E.has_base2) epi_write_blocks<QT>(st + 64 * K2, 64, pw_lo, (int)((pw_hi - pw_lo) / 8), row, S2f, MP, m, lane);
+    asm volatile("" ::: "memory");  // reads done before the next row's writes
+  }
+}
+
 // One wave = kQNW row blocks (64 output rows) x one contiguous superchunk range
 // (split-K over waves for memory-level parallelism); 4 independent waves per
 // workgroup.  part[ks][m][col] (m < B) receives the wave's partial sums.
 // SMALL (B <= kSmallB): batch row m lives only in accumulator register m of
 // lanes 0-15, so the per-group epilogue updates just those registers.
 
-template <int QT, int MT, bool SMALL>
+template <int QT, int MT, bool SMALL, int EPI>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
                                                const float2* __restrict__ S, int B, int MP,
-                                               float* __restrict__ part, int N_total) {
+                                               float* __restrict__ part, int N_total, QEpi E) {
+  static_assert(EPI == QEPI_PART || SMALL, "fused epilogues are for the small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -543,9 +689,18 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 #pragma unroll
         for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
           const int mm = mt * 16 + 4 * q + i;
-          if (mm < B) part[((long)ks * B + mm) * N_total + M.col_off + n] = acc[mt][w][i];
+          if (mm < B) {
+            float* dst = part + ((long)ks * B + mm) * N_total + M.col_off + n;
+            if constexpr (EPI == QEPI_PART) *dst = acc[mt][w][i];
+            else part_store(dst, acc[mt][w][i]);
+          }
         }
     }
+  }
+  if constexpr (EPI == QEPI_SWIGLU) {
+    __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
+    if (!last_arrival(E.counters + rg_loc, 2 * ksplit, lane)) return;
+    epi_swiglu<QT>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stage[threadIdx.x >> 6], lane);
   }
 }
 
@@ -562,8 +717,16 @@ __global__ void __launch_bounds__(256) k_qreduce(const float* __restrict__ part,
   const long total = (long)B * N;
   float sum = 0.0f;
   if (n < N) {
+    // splits g, g+4, ... in order, loaded 8 at a time (one memory round trip each)
     const float* p = part + (long)m * N + n;
-    for (int k = g; k < ksplit; k += 4) sum += p[(long)k * total];
+    for (int k0 = g; k0 < ksplit; k0 += 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = k0 + 4 * u < ksplit ? p[(long)(k0 + 4 * u) * total] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + 4 * u < ksplit) sum += v[u];
+    }
   }
   red[g][col] = sum;
   __syncthreads();
@@ -590,18 +753,27 @@ __global__ void k_qswiglu(const float* __restrict__ part, int ksplit, int B, int
     const int m = (int)(idx / h), i = (int)(idx - (long)m * h);
     float g = bias_g ? load_any(bias_g, i, bias_g_dtype) : 0.0f;
     float u = bias_u ? load_any(bias_u, i, bias_u_dtype) : 0.0f;
-    const float* p = part + (long)m * 2 * h;
-    for (int k = 0; k < ksplit; ++k) {
-      g += p[(long)k * B * 2 * h + i];
-      u += p[(long)k * B * 2 * h + h + i];
+    const float* p = part + (long)m * 2 * h + i;
+    for (int k0 = 0; k0 < ksplit; k0 += 8) {
+      float vg[8], vu[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        vg[q] = k0 + q < ksplit ? p[(long)(k0 + q) * B * 2 * h] : 0.f;
+        vu[q] = k0 + q < ksplit ? p[(long)(k0 + q) * B * 2 * h + h] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (k0 + q < ksplit) {
+          g += vg[q];
+          u += vu[q];
+        }
     }
-    auto rnd = [&](float v) { return round16 == 2 ? to_f32(from_f32<__bf16>(v)) : (float)(_Float16)v; };
     if (round16) {
-      g = rnd(g);
-      u = rnd(u);
+      g = round16_of(g, round16);
+      u = round16_of(u, round16);
     }
     float hv = silu_clip(g) * u;
-    if (round16) hv = rnd(hv);
+    if (round16) hv = round16_of(hv, round16);
     hidden[idx] = hv;
   }
 }
@@ -646,15 +818,26 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
   dim3 grid((unsigned)((items + 3) / 4));
-#define KQ_GEMV(QTV, MTV, SM)                                                                                       \
-  hipLaunchKernelGGL((k_qgemv<QTV, MTV, SM>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit, G.C_tot, \
-                     G.Phi, G.S, G.B, G.MP, G.part, G.N_total)
+#define KQ_GEMV(QTV, MTV, SM, EP)                                                                               \
+  hipLaunchKernelGGL((k_qgemv<QTV, MTV, SM, EP>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,      \
+                     G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi)
   const int mt = G.MP / 16;
   const bool small = G.B <= kSmallB;
+  const int ep = G.epi.kind;
+  if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
+    return hipErrorInvalidValue;
   if (qt == Q_INT4) {
-    if (small) KQ_GEMV(Q_INT4, 1, true); else if (mt == 1) KQ_GEMV(Q_INT4, 1, false); else KQ_GEMV(Q_INT4, 2, false);
+    if (small) {
+      if (ep == QEPI_SWIGLU) KQ_GEMV(Q_INT4, 1, true, QEPI_SWIGLU);
+      else KQ_GEMV(Q_INT4, 1, true, QEPI_PART);
+    } else if (mt == 1) KQ_GEMV(Q_INT4, 1, false, QEPI_PART);
+    else KQ_GEMV(Q_INT4, 2, false, QEPI_PART);
   } else {
-    if (small) KQ_GEMV(Q_TERN, 1, true); else if (mt == 1) KQ_GEMV(Q_TERN, 1, false); else KQ_GEMV(Q_TERN, 2, false);
+    if (small) {
+      if (ep == QEPI_SWIGLU) KQ_GEMV(Q_TERN, 1, true, QEPI_SWIGLU);
+      else KQ_GEMV(Q_TERN, 1, true, QEPI_PART);
+    } else if (mt == 1) KQ_GEMV(Q_TERN, 1, false, QEPI_PART);
+    else KQ_GEMV(Q_TERN, 2, false, QEPI_PART);
   }
 #undef KQ_GEMV
   return hipGetLastError();

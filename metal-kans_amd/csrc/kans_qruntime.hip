@@ -28,6 +28,7 @@ struct kans_qlayer {
   int bias_dtype = DT_F32;
   // decode workspace: activation basis, its group sums, split-K partials
   DevBuf Phi, S, part;
+  DevBuf cnt;                // arrival counters of the fused epilogues, one per row group (0 between launches)
 };
 
 struct kans_gated {
@@ -38,6 +39,10 @@ struct kans_gated {
 namespace {
 
 constexpr int kMaxDecodeB = 32;
+
+// GatedKAN at small batches: SwiGLU and the down layer's basis in the
+// gate|up GEMV's epilogue (QEPI_SWIGLU) instead of k_qswiglu + k_prep.
+bool g_fused_swiglu = true;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
 
@@ -100,6 +105,9 @@ int alloc_tiles(kans_qlayer* L) {
   int rc = L->R.reserve(bytes);
   if (rc) return rc;
   HIP_TRY(hipMemsetAsync(L->R.p, 0, bytes, kans_default_stream()));
+  const size_t cbytes = (size_t)(L->nrb_pad / L->nw) * sizeof(int);
+  if ((rc = L->cnt.reserve(cbytes))) return rc;
+  HIP_TRY(hipMemsetAsync(L->cnt.p, 0, cbytes, kans_default_stream()));
   return 0;
 }
 
@@ -143,8 +151,8 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hip
 }
 
 // GEMV of layer a (and b, sharing a's activations): split-K partial sums in
-// a->part ([ksplit][B][a.D_out + b.D_out]).
-int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, hipStream_t st) {
+// a->part ([ksplit][B][a.D_out + b.D_out]), then the epilogue `epi`.
+int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, hipStream_t st) {
   QGemv G;
   G.rec0 = a->R.p;
   G.D_out0 = a->D_out;
@@ -161,7 +169,17 @@ int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, hipStream_t s
   G.MP = mp_of(B);
   G.part = (float*)a->part.p;
   G.N_total = a->D_out + (b ? b->D_out : 0);
+  G.epi = epi;
   HIP_TRY(qgemv(a->quant, G, st));
+  return 0;
+}
+
+// GEMV of layer L on its prepared Phi / S, then the split-K reduce + bias into Y.
+int gemv_reduce_locked(kans_qlayer* L, int B, int ks, void* Y, int y_dtype, long ldy, hipStream_t st) {
+  int rc = gemv_locked(L, nullptr, B, ks, QEpi{}, st);
+  if (rc) return rc;
+  HIP_TRY(qreduce((const float*)L->part.p, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y,
+                  y_dtype, ldy, st));
   return 0;
 }
 
@@ -182,10 +200,7 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
-  if ((rc = gemv_locked(L, nullptr, B, ks, st))) return rc;
-  HIP_TRY(qreduce((const float*)L->part.p, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y,
-                  y_dtype, ldy, st));
-  return 0;
+  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, st);
 }
 
 int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
@@ -200,16 +215,32 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot, B, d->quant);
   if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
-  if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
   if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
-  if ((rc = gemv_locked(g, u, B, ks1, st))) return rc;
+  if (g_fused_swiglu && B <= kSmallB && ks1 <= kMaxEpiSplit) {
+    // gate|up GEMV -> (SwiGLU, down layer's basis) in its epilogue
+    QEpi e1;
+    e1.kind = QEPI_SWIGLU;
+    e1.counters = (int*)g->cnt.p;
+    e1.bias = g->has_bias ? g->bias.p : nullptr;
+    e1.bias_dtype = g->bias_dtype;
+    e1.bias_u = u->has_bias ? u->bias.p : nullptr;
+    e1.bias_u_dtype = u->bias_dtype;
+    e1.round16 = round16;
+    e1.K2 = d->K;
+    e1.has_base2 = d->has_base;
+    e1.Cb2 = d->Cb;
+    e1.C_tot2 = d->C_tot;
+    e1.Phi2 = (_Float16*)d->Phi.p;
+    e1.S2 = (float2*)d->S.p;
+    if ((rc = gemv_locked(g, u, B, ks1, e1, st))) return rc;
+    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, st);
+  }
+  if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
+  if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, st))) return rc;
   HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr, g->bias_dtype,
                   u->has_bias ? u->bias.p : nullptr, u->bias_dtype, round16, (float*)G->hidden.p, st));
   if ((rc = prep_locked(d, G->hidden.p, DT_F32, h, B, st))) return rc;
-  if ((rc = gemv_locked(d, nullptr, B, ks2, st))) return rc;
-  HIP_TRY(qreduce((const float*)d->part.p, ks2, B, d->D_out, d->has_bias ? d->bias.p : nullptr, d->bias_dtype, Y,
-                  y_dtype, ldy, st));
-  return 0;
+  return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, st);
 }
 
 size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
@@ -315,6 +346,13 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
   HIP_TRY(hipStreamSynchronize(st));
   *out = L;
   return 0;
+}
+
+int kans_gated_set_fused_swiglu(int on) {
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  const int prev = g_fused_swiglu ? 1 : 0;
+  g_fused_swiglu = on != 0;
+  return prev;
 }
 
 int kans_qlayer_destroy(kans_qlayer* L) {

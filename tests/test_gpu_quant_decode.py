@@ -138,16 +138,73 @@ def test_gated_block_decode(gpu, fmt, B, biased):
         assert lib.kans_dev_malloc(ctypes.byref(yd), B * d * 2) == 0
         try:
             assert lib.kans_memcpy_h2d(xd, x.ctypes.data, x.nbytes) == 0
+            outs = []
             for graph in (0, 1):
                 assert lib.kans_gated_time(blk, xd, DT_F16, yd, DT_F16, B, 1, 3, graph, ctypes.byref(ms)) == 0, \
                     lib.kans_last_error()
                 y16 = np.empty((B, d), np.float16)
                 assert lib.kans_memcpy_d2h(y16.ctypes.data, yd, y16.nbytes) == 0
                 assert O.rel_err(y16.astype(np.float32), ref) <= 2e-2
+                outs.append(y16)
+            assert np.array_equal(outs[0], outs[1])  # graph replays give the eager result
         finally:
             lib.kans_dev_free(xd)
             lib.kans_dev_free(yd)
         assert lib.kans_gated_stream_bytes(blk, B) > 0
+    finally:
+        lib.kans_gated_destroy(blk)
+        for h in layers:
+            lib.kans_qlayer_destroy(h)
+
+
+GATED_EDGE = [  # d, h, K of gate/up, K of down, down has base, biased
+    (96, 200, 4, 4, True, True), (40, 65, 3, 5, False, False), (128, 64, 4, 1, True, True),
+    (72, 130, 2, 32, True, False), (512, 1000, 4, 4, True, True), (2048, 256, 4, 4, True, True)]
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("cfg", GATED_EDGE, ids=lambda c: "d{}h{}K{}-{}b{}{}".format(*c[:4], int(c[4]), int(c[5])))
+def test_gated_fused_epilogue_matches_unfused(gpu, fmt, cfg):
+    """B <= 2 computes SwiGLU and the down layer's basis in the gate|up GEMV's epilogue (the last
+    wave of each 64-feature group reduces the split-K partials): the output must equal the
+    separate-kernel path bit for bit, also on a repeated call (the arrival counters reset
+    themselves), for h not a multiple of 64, odd K, K = 1 and K = 32 in the down layer, with and
+    without its base branch, with 1 to 20 split-K waves per matrix and group."""
+    lib = gpu
+    d, hdim, Kg, Kd, base_d, biased = cfg
+    layers, refs = [], []
+    for i, (di, do, K, base) in enumerate(((d, hdim, Kg, True), (d, hdim, Kg, True), (hdim, d, Kd, base_d))):
+        h, r = make_qlayer(lib, fmt, di, do, K, base, biased, seed=200 + i,
+                           bias_dtype=DT_F16 if (biased and i == 1) else DT_F32)
+        layers.append(h)
+        refs.append(r)
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0, lib.kans_last_error()
+
+    def run(x, B, round16):
+        y = np.full((B, d), np.nan, np.float32)
+        assert lib.kans_gated_forward_host(blk, x.ctypes.data, DT_F16, y.ctypes.data, DT_F32, B, round16) == 0, \
+            lib.kans_last_error()
+        return y
+
+    try:
+        for B in (1, 2):
+            x = np.random.default_rng(B + d).normal(0, 1, (B, d)).astype(np.float16)
+            ref = O.gated_forward(x.astype(np.float32), *refs)
+            for round16 in (0, 1, 2):
+                assert lib.kans_gated_set_fused_swiglu(1) == 1
+                try:
+                    y1, y1b = run(x, B, round16), run(x, B, round16)
+                    lib.kans_gated_set_fused_swiglu(0)
+                    y0 = run(x, B, round16)
+                finally:
+                    lib.kans_gated_set_fused_swiglu(1)
+                print(f"{fmt} {cfg} B={B} round16={round16}: rel err {O.rel_err(y1, ref):.2e}")
+                assert np.isfinite(y1).all()
+                assert np.array_equal(y1, y0), np.max(np.abs(y1 - y0))
+                assert np.array_equal(y1, y1b)
+                if round16 < 2:
+                    assert O.rel_err(y1, ref) <= 2e-2
     finally:
         lib.kans_gated_destroy(blk)
         for h in layers:
