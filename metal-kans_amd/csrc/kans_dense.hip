@@ -357,7 +357,7 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // Requires KP = K + has_base <= block_slots(WAVES, BASIS) (the launcher checks).
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int block_slots(int waves, int basis) {
-  return waves == 8 && (basis == BASIS_RBF || basis == BASIS_RBF_TABLE) ? 9 : 10;
+  return waves == 8 && (basis == BASIS_RBF || basis == BASIS_RBF_TABLE || basis == BASIS_RBF_REC) ? 9 : 10;
 }
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
@@ -365,7 +365,8 @@ __host__ __device__ constexpr int block_slots(int waves, int basis) {
 // ~6 compares / selects (B-spline), plus the fp32 -> 16-bit packing.
 template <int BASIS, int NV, int MFMAS>
 constexpr int kValuPerMfma =
-    ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1 : BASIS == BASIS_BSPLINE ? 6 : 3) * NV + NV / 2 +
+    ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1 : BASIS == BASIS_BSPLINE ? 6 : BASIS == BASIS_RBF_REC ? 2 : 3) *
+         NV + NV / 2 +
      MFMAS - 1) / MFMAS;
 
 template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES>
@@ -688,11 +689,20 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
     }
   } else if (waves == 8) {
     if constexpr (kBlock8) {
-      constexpr int BB = BASIS == BASIS_RBF ? BASIS_RBF_TABLE : BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS;
       const int m_tiles8 = (L.B + 8 * WM - 1) / (8 * WM);
-      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8>), dim3(m_tiles8 * n_tiles, splits), dim3(512), 0,
-                         st, (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy,
-                         part, L.B, L.D_in, L.D_out, m_tiles8, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+      auto go = [&](auto BBC) {
+        constexpr int BB = decltype(BBC)::value;
+        hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8>), dim3(m_tiles8 * n_tiles, splits), dim3(512),
+                           0, st, (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y,
+                           L.ldy, part, L.B, L.D_in, L.D_out, m_tiles8, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+      };
+      if constexpr (BASIS == BASIS_RBF) {
+        // uniform centres: the two-multiply recurrence; otherwise exp2 per value
+        if (L.bp.rbf_rec) go(std::integral_constant<int, BASIS_RBF_REC>{});
+        else go(std::integral_constant<int, BASIS_RBF_TABLE>{});
+      } else {
+        go(std::integral_constant<int, BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS>{});
+      }
     }
   } else {
     hipLaunchKernelGGL((kan_fused_dense<T, TX, TY, BASIS, WM, NB>), grid, dim3(kThreads), 0, st, (const TX*)L.X,

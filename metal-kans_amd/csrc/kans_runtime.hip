@@ -133,6 +133,27 @@ static void set_rbf_table(BasisParams& bp) {
   const double sq = bp.neg_l < 0.0f ? std::sqrt(-(double)bp.neg_l) : 0.0;
   bp.rbf_s = (float)sq;
   for (int k = 0; k < bp.K; ++k) bp.rbf_sc[k] = (float)(sq * (double)bp.centers[k]);
+  // Recurrence (BASIS_RBF_REC, 16-bit block kernel only) when the centres are
+  // uniform to 1e-3 of their spacing h and the scaled span is at most
+  // kRbfRecSpan; otherwise exp2 per value.  The tolerance admits a uniform grid
+  // stored in fp16 (FastKAN.half() rounds the centres: 2.3e-4 h at config 3);
+  // moving a centre by dc changes phi by at most sqrt(2 inv_den / e) |dc|
+  // (e = 2.718...), i.e. 6e-4 for the reference's inv_den = 1 / (2 h^2) and
+  // |dc| = 1e-3 h: the size of the fp16 rounding of phi itself.
+  bp.rbf_rec = 0;
+  const int K = bp.K;
+  if (K < 2 || !(sq > 0.0)) return;
+  const double c0 = sq * (double)bp.centers[0];
+  const double d = (sq * (double)bp.centers[K - 1] - c0) / (K - 1);
+  if (!(d > 0.0) || !std::isfinite(d) || (K - 1) * d > (double)kRbfRecSpan) return;
+  for (int k = 0; k < K; ++k)
+    if (std::fabs(sq * (double)bp.centers[k] - (c0 + k * d)) > 1e-3 * d) return;
+  bp.rec_lo = -kRbfRecPad;
+  bp.rec_hi = (float)((K - 1) * d + (double)kRbfRecPad);
+  bp.rec_2d = (float)(2.0 * d);
+  bp.rec_c = (float)(-d * d);
+  bp.rec_q = (float)std::exp2(-2.0 * d * d);
+  bp.rbf_rec = 1;
 }
 
 static int validate_dims(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias) {
@@ -505,7 +526,8 @@ int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
   int n;
   if (waves)
     n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves>", dt[L->dtype],
-                 L->basis == BASIS_RBF ? "BASIS_RBF_TABLE" : bs[L->basis], wm, nb, waves);
+                 L->basis == BASIS_RBF ? (L->bp.rbf_rec ? "BASIS_RBF_REC" : "BASIS_RBF_TABLE") : bs[L->basis], wm, nb,
+                 waves);
   else
     n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", dt[L->dtype], bs[L->basis], wm, nb);
   if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);

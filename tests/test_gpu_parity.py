@@ -133,6 +133,37 @@ def test_rbf_arbitrary_centres(gpu):
         L(x)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("case", ["uniform8", "uniform5_wide", "uniform9_span", "nonuniform8"])
+def test_block_rbf_recurrence_and_table(gpu, dtype, case):
+    """The 8-wave block kernel evaluates RBF layers on uniform centres whose scaled span is at most 6 by the
+    phi_{k+1} = phi_k * r_k recurrence (BASIS_RBF_REC) and every other grid by exp2 per value
+    (BASIS_RBF_TABLE).  Both against the oracle, with inputs far outside the grid (where the recurrence
+    clamps) and on the centres."""
+    import metal_kans as mk
+    K, rng_, path = {"uniform8": (8, (-2, 2), b"BASIS_RBF_REC"), "uniform5_wide": (5, (-1, 1), b"BASIS_RBF_REC"),
+                     "uniform9_span": (9, (-2, 2), b"BASIS_RBF_TABLE"),
+                     "nonuniform8": (8, (-2, 2), b"BASIS_RBF_TABLE")}[case]
+    # K + base <= 9 slots keeps the layer on the block kernel
+    L = make_layer(mk, "rbf", 72, 300, K, seed=31, grid_range=rng_, base=K < 9)
+    if case == "uniform5_wide":
+        L.inv_denominator = np.float32(0.3)   # wide Gaussians: scaled span 1.3
+    if case == "nonuniform8":
+        L.grid = np.array([-2.0, -1.3, -0.9, 0.0, 0.2, 0.9, 1.6, 2.0], np.float32)
+    x = np.random.default_rng(6).normal(0, 1.5, (260, 72)).astype(np.float32)
+    x[0, :10] = [1e4, -1e4, 7.5, -7.5, 3.0, -3.0, 0.0, 2.0, -2.0, 1e-3]
+    x[1, :K] = np.asarray(L.grid, np.float32)   # exactly on the centres
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    L.set_tiling(32, 8, 1)
+    y = L(x)
+    assert np.isfinite(y).all()
+    assert O.rel_err(y, y_ref) <= TOL[dtype]
+    name = ctypes.create_string_buffer(160)
+    assert gpu.kans_layer_kernel(L._engine().handle, 260, name, 160) == 0
+    assert path in name.value, name.value
+
+
 def test_inputs_outside_grid_and_extremes(gpu):
     import metal_kans as mk
     x = np.random.default_rng(8).uniform(-6, 6, (64, 32)).astype(np.float32)
