@@ -356,8 +356,25 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 //
 // Requires KP = K + has_base <= block_slots(WAVES, BASIS) (the launcher checks).
 // ---------------------------------------------------------------------------
+// emit<KN> of a table generator (BsplineTab) into the A-fragments a
+template <int KN, typename G, typename Frag, int RB>
+__device__ __forceinline__ void gen_emit(const G& g, Frag (&a)[RB]) {
+  g.template emit<KN>(a);
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 __host__ __device__ constexpr int block_slots(int waves, int basis) {
-  return waves == 8 && (basis == BASIS_RBF || basis == BASIS_RBF_TABLE || basis == BASIS_RBF_REC) ? 9 : 10;
+  return waves == 8 && (basis == BASIS_RBF || basis == BASIS_RBF_TABLE || basis == BASIS_RBF_REC ||
+                        basis == BASIS_BSPLINE_TAB || basis == BASIS_BSPLINE_TAB0)
+             ? 9
+             : 10;
 }
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
@@ -365,7 +382,11 @@ __host__ __device__ constexpr int block_slots(int waves, int basis) {
 // ~6 compares / selects (B-spline), plus the fp32 -> 16-bit packing.
 template <int BASIS, int NV, int MFMAS>
 constexpr int kValuPerMfma =
-    ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1 : BASIS == BASIS_BSPLINE ? 6 : BASIS == BASIS_RBF_REC ? 2 : 3) *
+    ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1
+      : BASIS == BASIS_BSPLINE                           ? 6
+      : BASIS == BASIS_RBF_REC                           ? 2
+      : BASIS == BASIS_BSPLINE_TAB || BASIS == BASIS_BSPLINE_TAB0 ? 0
+                                                         : 3) *
          NV + NV / 2 +
      MFMAS - 1) / MFMAS;
 
@@ -489,7 +510,16 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
 
   // ---- prologue: block fb_begin in stage0 and registers ----------------------
-  BasisGen<BASIS, NV> gen;
+  // B-spline table kernels: HB = has_base at compile time
+  constexpr bool kTab = BASIS == BASIS_BSPLINE_TAB || BASIS == BASIS_BSPLINE_TAB0;
+  typedef typename std::conditional<kTab, BsplineTab<T, NV>, BasisGen<BASIS, NV>>::type Gen;
+  Gen gen;
+  __shared__ uint4 bs_sel[kBsplineTabG];  // table kernels: perm selectors per span
+  if constexpr (kTab) {
+    if (tid < kBsplineTabG)
+      bs_sel[tid] = make_uint4(bspline_tab_selector(tid, 0), bspline_tab_selector(tid, 1),
+                               bspline_tab_selector(tid, 2), bspline_tab_selector(tid, 3));
+  }
   if constexpr (BASIS == BASIS_RBF_TABLE) {
     // scaled centres s*c_k, entry K = 0 (read by the unused step after a
     // block's last slot)
@@ -506,14 +536,11 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   // af[P^1]; the last slot of a block computes one unused extra) and the
   // B-fragment reads of slot s+1 (clamped to the block).  Each bf[nb] is
   // re-read as soon as its last MFMA has issued.
-  auto slot = [&](const uint4* cur, int s, auto PP) {
+  // gen_next(af[P ^ 1]) produces the A-fragment of slot s + 1; sn = the slot
+  // whose B-fragments are read (s + 1 clamped to the block).
+  auto slot_core = [&](const uint4* cur, int sn, auto PP, auto&& gen_next) __attribute__((always_inline)) {
     constexpr int P = decltype(PP)::value;
-    {
-      float v[NV];
-      gen.template step<P ^ 1>(s + 1 - has_base, bp, v);
-      pack(af[P ^ 1], v);
-    }
-    const int sn = min(s + 1, KP - 1);
+    gen_next(af[P ^ 1]);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -538,6 +565,33 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
     // B-spline schedules measured better without the fence.
     if constexpr (BASIS == BASIS_CHEBY_POST) __builtin_amdgcn_sched_barrier(0);
   };
+  auto slot = [&](const uint4* cur, int s, auto PP) {
+    constexpr int P = decltype(PP)::value;
+    slot_core(cur, min(s + 1, KP - 1), PP, [&](frag(&a)[RB]) __attribute__((always_inline)) {
+      if constexpr (!kTab) {
+        float v[NV];
+        gen.template step<P ^ 1>(s + 1 - has_base, bp, v);
+        pack(a, v);
+      }
+    });
+  };
+  // Table kernels: K = 8 and HB = has_base known at compile time, so every
+  // slot's basis index is a constant and emit<k> reads fixed table registers.
+  auto tab_slots = [&](const uint4* cur) __attribute__((always_inline)) {
+    constexpr int HB = BASIS == BASIS_BSPLINE_TAB ? 1 : 0;
+    constexpr int KPC = kBsplineTabG + 3 + HB;
+    static_for<0, KPC>([&](auto SC) __attribute__((always_inline)) {
+      constexpr int sc = decltype(SC)::value;
+      constexpr int kn = sc + 1 - HB;  // basis of slot sc + 1
+      slot_core(cur, sc + 1 < KPC ? sc + 1 : KPC - 1, std::integral_constant<int, sc & 1>{},
+                [&](frag(&a)[RB]) __attribute__((always_inline)) {
+        if constexpr (kTab && kn < kBsplineTabG + 3) gen_emit<kn>(gen, a);
+      });
+      // keep the unrolled slots apart, as the loop's basic blocks keep them for
+      // the other bases: hoisting later slots' B-fragment reads costs registers
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
   auto block = [&](int fb, const uint4* cur, uint4* nxt) {
     float xf[NV];
     xunpack(fb, xf);
@@ -545,26 +599,43 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       xload(fb + 1);
       dma(fb + 1, nxt);
     }
-    bread(bf, cur, 0);
-    // basis k is emitted at slot k + has_base: basis 0 lands at parity has_base
-    gen.begin(xf, bp, has_base != 0);
-    {
-      float v[NV];
-      if (has_base) {
+    if constexpr (kTab) {
+      // the table first: its selector reads and temporaries die before the
+      // first slot's B-fragments occupy their 32 registers
+      gen.begin(xf, bp, bs_sel);
+      __builtin_amdgcn_sched_barrier(0);
+      bread(bf, cur, 0);
+      if constexpr (BASIS == BASIS_BSPLINE_TAB) {
+        float v[NV];
 #pragma unroll
         for (int i = 0; i < NV; ++i) v[i] = silu_f32(xf[i]);
+        pack(af[0], v);
       } else {
-        gen.template step<0>(0, bp, v);
+        gen_emit<0>(gen, af[0]);
       }
-      pack(af[0], v);
+      tab_slots(cur);
+    } else {
+      bread(bf, cur, 0);
+      // basis k is emitted at slot k + has_base: basis 0 lands at parity has_base
+      gen.begin(xf, bp, has_base != 0);
+      {
+        float v[NV];
+        if (has_base) {
+#pragma unroll
+          for (int i = 0; i < NV; ++i) v[i] = silu_f32(xf[i]);
+        } else {
+          gen.template step<0>(0, bp, v);
+        }
+        pack(af[0], v);
+      }
+      // slot pairs as one branch-free basic block; an odd last slot is peeled
+      int s = 0;
+      for (; s + 1 < KP; s += 2) {
+        slot(cur, s, std::integral_constant<int, 0>{});
+        slot(cur, s + 1, std::integral_constant<int, 1>{});
+      }
+      if (s < KP) slot(cur, s, std::integral_constant<int, 0>{});
     }
-    // slot pairs as one branch-free basic block; an odd last slot is peeled
-    int s = 0;
-    for (; s + 1 < KP; s += 2) {
-      slot(cur, s, std::integral_constant<int, 0>{});
-      slot(cur, s + 1, std::integral_constant<int, 1>{});
-    }
-    if (s < KP) slot(cur, s, std::integral_constant<int, 0>{});
     __syncthreads();
   };
   for (int fb = fb_begin; fb < fb_end; fb += 2) {
@@ -700,6 +771,11 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
         // uniform centres: the two-multiply recurrence; otherwise exp2 per value
         if (L.bp.rbf_rec) go(std::integral_constant<int, BASIS_RBF_REC>{});
         else go(std::integral_constant<int, BASIS_RBF_TABLE>{});
+      } else if constexpr (BASIS == BASIS_BSPLINE) {
+        // G = 5: per-input basis table (one v_perm per two values per slot)
+        if (L.bp.grid_size == kBsplineTabG && L.has_base) go(std::integral_constant<int, BASIS_BSPLINE_TAB>{});
+        else if (L.bp.grid_size == kBsplineTabG) go(std::integral_constant<int, BASIS_BSPLINE_TAB0>{});
+        else go(std::integral_constant<int, BASIS_BSPLINE>{});
       } else {
         go(std::integral_constant<int, BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS>{});
       }

@@ -526,8 +526,11 @@ int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
   int n;
   if (waves)
     n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves>", dt[L->dtype],
-                 L->basis == BASIS_RBF ? (L->bp.rbf_rec ? "BASIS_RBF_REC" : "BASIS_RBF_TABLE") : bs[L->basis], wm, nb,
-                 waves);
+                 L->basis == BASIS_RBF       ? (L->bp.rbf_rec ? "BASIS_RBF_REC" : "BASIS_RBF_TABLE")
+                 : L->basis == BASIS_BSPLINE && waves == 8 && L->bp.grid_size == kBsplineTabG
+                     ? (L->has_base ? "BASIS_BSPLINE_TAB" : "BASIS_BSPLINE_TAB0")
+                     : bs[L->basis],
+                 wm, nb, waves);
   else
     n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", dt[L->dtype], bs[L->basis], wm, nb);
   if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);

@@ -164,6 +164,29 @@ def test_block_rbf_recurrence_and_table(gpu, dtype, case):
     assert path in name.value, name.value
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("base", [True, False])
+def test_block_bspline_table(gpu, dtype, base):
+    """16-bit B-spline layers with G = 5 on the block kernel place each input's eight basis values into a
+    register table once per feature block (BASIS_BSPLINE_TAB / _TAB0): against the oracle with inputs on
+    every knot, just inside and outside the grid, far outside it, and a bias-free layer."""
+    import metal_kans as mk
+    L = make_layer(mk, "bspline", 40, 280, 8, bias=base, base=base, seed=41, grid_range=(-1.0, 1.0))
+    x = np.random.default_rng(9).uniform(-1.3, 1.3, (300, 40)).astype(np.float32)
+    x[0, :6] = np.linspace(-1, 1, 6)                       # the knots (span boundaries)
+    x[1, :8] = [-1.0000001, 0.9999999, 1.0000001, -0.9999999, 1e4, -1e4, 3.0, -3.0]
+    x[2, :6] = np.linspace(-1, 1, 6) + np.float32(1e-7)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    L.set_tiling(32, 8, 1)
+    y = L(x)
+    assert np.isfinite(y).all()
+    assert O.rel_err(y, y_ref) <= TOL[dtype]
+    name = ctypes.create_string_buffer(160)
+    assert gpu.kans_layer_kernel(L._engine().handle, 300, name, 160) == 0
+    assert (b"BASIS_BSPLINE_TAB," if base else b"BASIS_BSPLINE_TAB0,") in name.value, name.value
+
+
 def test_inputs_outside_grid_and_extremes(gpu):
     import metal_kans as mk
     x = np.random.default_rng(8).uniform(-6, 6, (64, 32)).astype(np.float32)
