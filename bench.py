@@ -138,9 +138,77 @@ def run_layer_workload(lib, mk, name, kind, B, d_in, d_out, K, dtype, seed, x_fn
             assert rc == 0
         lib.kans_synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / steps
+    if dtype != "f32":
+        ceil = mfma_ceiling_same_data(lib, L, x, kind, dtype)
+        out["mfma_ceiling_same_data_tflops"] = ceil
+        out["frac_of_data_ceiling"] = round(flops / ms / 1e9 / ceil, 4)
     log(f"[bench] {name}: {out}")
     state = {"x": x, "L": L, "eng": eng, "xd": xd, "yd": yd, "flops": flops, "wall_ms": wall}
     return out, state
+
+
+def _bits16(a, dtype):
+    """fp32 values -> uint16 bit patterns of the layer's 16-bit operand type."""
+    from metal_kans._engine import to_bf16_bits
+    a = np.asarray(a, np.float32)
+    return to_bf16_bits(a) if dtype == "bf16" else a.astype(np.float16).view(np.uint16)
+
+
+def _basis_values(L, kind, xs, k):
+    """Basis k of the layer at the values xs (fp32): the operand values the fused kernel feeds MFMA."""
+    xs = np.asarray(xs, np.float32)
+    if kind == "cheby":
+        t = np.clip(xs, -1.0, 1.0)
+        a, b = np.ones_like(t), t
+        for _ in range(k):
+            a, b = b, 2.0 * t * b - a
+        return a
+    if kind == "rbf":
+        c = np.float32(np.asarray(L.grid, np.float32).ravel()[k])
+        return np.exp(-((xs - c) ** 2) * np.float32(L.inv_denominator))
+    gmin, inv_h = (float(v) for v in np.asarray(L.grid_params, np.float64).ravel()[:2])
+    G = L.grid_size
+    pos = (xs - gmin) * inv_h
+    span = np.clip(np.floor(pos), 0, G - 1)
+    u = np.clip(pos - span, 0.0, 1.0)
+    w = [(1 - u) ** 3 / 6, (3 * u ** 3 - 6 * u ** 2 + 4) / 6, (-3 * u ** 3 + 3 * u ** 2 + 3 * u + 1) / 6, u ** 3 / 6]
+    d = k - span
+    return sum(np.where(d == j, w[j], 0.0) for j in range(4)).astype(np.float32)
+
+
+def mfma_ceiling_same_data(lib, L, x, kind, dtype, seed=7, iters=2000):
+    """TFLOP/s of back-to-back MFMAs (kans_mfma_ceiling) on 16 A and 16 B operand fragments sampled from
+    this layer's own MFMA operands: A = the basis / SiLU values of 32 consecutive rows x 16 features of x
+    for one slot, B = the matching W' tile (W for slot k >= 1, W_base for slot 0), in the kernel's fragment
+    layout.  The MFMA rate depends on the operand data, so this is the ceiling the fused kernel is measured
+    against beside the published peak."""
+    rng = np.random.default_rng(seed)
+    B, d_in = x.shape
+    W = np.asarray(getattr(L, L._weight_attr), np.float32)
+    K = W.shape[1] // d_in
+    Wb = np.asarray(L.w_base, np.float32)
+    d_out = Wb.shape[0]
+    lane = np.arange(64)
+    a = np.empty((16, 64, 8), np.uint16)
+    b = np.empty((16, 64, 8), np.uint16)
+    for f in range(16):
+        r0 = int(rng.integers(0, B // 32)) * 32
+        fb = int(rng.integers(0, d_in // 16))
+        s = int(rng.integers(0, K + 1))
+        rows = r0 + (lane % 32)
+        feats = fb * 16 + 8 * (lane // 32)[:, None] + np.arange(8)[None, :]
+        xv = x[rows[:, None], feats]
+        av = xv / (1.0 + np.exp(-xv)) if s == 0 else _basis_values(L, kind, xv, s - 1)
+        a[f] = _bits16(av, dtype)
+        ob = int(rng.integers(0, d_out // 32))
+        outs = ob * 32 + (lane % 32)
+        bv = Wb[outs[:, None], feats] if s == 0 else W[outs[:, None], feats * K + (s - 1)]
+        b[f] = _bits16(bv, dtype)
+    t = ctypes.c_double()
+    rc = lib.kans_mfma_ceiling(1 if dtype == "f16" else 2, a.ctypes.data, b.ctypes.data, iters, ctypes.byref(t))
+    if rc:
+        raise RuntimeError(lib.kans_last_error().decode())
+    return round(t.value, 1)
 
 
 def measured_traffic(kernel):
@@ -286,6 +354,7 @@ def run_cfg5(lib, warmup, iters):
         Wb = rng.standard_normal((do, di), dtype=np.float32) * np.float32(0.02)
         mats.append((W, Wb))
     out = {}
+    stream_ceiling = {}
     for fmt in ("int4", "ternary"):
         layers = [_quantized_layer(lib, fmt, W, Wb, K) for (W, Wb) in mats]
         blk = ctypes.c_void_p()
@@ -299,8 +368,18 @@ def run_cfg5(lib, warmup, iters):
                 raise RuntimeError(lib.kans_last_error().decode())
             nbytes = lib.kans_gated_stream_bytes(blk, B)
             gbs = nbytes / ms.value / 1e6
+            if fmt not in stream_ceiling:
+                # one read-only streaming kernel over the same number of bytes (kans_stream_ceiling)
+                sb = DevBuf(lib, (nbytes + 15) // 16 * 16)
+                g = ctypes.c_double()
+                assert lib.kans_stream_ceiling(sb.p, (nbytes + 15) // 16 * 16, ctypes.byref(g)) == 0, \
+                    lib.kans_last_error()
+                sb.free()
+                stream_ceiling[fmt] = round(g.value, 1)
             out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
                                               "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                              "stream_ceiling_GB_per_s": stream_ceiling[fmt],
+                                              "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
                                               "bytes": int(nbytes), "batch": B}
             xd.free()
             yd.free()
@@ -401,7 +480,11 @@ def main():
                    "flops_per_step": F},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["f16"], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK["f16"], 4), "traffic": measured_traffic(head_kernel),
-                     "traffic_unit": "bytes per launch", "kernel": head_kernel, "kernel_ms": kernel_ms},
+                     "traffic_unit": "bytes per launch", "kernel": head_kernel, "kernel_ms": kernel_ms,
+                     "measured_ceiling": {"what": "back-to-back MFMAs on operand fragments sampled from this "
+                                                  "layer's own basis values and weights (kans_mfma_ceiling)",
+                                          "tflops": head["mfma_ceiling_same_data_tflops"],
+                                          "frac": round(achieved / head["mfma_ceiling_same_data_tflops"], 4)}},
     }
     workloads = {"cfg3_fastkan_fp16": head}
     if not a.quick:

@@ -278,6 +278,14 @@ long long kans_gated_stream_bytes(const kans_gated* block, int B);
  * counterpart: a tuning and test switch). */
 int kans_gated_set_fused_swiglu(int on);
 
+/* Measured ceilings for the roofline report (no reference counterpart; measurement only).
+ * kans_mfma_ceiling: TFLOP/s of back-to-back v_mfma_f32_32x32x16 (dtype DT_F16 / DT_BF16) on 16 A and
+ * 16 B operand fragments given as host arrays [16][64 lanes][8 x 16-bit], at the fused block kernel's
+ * occupancy; `iters` x 32 MFMAs per wave.  kans_stream_ceiling: GB/s of a read-only streaming kernel
+ * over `bytes` of the device buffer `buf` (16-byte aligned). */
+int kans_mfma_ceiling(int dtype, const void* a_frags, const void* b_frags, int iters, double* tflops);
+int kans_stream_ceiling(const void* buf, size_t bytes, double* gb_per_s);
+
 /* device memory helpers; kans_copy_device is a plain copy kernel (16-byte multiples) used to
  * calibrate hardware byte counters */
 int kans_dev_malloc(void** ptr, size_t bytes);
