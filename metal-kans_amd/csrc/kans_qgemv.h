@@ -15,9 +15,9 @@ constexpr int kQSuper = 128;
 // general one (three waves per SIMD at MT = 1, one superchunk in flight).
 constexpr int kSmallB = 2;
 // Work items (waves) per CU the split-K aims for: the small-batch kernel's
-// resident waves per CU (INT4 two, ternary three per SIMD: its register
+// resident waves per CU (INT4 three, ternary four per SIMD: its register
 // footprint), the general kernel's ~10.
-inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 12) : 10; }
+inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 16) : 10; }
 
 // 16-row blocks per decode wave (64 output rows: each activation fragment
 // serves 4 weight tiles, and a wave reads 4 KB of INT4 codes per superchunk).

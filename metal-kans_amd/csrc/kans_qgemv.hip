@@ -491,14 +491,22 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
 // One wave = kQNW row blocks (64 output rows) x one contiguous superchunk range
 // (split-K over waves for memory-level parallelism); 4 independent waves per
 // workgroup.  part[ks][m][col] (m < B) receives the wave's partial sums.
-// SMALL (B <= kSmallB): batch row m lives only in accumulator register m of
-// lanes 0-15, so the per-group epilogue updates just those registers.
+// SR > 0 (small batch, B = SR <= kSmallB): the activation fragment carries
+// batch row m in MFMA rows m, 4 + m, 8 + m and 12 + m, so every lane group
+// q = 0..3 receives all SR live rows in accumulator registers 0..SR-1, and lane
+// (q, r) finishes row block q of the wave: one full-wave 16-byte load brings
+// each lane the group parameters of its own row (row block q, row r) and the
+// epilogue applies them to every tile (only tile q's result is kept and
+// stored).  The parameters cost 4 registers per superchunk in flight instead
+// of 16, and one load instruction instead of four.
 
-template <int QT, int MT, bool SMALL, int EPI>
+template <int QT, int MT, int SR, int EPI>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
                                                const float2* __restrict__ S, int B, int MP,
                                                float* __restrict__ part, int N_total, QEpi E) {
+  constexpr bool SMALL = SR > 0;
+  constexpr int NR = SMALL ? SR : 4;  // accumulator rows per lane that can be live
   static_assert(EPI == QEPI_PART || SMALL, "fused epilogues are for the small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
@@ -526,8 +534,9 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   const _Float16* arow_p[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    arow[mt] = mt * 16 + r < B;
-    arow_p[mt] = Phi + (long)(mt * 16 + r) * ldphi + 8 * q;
+    const int row = SMALL ? (r & 3) : mt * 16 + r;  // SMALL: batch row replicated every 4 MFMA rows
+    arow[mt] = row < B;
+    arow_p[mt] = Phi + (long)row * ldphi + 8 * q;
   }
 
   typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
@@ -537,11 +546,11 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   // activation fragments / group sums (L2 resident).
   struct Wts {
     QWord qw[NW];
-    float4 sb[NW];
+    float4 sb[SMALL ? 1 : NW];  // SMALL: this lane's own row (row block q, row r)
   };
   struct Acts {
     half8v a[MT][4];
-    float2 sg[MT][4];  // INT4: group sums of rows m = 16mt + 4q + i
+    float2 sg[MT][NR];  // INT4: group sums of rows m = 16mt + 4q + i (SMALL: m = i)
   };
   struct Ops {
     Wts w;
@@ -552,31 +561,36 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
-      // the four lanes of a row (q = 0..3) share its group parameters; with
-      // SMALL only lanes 0-15 (q = 0) hold live accumulators, so only they load
-      // (16 distinct 16-byte requests instead of 64 duplicated ones)
-      if (!SMALL || q == 0)
-        o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
-      else
-        o.sb[w] = make_float4(0.f, 0.f, 0.f, 0.f);
+      // general: the four lanes of a row (q = 0..3) share its group parameters
+      if constexpr (!SMALL) o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
     }
+    if constexpr (SMALL) o.sb[0] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + lane * 16);
   };
   auto load_x = [&](int c, Acts& o) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (arow[mt]) u = *reinterpret_cast<const uint4*>(arow_p[mt] + (long)c * 128 + 32 * t);
-        o.a[mt][t] = *reinterpret_cast<half8v*>(&u);
+        if constexpr (SMALL) {
+          // rows >= B: stale values are harmless (see above)
+          if (arow[mt]) o.a[mt][t] = *reinterpret_cast<const half8v*>(arow_p[mt] + (long)c * 128 + 32 * t);
+        } else {
+          uint4 u = make_uint4(0u, 0u, 0u, 0u);
+          if (arow[mt]) u = *reinterpret_cast<const uint4*>(arow_p[mt] + (long)c * 128 + 32 * t);
+          o.a[mt][t] = *reinterpret_cast<half8v*>(&u);
+        }
       }
     if constexpr (QT == Q_INT4) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
-          const int mm = mt * 16 + 4 * q + i;
-          o.sg[mt][i] = mm < B ? S[(long)c * MP + mm] : make_float2(0.f, 0.f);
+        for (int i = 0; i < NR; ++i) {
+          if constexpr (SMALL) {
+            o.sg[mt][i] = S[(long)c * MP + i];  // row i < SR = B, the same for every lane
+          } else {
+            const int mm = mt * 16 + 4 * q + i;
+            o.sg[mt][i] = mm < B ? S[(long)c * MP + mm] : make_float2(0.f, 0.f);
+          }
         }
     }
   };
@@ -598,12 +612,13 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         }
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const float s = gs ? ow.sb[w].z : ow.sb[w].x;
-          const float s2 = gs ? ow.sb[w].w : ow.sb[w].y;
+          const float4& sbw = ow.sb[SMALL ? 0 : w];
+          const float s = gs ? sbw.z : sbw.x;
+          const float s2 = gs ? sbw.w : sbw.y;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
+            for (int i = 0; i < NR; ++i) {
               const float S_ = gs ? ox.sg[mt][i].y : ox.sg[mt][i].x;
               acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
             }
@@ -623,11 +638,12 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         }
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const float s = t == 0 ? ow.sb[w].x : t == 1 ? ow.sb[w].y : t == 2 ? ow.sb[w].z : ow.sb[w].w;
+          const float4& sbw = ow.sb[SMALL ? 0 : w];
+          const float s = t == 0 ? sbw.x : t == 1 ? sbw.y : t == 2 ? sbw.z : sbw.w;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], acc[mt][w][i]);
+            for (int i = 0; i < NR; ++i) acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], acc[mt][w][i]);
         }
       }
     }
@@ -641,7 +657,11 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       // range repeat the last superchunk (an L2 hit, no extra HBM traffic), so
       // the loop body is branch-free between the exits and compute(c) waits for
       // exactly the operands of c (vmcnt counts in issue order).
+      // cleared once: lanes that never load keep zeros (see above)
       Ops o0, o1, o2;
+      __builtin_memset(&o0, 0, sizeof(Ops));
+      __builtin_memset(&o1, 0, sizeof(Ops));
+      __builtin_memset(&o2, 0, sizeof(Ops));
       auto issue = [&](int c, Ops& o) {
         const int cc = min(c, c_hi - 1);
         load_x(cc, o.x);
@@ -679,22 +699,35 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     }
   }
 
-  // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const int n = (rb0 + w) * 16 + r;
+  if constexpr (SMALL) {
+    // lane (q, r): row block q, column 16*(rb0 + q) + r, rows i < B from acc[0][q][i]
+    const int n = (rb0 + q) * 16 + r;
     if (n < M.D_out) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int i = 0; i < NR; ++i) {
+        float v = acc[0][0][i];
+        v = q == 1 ? acc[0][1][i] : v;
+        v = q == 2 ? acc[0][2][i] : v;
+        v = q == 3 ? acc[0][3][i] : v;
+        float* dst = part + ((long)ks * B + i) * N_total + M.col_off + n;
+        if constexpr (EPI == QEPI_PART) *dst = v;
+        else part_store(dst, v);
+      }
+    }
+  } else {
+    // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
 #pragma unroll
-        for (int i = 0; i < (SMALL ? kSmallB : 4); ++i) {
-          const int mm = mt * 16 + 4 * q + i;
-          if (mm < B) {
-            float* dst = part + ((long)ks * B + mm) * N_total + M.col_off + n;
-            if constexpr (EPI == QEPI_PART) *dst = acc[mt][w][i];
-            else part_store(dst, acc[mt][w][i]);
+    for (int w = 0; w < NW; ++w) {
+      const int n = (rb0 + w) * 16 + r;
+      if (n < M.D_out) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < NR; ++i) {
+            const int mm = mt * 16 + 4 * q + i;
+            if (mm < B) part[((long)ks * B + mm) * N_total + M.col_off + n] = acc[mt][w][i];
           }
-        }
+      }
     }
   }
   if constexpr (EPI == QEPI_SWIGLU) {
@@ -826,19 +859,26 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   const int ep = G.epi.kind;
   if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
     return hipErrorInvalidValue;
+  // small batches: one kernel per row count (B = 1, 2), each with and without
+  // the fused SwiGLU epilogue
+#define KQ_SMALL(QTV)                                                                                 \
+  do {                                                                                                \
+    if (G.B == 1) {                                                                                   \
+      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, 1, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, 1, QEPI_PART);      \
+    } else {                                                                                          \
+      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, 2, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, 2, QEPI_PART);      \
+    }                                                                                                 \
+  } while (0)
   if (qt == Q_INT4) {
-    if (small) {
-      if (ep == QEPI_SWIGLU) KQ_GEMV(Q_INT4, 1, true, QEPI_SWIGLU);
-      else KQ_GEMV(Q_INT4, 1, true, QEPI_PART);
-    } else if (mt == 1) KQ_GEMV(Q_INT4, 1, false, QEPI_PART);
-    else KQ_GEMV(Q_INT4, 2, false, QEPI_PART);
+    if (small) KQ_SMALL(Q_INT4);
+    else if (mt == 1) KQ_GEMV(Q_INT4, 1, 0, QEPI_PART);
+    else KQ_GEMV(Q_INT4, 2, 0, QEPI_PART);
   } else {
-    if (small) {
-      if (ep == QEPI_SWIGLU) KQ_GEMV(Q_TERN, 1, true, QEPI_SWIGLU);
-      else KQ_GEMV(Q_TERN, 1, true, QEPI_PART);
-    } else if (mt == 1) KQ_GEMV(Q_TERN, 1, false, QEPI_PART);
-    else KQ_GEMV(Q_TERN, 2, false, QEPI_PART);
+    if (small) KQ_SMALL(Q_TERN);
+    else if (mt == 1) KQ_GEMV(Q_TERN, 1, 0, QEPI_PART);
+    else KQ_GEMV(Q_TERN, 2, 0, QEPI_PART);
   }
+#undef KQ_SMALL
 #undef KQ_GEMV
   return hipGetLastError();
 }
