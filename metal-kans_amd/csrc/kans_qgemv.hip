@@ -737,6 +737,234 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for 2 < B <= 32 (k_qgemv_wg).  The four waves of a workgroup
+// take four consecutive row groups over ONE superchunk range, so they share
+// every superchunk's activation fragments (MT x 4 KB) and INT4 group sums:
+// these are copied from L2 into a three-stage LDS ring by global_load_lds
+// (no registers), one 1 KB instruction per fragment, in exactly the order the
+// lanes read them (one conflict-free ds_read_b128 each).  The registers this
+// frees hold a three-deep ring of the wave's own weight records (codes and
+// group parameters), so two superchunks of weights stay in flight while one
+// is multiplied.  Per superchunk: wait until this wave's loads of superchunk
+// c have landed (vmcnt counts in issue order, so only the loads of c + 1 may
+// still be pending), barrier (every wave's share of stage c is in LDS and
+// every wave is done with stage c - 1), issue superchunk c + 2 into the
+// freed stage, multiply.  A wave past the last row group streams the last
+// row group again and stores nothing, so every wave issues the same loads
+// and reaches the same barriers.
+// ---------------------------------------------------------------------------
+template <int QT, int MT>
+__global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
+                                                  int C_tot, const _Float16* __restrict__ Phi,
+                                                  const float2* __restrict__ S, int B, int MP,
+                                                  float* __restrict__ part, int N_total) {
+  constexpr int NW = kQNW;
+  constexpr int FR = MT * 4;                    // activation fragments (1 KB each) per superchunk
+  constexpr int OPS = 2 * NW + FR / 4 + (QT == Q_INT4 ? 1 : 0);  // vector-memory instructions per wave and superchunk
+  // three separate arrays per ring (not one indexed array): the compiler then
+  // sees that reads of one stage do not depend on the copies into another,
+  // and waits only for this stage's copies
+  __shared__ uint4 sa0[FR * 64], sa1[FR * 64], sa2[FR * 64];
+  __shared__ float2 ss0[32], ss1[32], ss2[32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = blockIdx.x % ksplit;
+  const int rg_want = (blockIdx.x / ksplit) * 4 + wave;
+  const bool live = rg_want < n_rg;
+  const int rg = live ? rg_want : n_rg - 1;
+  const QMatDev& M = rg < rg_split ? m0 : m1;
+  const int rg_loc = rg < rg_split ? rg : rg - rg_split;
+  const int rb0 = rg_loc * NW;
+  const int c_lo = (int)((long)C_tot * ks / ksplit);
+  const int c_hi = (int)((long)C_tot * (ks + 1) / ksplit);
+  if (c_lo >= c_hi) return;  // uniform per workgroup
+  const int q = lane >> 4, r = lane & 15;
+  const long ldphi = (long)C_tot * 128;
+  UnpackConsts uk;
+  uk.init();
+
+  typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
+  const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
+  struct Wts {
+    QWord qw[NW];
+    float4 sb[NW];
+  };
+  auto load_w = [&](int c, Wts& o) {
+    const char* rec = rbase + (long)c * qrec_bytes(QT);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
+      o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
+    }
+  };
+  // fragment j = 4 mt + t of superchunk c: lane l holds row 16 mt + l % 16,
+  // reduction indices 128 c + 32 t + 8 (l / 16) .. + 7; wave w copies the
+  // fragments j = w, w + 4, ...; every wave copies the INT4 group sums
+  // (identical data, so each wave issues the same number of loads).
+  auto dma = [&](int c, uint4* sa, float2* ss) {
+#pragma unroll
+    for (int jj = 0; jj < FR / 4; ++jj) {  // a constant count: the compiler's wait counts stay exact
+      const int j = wave + 4 * jj;
+      const int row = (j >> 2) * 16 + r;
+      const _Float16* src = Phi + (long)row * ldphi + (long)c * 128 + 32 * (j & 3) + 8 * q;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&sa[j * 64], 16, 0, 0);
+    }
+    if constexpr (QT == Q_INT4) {
+      const float* ssrc = reinterpret_cast<const float*>(S + (long)c * MP) + min(lane, 2 * MP - 1);
+      __builtin_amdgcn_global_load_lds(ssrc, (__attribute__((address_space(3))) void*)ss, 4, 0, 0);
+    }
+  };
+  auto issue = [&](int c, uint4* sa, float2* ss, Wts& o) {
+    const int cc = min(c, c_hi - 1);
+    load_w(cc, o);
+    dma(cc, sa, ss);
+  };
+  // waits for everything but the OPS loads of the superchunk after this one,
+  // then the workgroup barrier; no fence (that would wait for all loads)
+  auto sync_stage = [&]() {
+    constexpr int kWait = (OPS & 15) | (0x7 << 4) | (0xf << 8) | ((OPS >> 4) << 14);
+    __builtin_amdgcn_s_waitcnt(kWait);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  floatx4 acc[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc[mt][w] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // one stage's fragments and group sums, read before the next DMA is issued
+  // (the compiler cannot tell the stages apart and would otherwise wait for
+  // that DMA before these reads)
+  struct Frags {
+    half8v a[MT][4];
+    float2 sg[MT][4];  // INT4: group sums of rows 16 mt + 4 q + i
+  };
+  auto read_frags = [&](const uint4* sa, const float2* ss, Frags& f) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint4 u = sa[(mt * 4 + t) * 64 + lane];
+        f.a[mt][t] = *reinterpret_cast<const half8v*>(&u);
+      }
+    if constexpr (QT == Q_INT4) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f.sg[mt][i] = ss[mt * 16 + 4 * q + i];
+    }
+  };
+  auto compute = [&](const Wts& ow, const Frags& f) {
+    const auto& a = f.a;
+    if constexpr (QT == Q_INT4) {
+#pragma unroll
+      for (int gs = 0; gs < 2; ++gs) {
+        floatx4 g[MT][NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const half8v b0 = unpack_int4(dw[2 * gs], uk);
+          const half8v b1 = unpack_int4(dw[2 * gs + 1], uk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][2 * gs + 1], b1, g[mt][w], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float S_ = gs ? f.sg[mt][i].y : f.sg[mt][i].x;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+              const float s = gs ? ow.sb[w].z : ow.sb[w].x;
+              const float s2 = gs ? ow.sb[w].w : ow.sb[w].y;
+              acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
+            }
+          }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        floatx4 g[MT][NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const half8v bf = (t & 1) ? unpack_tern<1>(dw[t >> 1], uk) : unpack_tern<0>(dw[t >> 1], uk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float s = t == 0 ? ow.sb[w].x : t == 1 ? ow.sb[w].y : t == 2 ? ow.sb[w].z : ow.sb[w].w;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], acc[mt][w][i]);
+        }
+      }
+    }
+  };
+
+  Wts w0, w1, w2;
+  Frags f;
+  issue(c_lo, sa0, ss0, w0);
+  issue(c_lo + 1, sa1, ss1, w1);
+  // whole rounds of three superchunks: a branch-free body keeps the
+  // compiler's own wait counts exact (a break inside it made them vmcnt(0))
+  int c = c_lo;
+  for (; c + 3 <= c_hi; c += 3) {
+    sync_stage();
+    read_frags(sa0, ss0, f);
+    issue(c + 2, sa2, ss2, w2);
+    compute(w0, f);
+    sync_stage();
+    read_frags(sa1, ss1, f);
+    issue(c + 3, sa0, ss0, w0);
+    compute(w1, f);
+    sync_stage();
+    read_frags(sa2, ss2, f);
+    issue(c + 4, sa1, ss1, w1);
+    compute(w2, f);
+  }
+  // the last one or two superchunks (stages 0 and 1, issued above)
+  if (c < c_hi) {
+    sync_stage();
+    read_frags(sa0, ss0, f);
+    compute(w0, f);
+    if (c + 1 < c_hi) {
+      __builtin_amdgcn_s_waitcnt(kWaitVmem);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      read_frags(sa1, ss1, f);
+      compute(w1, f);
+    }
+  }
+  // every load of the ring has landed before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);
+
+  if (!live) return;
+  // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int n = (rb0 + w) * 16 + r;
+    if (n < M.D_out) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int mm = mt * 16 + 4 * q + i;
+          if (mm < B) part[((long)ks * B + mm) * N_total + M.col_off + n] = acc[mt][w][i];
+        }
+    }
+  }
+}
+
 // y[m][col] = sum_ks part[ks][m][col] + bias.  Block = 64 columns x 4 split
 // lanes: lane g sums the splits ks = g, g+4, ... in order, then the four
 // partial sums are added in order (deterministic).
@@ -869,15 +1097,22 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
       if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, 2, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, 2, QEPI_PART);      \
     }                                                                                                 \
   } while (0)
+  // larger batches: workgroups of four row groups sharing one superchunk range
+  const dim3 grid_wg((unsigned)((G.n_rg + 3) / 4 * G.ksplit));
+#define KQ_WG(QTV, MTV)                                                                                        \
+  hipLaunchKernelGGL((k_qgemv_wg<QTV, MTV>), grid_wg, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,    \
+                     G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total)
+  if (!small && G.MP > 32) return hipErrorInvalidValue;
   if (qt == Q_INT4) {
     if (small) KQ_SMALL(Q_INT4);
-    else if (mt == 1) KQ_GEMV(Q_INT4, 1, 0, QEPI_PART);
-    else KQ_GEMV(Q_INT4, 2, 0, QEPI_PART);
+    else if (mt == 1) KQ_WG(Q_INT4, 1);
+    else KQ_WG(Q_INT4, 2);
   } else {
     if (small) KQ_SMALL(Q_TERN);
-    else if (mt == 1) KQ_GEMV(Q_TERN, 1, 0, QEPI_PART);
-    else KQ_GEMV(Q_TERN, 2, 0, QEPI_PART);
+    else if (mt == 1) KQ_WG(Q_TERN, 1);
+    else KQ_WG(Q_TERN, 2);
   }
+#undef KQ_WG
 #undef KQ_SMALL
 #undef KQ_GEMV
   return hipGetLastError();
