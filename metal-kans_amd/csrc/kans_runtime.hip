@@ -316,36 +316,60 @@ int kans_layer_load_weights_device(kans_layer* L, const void* W, const void* W_b
 
 }  // extern "C"
 
-// Tile configuration: among the instantiated (WM, NB) shapes, in the order of
-// preference for the layer's dtype and basis, take the first that gives every
-// CU its two resident workgroups; otherwise the one with the most tiles, then
-// split the feature blocks until ~512 workgroups exist.  Preference orders
-// come from MI355X timings at 16384 x 1024 -> 1024 (16-bit) and 8192 x 1024 ->
-// {1024, 4096} (fp32):
+// Tile configuration.  Preference orders come from MI355X timings at
+// 16384 x 1024 -> 1024 (16-bit) and 8192 x 1024 -> {1024, 4096} (fp32):
 //   16-bit, every basis (32,8) -- the 8-wave block kernel: 8 basis values per
 //                                lane feed 8 MFMAs;
 //   fp32 Chebyshev / RBF (32,4); fp32 B-spline (32,8).
+// 1. The first shape in that order whose tiles alone fill every CU's resident
+//    workgroup slots (256 for the 8-wave block kernel, 512 otherwise).
+// 2. Else the first of (32,4), (32,8), (64,4), (32,1) that fills half of them
+//    with a feature split of at most nfb / 8 (>= 8 feature blocks per split):
+//    measured on the config-2 chain's layers (4096 x 784 -> 256 best at
+//    (32,4) x 4 splits, 4096 x 256 -> 256 at (32,1) unsplit).
+// 3. Else the shape with the most tiles, split towards 512 workgroups, at most
+//    nfb / 2 ways (4096 x 256 -> 10: (32,1) x 8).
 static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
   static const int pref_n8[4][2] = {{32, 8}, {64, 4}, {32, 4}, {32, 1}};
   static const int pref_n4[4][2] = {{32, 4}, {64, 4}, {32, 8}, {32, 1}};
+  static const int pref_small[4][2] = {{32, 4}, {32, 8}, {64, 4}, {32, 1}};
   const bool f32 = L->dtype == DT_F32;
   const int(*cand)[2] = (f32 && L->basis != BASIS_BSPLINE) ? pref_n4 : pref_n8;
   const int nob = (L->D_out + 31) / 32;
-  auto tiles = [&](int ww, int nn) { return ((B + 4 * ww - 1) / (4 * ww)) * ((nob + nn - 1) / nn); };
-  int bw = 32, bn = 1, bt = tiles(32, 1);  // (32, 1) always fits
-  for (int i = 0; i < 4; ++i) {
+  const int KP = L->K + L->has_base;
+  // workgroups of shape (ww, nn): the 8-wave block kernel's tile is 8 row blocks tall
+  auto waves_of = [&](int ww, int nn) { return block_waves(!f32, L->basis, ww, nn, KP) == 8 ? 8 : 4; };
+  auto wgs = [&](int ww, int nn) {
+    const int rows = waves_of(ww, nn) * ww;
+    return ((B + rows - 1) / rows) * ((nob + nn - 1) / nn);
+  };
+  auto slots = [&](int ww, int nn) { return waves_of(ww, nn) == 8 ? 256 : 512; };
+  auto mostly_padding = [&](int nn) {
+    const int padded = ((nob + nn - 1) / nn) * nn;
+    return nn > 1 && 2 * nob < padded;  // over half of the N-tile would be padding
+  };
+  int bw = 0, bn = 0, s = 1;
+  for (int i = 0; i < 4 && !bw; ++i) {
     const int* c = cand[i];
-    const int padded = ((nob + c[1] - 1) / c[1]) * c[1];
-    if (c[1] > 1 && 2 * nob < padded) continue;  // over half of the N-tile would be padding
-    const int t = tiles(c[0], c[1]);
-    if (t >= 512) { bw = c[0]; bn = c[1]; bt = t; break; }
-    if (t > bt) { bw = c[0]; bn = c[1]; bt = t; }
+    if (!mostly_padding(c[1]) && wgs(c[0], c[1]) >= slots(c[0], c[1])) { bw = c[0]; bn = c[1]; }
   }
-  int s = 1;
-  if (bt < 384) {
-    s = (512 + bt - 1) / bt;
-    if (s > L->nfb) s = L->nfb;
-    if (s < 1) s = 1;
+  const int smax = std::max(1, L->nfb / 8);
+  for (int i = 0; i < 4 && !bw; ++i) {
+    const int* c = pref_small[i];
+    if (mostly_padding(c[1])) continue;
+    const int t = wgs(c[0], c[1]), need = slots(c[0], c[1]) / 2;
+    const int sc = std::min(smax, (need + t - 1) / t);
+    if ((long)t * sc >= need) { bw = c[0]; bn = c[1]; s = sc; }
+  }
+  if (!bw) {
+    bw = 32; bn = 1;
+    int bt = wgs(32, 1);  // (32, 1) always fits
+    for (int i = 0; i < 4; ++i) {
+      const int* c = cand[i];
+      if (mostly_padding(c[1])) continue;
+      if (wgs(c[0], c[1]) > bt) { bw = c[0]; bn = c[1]; bt = wgs(c[0], c[1]); }
+    }
+    s = std::max(1, std::min((512 + bt - 1) / bt, std::max(1, L->nfb / 2)));
   }
   if (L->forced_wm && L->forced_nb) { bw = L->forced_wm; bn = L->forced_nb; }
   if (L->forced_splits) s = L->forced_splits;
