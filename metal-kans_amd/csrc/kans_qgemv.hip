@@ -23,12 +23,17 @@
 //     sum(phi) for INT4, y += s * sum(phi*t) for ternary;
 //   * the activation basis phi (T_k and SiLU of the layer input, fp16, permuted
 //     to match the unpack order) and its per-group sums are computed once per
-//     layer into a small buffer that stays in L2; every wave reads its A
+//     layer into a small buffer that stays in L2; the waves read their A
 //     fragments (v_mfma_f32_16x16x32_f16, 16 batch rows per tile) from there;
 //   * one wave owns 4 row blocks (64 output rows) and a contiguous range of
 //     superchunks (split-K over waves for memory-level parallelism); partial
 //     sums go to an fp32 workspace that a small kernel reduces (+ bias), in
-//     the GatedKAN block together with SwiGLU(gate, up).
+//     the GatedKAN block together with SwiGLU(gate, up) -- at B <= 2 the
+//     gate|up GEMV's last wave per feature group does that itself;
+//   * B <= 2 (k_qgemv): each wave on its own, activations straight from L2
+//     into a three-deep register ring with the weights;
+//   * 2 < B <= 32 (k_qgemv_wg): the four waves of a workgroup share one
+//     superchunk range and its activations, staged in LDS.
 #include "kans_common.h"
 #include "kans_api_internal.h"
 #include "kans_qgemv.h"
@@ -488,26 +493,27 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
   }
 }
 
-// One wave = kQNW row blocks (64 output rows) x one contiguous superchunk range
-// (split-K over waves for memory-level parallelism); 4 independent waves per
-// workgroup.  part[ks][m][col] (m < B) receives the wave's partial sums.
-// SR > 0 (small batch, B = SR <= kSmallB): the activation fragment carries
-// batch row m in MFMA rows m, 4 + m, 8 + m and 12 + m, so every lane group
-// q = 0..3 receives all SR live rows in accumulator registers 0..SR-1, and lane
-// (q, r) finishes row block q of the wave: one full-wave 16-byte load brings
-// each lane the group parameters of its own row (row block q, row r) and the
-// epilogue applies them to every tile (only tile q's result is kept and
-// stored).  The parameters cost 4 registers per superchunk in flight instead
-// of 16, and one load instruction instead of four.
-
-template <int QT, int MT, int SR, int EPI>
+// Small-batch decode GEMV (B = SR <= kSmallB).  One wave = kQNW row blocks
+// (64 output rows) x one contiguous superchunk range (split-K over waves for
+// memory-level parallelism); 4 independent waves per workgroup.
+// part[ks][m][col] (m < B) receives the wave's partial sums.
+//
+// The activation fragment carries batch row m in MFMA rows m, 4 + m, 8 + m
+// and 12 + m, so every lane group q = 0..3 receives all SR live rows in
+// accumulator registers 0..SR-1, and lane (q, r) finishes row block q of the
+// wave: one full-wave 16-byte load brings each lane the group parameters of
+// its own row (row block q, row r) and the epilogue applies them to every tile
+// (only tile q's result is kept and stored).  The parameters cost 4 registers
+// per superchunk in flight instead of 16, and one load instruction instead of
+// four.  Lanes whose MFMA row is not a batch row never load their activation
+// fragment (it stays 0); their results only reach accumulator rows that are
+// not stored.
+template <int QT, int SR, int EPI>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
                                                const float2* __restrict__ S, int B, int MP,
                                                float* __restrict__ part, int N_total, QEpi E) {
-  constexpr bool SMALL = SR > 0;
-  constexpr int NR = SMALL ? SR : 4;  // accumulator rows per lane that can be live
-  static_assert(EPI == QEPI_PART || SMALL, "fused epilogues are for the small-batch kernel");
+  static_assert(SR >= 1 && SR <= kSmallB, "small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -524,210 +530,120 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   UnpackConsts uk;
   uk.init();
 
-  floatx4 acc[MT][NW];
+  floatx4 acc[NW];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int w = 0; w < NW; ++w) acc[mt][w] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < NW; ++w) acc[w] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  bool arow[MT];
-  const _Float16* arow_p[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = SMALL ? (r & 3) : mt * 16 + r;  // SMALL: batch row replicated every 4 MFMA rows
-    arow[mt] = row < B;
-    arow_p[mt] = Phi + (long)row * ldphi + 8 * q;
-  }
+  const int arow = r & 3;  // batch row of this lane's MFMA row (replicated every 4 rows)
+  const bool alive = arow < B;
+  const _Float16* arow_p = Phi + (long)arow * ldphi + 8 * q;
 
   typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
 
   // operands of one superchunk: weights / group parameters (HBM stream) and
   // activation fragments / group sums (L2 resident).
-  struct Wts {
-    QWord qw[NW];
-    float4 sb[SMALL ? 1 : NW];  // SMALL: this lane's own row (row block q, row r)
-  };
-  struct Acts {
-    half8v a[MT][4];
-    float2 sg[MT][NR];  // INT4: group sums of rows m = 16mt + 4q + i (SMALL: m = i)
-  };
   struct Ops {
-    Wts w;
-    Acts x;
+    QWord qw[NW];
+    float4 sb;        // this lane's own row (row block q, row r)
+    half8v a[4];
+    float2 sg[SR];    // INT4: group sums of batch rows 0 .. SR-1 (the same in every lane)
   };
-  auto load_w = [&](int c, Wts& o) {
-    const char* rec = rbase + (long)c * qrec_bytes(QT);
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
-      // general: the four lanes of a row (q = 0..3) share its group parameters
-      if constexpr (!SMALL) o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
-    }
-    if constexpr (SMALL) o.sb[0] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + lane * 16);
-  };
-  auto load_x = [&](int c, Acts& o) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if constexpr (SMALL) {
-          // rows >= B: stale values are harmless (see above)
-          if (arow[mt]) o.a[mt][t] = *reinterpret_cast<const half8v*>(arow_p[mt] + (long)c * 128 + 32 * t);
-        } else {
-          uint4 u = make_uint4(0u, 0u, 0u, 0u);
-          if (arow[mt]) u = *reinterpret_cast<const uint4*>(arow_p[mt] + (long)c * 128 + 32 * t);
-          o.a[mt][t] = *reinterpret_cast<half8v*>(&u);
-        }
-      }
-    if constexpr (QT == Q_INT4) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-          if constexpr (SMALL) {
-            o.sg[mt][i] = S[(long)c * MP + i];  // row i < SR = B, the same for every lane
-          } else {
-            const int mm = mt * 16 + 4 * q + i;
-            o.sg[mt][i] = mm < B ? S[(long)c * MP + mm] : make_float2(0.f, 0.f);
-          }
-        }
-    }
-  };
-  auto compute = [&](const Wts& ow, const Acts& ox) {
+  auto compute = [&](const Ops& o) {
     if constexpr (QT == Q_INT4) {
 #pragma unroll
       for (int gs = 0; gs < 2; ++gs) {
-        floatx4 g[MT][NW];
+        floatx4 g[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&o.qw[w]);
           const half8v b0 = unpack_int4(dw[2 * gs], uk);
           const half8v b1 = unpack_int4(dw[2 * gs + 1], uk);
+          g[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          g[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[2 * gs + 1], b1, g[w], 0, 0, 0);
+        }
+        const float s = gs ? o.sb.z : o.sb.x;
+        const float s2 = gs ? o.sb.w : o.sb.y;
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][2 * gs + 1], b1, g[mt][w], 0, 0, 0);
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+          for (int i = 0; i < SR; ++i) {
+            const float S_ = gs ? o.sg[i].y : o.sg[i].x;
+            acc[w][i] = __builtin_fmaf(s, g[w][i], __builtin_fmaf(s2, S_, acc[w][i]));
           }
-        }
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float4& sbw = ow.sb[SMALL ? 0 : w];
-          const float s = gs ? sbw.z : sbw.x;
-          const float s2 = gs ? sbw.w : sbw.y;
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < NR; ++i) {
-              const float S_ = gs ? ox.sg[mt][i].y : ox.sg[mt][i].x;
-              acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
-            }
-        }
       }
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        floatx4 g[MT][NW];
+        floatx4 g[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
+          const unsigned* dw = reinterpret_cast<const unsigned*>(&o.qw[w]);
           const half8v bf = (t & 1) ? unpack_tern<1>(dw[t >> 1], uk) : unpack_tern<0>(dw[t >> 1], uk);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ox.a[mt][t], bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          g[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[t], bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         }
+        const float s = t == 0 ? o.sb.x : t == 1 ? o.sb.y : t == 2 ? o.sb.z : o.sb.w;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float4& sbw = ow.sb[SMALL ? 0 : w];
-          const float s = t == 0 ? sbw.x : t == 1 ? sbw.y : t == 2 ? sbw.z : sbw.w;
+        for (int w = 0; w < NW; ++w)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < NR; ++i) acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], acc[mt][w][i]);
-        }
+          for (int i = 0; i < SR; ++i) acc[w][i] = __builtin_fmaf(s, g[w][i], acc[w][i]);
       }
     }
   };
 
   if (c_lo < c_hi) {
-    if constexpr (SMALL) {
-      // Three-deep ring: superchunks c+1 and c+2 are in flight while c is
-      // consumed (~10 KB per wave: the stream needs that much in flight to
-      // cover the HBM latency at full bandwidth).  Loads past the end of the
-      // range repeat the last superchunk (an L2 hit, no extra HBM traffic), so
-      // the loop body is branch-free between the exits and compute(c) waits for
-      // exactly the operands of c (vmcnt counts in issue order).
-      // cleared once: lanes that never load keep zeros (see above)
-      Ops o0, o1, o2;
-      __builtin_memset(&o0, 0, sizeof(Ops));
-      __builtin_memset(&o1, 0, sizeof(Ops));
-      __builtin_memset(&o2, 0, sizeof(Ops));
-      auto issue = [&](int c, Ops& o) {
-        const int cc = min(c, c_hi - 1);
-        load_x(cc, o.x);
-        load_w(cc, o.w);
-      };
-      issue(c_lo, o0);
-      issue(c_lo + 1, o1);
-      for (int c = c_lo; c < c_hi; c += 3) {
-        issue(c + 2, o2);
-        compute(o0.w, o0.x);
-        if (c + 1 >= c_hi) break;
-        issue(c + 3, o0);
-        compute(o1.w, o1.x);
-        if (c + 2 >= c_hi) break;
-        issue(c + 4, o1);
-        compute(o2.w, o2.x);
+    // Three-deep ring: superchunks c+1 and c+2 are in flight while c is
+    // consumed (~10 KB per wave: the stream needs that much in flight to
+    // cover the HBM latency at full bandwidth).  Loads past the end of the
+    // range repeat the last superchunk (an L2 hit, no extra HBM traffic), so
+    // the loop body is branch-free between the exits and compute(c) waits for
+    // exactly the operands of c (vmcnt counts in issue order).  Cleared once:
+    // lanes that never load keep zeros.
+    Ops o0, o1, o2;
+    __builtin_memset(&o0, 0, sizeof(Ops));
+    __builtin_memset(&o1, 0, sizeof(Ops));
+    __builtin_memset(&o2, 0, sizeof(Ops));
+    auto issue = [&](int c, Ops& o) {
+      const int cc = min(c, c_hi - 1);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (alive) o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
+      if constexpr (QT == Q_INT4) {
+#pragma unroll
+        for (int i = 0; i < SR; ++i) o.sg[i] = S[(long)cc * MP + i];
       }
-    } else {
-      // Larger batches hold MT activation tiles per superchunk: one superchunk
-      // of weights in flight (a deeper ring would cost occupancy).  The
-      // activation fragments of c are loaded just before that prefetch, so
-      // waiting for them never waits for it.
-      Wts w0, w1;
-      load_w(c_lo, w0);
-      for (int c = c_lo; c < c_hi; c += 2) {
-        Acts x;
-        load_x(c, x);
-        if (c + 1 < c_hi) load_w(c + 1, w1);
-        compute(w0, x);
-        if (c + 1 >= c_hi) break;
-        load_x(c + 1, x);
-        if (c + 2 < c_hi) load_w(c + 2, w0);
-        compute(w1, x);
-      }
+      const char* rec = rbase + (long)cc * qrec_bytes(QT);
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
+      o.sb = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + lane * 16);
+    };
+    issue(c_lo, o0);
+    issue(c_lo + 1, o1);
+    for (int c = c_lo; c < c_hi; c += 3) {
+      issue(c + 2, o2);
+      compute(o0);
+      if (c + 1 >= c_hi) break;
+      issue(c + 3, o0);
+      compute(o1);
+      if (c + 2 >= c_hi) break;
+      issue(c + 4, o1);
+      compute(o2);
     }
   }
 
-  if constexpr (SMALL) {
-    // lane (q, r): row block q, column 16*(rb0 + q) + r, rows i < B from acc[0][q][i]
-    const int n = (rb0 + q) * 16 + r;
-    if (n < M.D_out) {
+  // lane (q, r): row block q, column 16*(rb0 + q) + r, rows i < B from acc[q][i]
+  const int n = (rb0 + q) * 16 + r;
+  if (n < M.D_out) {
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
-        float v = acc[0][0][i];
-        v = q == 1 ? acc[0][1][i] : v;
-        v = q == 2 ? acc[0][2][i] : v;
-        v = q == 3 ? acc[0][3][i] : v;
-        float* dst = part + ((long)ks * B + i) * N_total + M.col_off + n;
-        if constexpr (EPI == QEPI_PART) *dst = v;
-        else part_store(dst, v);
-      }
-    }
-  } else {
-    // acc[mt][w][i] -> row m = 16mt + 4q + i, column 16*(rb0 + w) + r of matrix M
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int n = (rb0 + w) * 16 + r;
-      if (n < M.D_out) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int i = 0; i < NR; ++i) {
-            const int mm = mt * 16 + 4 * q + i;
-            if (mm < B) part[((long)ks * B + mm) * N_total + M.col_off + n] = acc[mt][w][i];
-          }
-      }
+    for (int i = 0; i < SR; ++i) {
+      float v = acc[0][i];
+      v = q == 1 ? acc[1][i] : v;
+      v = q == 2 ? acc[2][i] : v;
+      v = q == 3 ? acc[3][i] : v;
+      float* dst = part + ((long)ks * B + i) * N_total + M.col_off + n;
+      if constexpr (EPI == QEPI_PART) *dst = v;
+      else part_store(dst, v);
     }
   }
   if constexpr (EPI == QEPI_SWIGLU) {
@@ -1079,8 +995,8 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
   dim3 grid((unsigned)((items + 3) / 4));
-#define KQ_GEMV(QTV, MTV, SM, EP)                                                                               \
-  hipLaunchKernelGGL((k_qgemv<QTV, MTV, SM, EP>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,      \
+#define KQ_GEMV(QTV, SR, EP)                                                                                 \
+  hipLaunchKernelGGL((k_qgemv<QTV, SR, EP>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,        \
                      G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi)
   const int mt = G.MP / 16;
   const bool small = G.B <= kSmallB;
@@ -1092,9 +1008,9 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
 #define KQ_SMALL(QTV)                                                                                 \
   do {                                                                                                \
     if (G.B == 1) {                                                                                   \
-      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, 1, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, 1, QEPI_PART);      \
+      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, QEPI_PART);            \
     } else {                                                                                          \
-      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 1, 2, QEPI_SWIGLU); else KQ_GEMV(QTV, 1, 2, QEPI_PART);      \
+      if (ep == QEPI_SWIGLU) KQ_GEMV(QTV, 2, QEPI_SWIGLU); else KQ_GEMV(QTV, 2, QEPI_PART);            \
     }                                                                                                 \
   } while (0)
   // larger batches: workgroups of four row groups sharing one superchunk range
