@@ -73,7 +73,7 @@ def test_qlayer_decode(gpu, fmt, shape):
     h, ref_l = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=d_in + d_out)
     try:
         rng = np.random.default_rng(7)
-        for B in (1, 3, 16, 17, 32):
+        for B in (1, 2, 3, 4, 16, 17, 32):  # B <= 2: k_qgemv (SR = B); 2 < B <= 32: k_qgemv_wg (MT = 1, 2)
             x = rng.uniform(-1.3, 1.3, (B, d_in)).astype(np.float32)
             ref = O.kan_forward("cheby", x, ref_l["W"], ref_l["W_base"], ref_l["bias"], {"K": K})
             for xdt, xin in ((DT_F32, x), (DT_F16, x.astype(np.float16))):
