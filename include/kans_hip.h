@@ -272,10 +272,11 @@ int kans_gated_time(kans_gated* block, const void* X, int x_dtype, void* Y, int 
                     int iters, int use_graph, float* ms);
 /* algorithmic bytes of one block forward: packed weights + group parameters + x and y (fp16) */
 long long kans_gated_stream_bytes(const kans_gated* block, int B);
-/* At B <= 2 the GatedKAN block computes SwiGLU(gate, up) and the down layer's basis in the gate|up
- * GEMV's epilogue (on = 1, the default: 4 launches per block instead of 6); on = 0 selects the
- * separate kernels.  Both give identical results.  Returns the previous setting (no reference
- * counterpart: a tuning and test switch). */
+/* The GatedKAN block computes SwiGLU(gate, up) and the down layer's basis in one step (on = 1, the
+ * default): in the gate|up GEMV's epilogue at B <= 2 (4 launches per block instead of 6), in one
+ * kernel after it otherwise (5 instead of 6); on = 0 selects the separate kernels.  Both give
+ * identical results.  Returns the previous setting (no reference counterpart: a tuning and test
+ * switch). */
 int kans_gated_set_fused_swiglu(int on);
 
 /* Measured ceilings for the roofline report (no reference counterpart; measurement only).

@@ -431,9 +431,12 @@ __device__ __forceinline__ void epi_write_blocks(const _Float16* st, int n_st, l
 // k_qswiglu (same sum order and rounding), then T_k(clamp(hidden)) and
 // SiLU(hidden) into the next layer's Phi / S as k_prep.  The group covering
 // the last features also writes the zero padding up to each segment's end.
-template <int QT>
+// Rows m_lo .. m_hi - 1; AT: read the partial sums with agent-scope loads
+// (written by other waves of the same launch), else plain loads (written by an
+// earlier launch).
+template <int QT, bool AT>
 __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int ksplit, int B, int MP, int h, int j,
-                                           int n_groups, _Float16* st, int lane) {
+                                           int n_groups, _Float16* st, int lane, int m_lo, int m_hi) {
   const int f = j * 64 + lane;
   const int K2 = E.K2;
   const long total = (long)B * 2 * h;
@@ -444,7 +447,7 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
   const long pw_lo = (long)E.Cb2 * 128 + 64L * j;
   const long pw_hi = last ? ldphi2 : pw_lo + 64;
   float* S2f = reinterpret_cast<float*>(E.S2);
-  for (int m = 0; m < B; ++m) {
+  for (int m = m_lo; m < m_hi; ++m) {
     float hvv = 0.0f;
     if (f < h) {
       float g = E.bias ? load_any(E.bias, f, E.bias_dtype) : 0.0f;
@@ -454,8 +457,9 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
         float vg[8], vu[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          vg[q] = k0 + q < ksplit ? part_load(p + (long)(k0 + q) * total) : 0.f;
-          vu[q] = k0 + q < ksplit ? part_load(p + (long)(k0 + q) * total + h) : 0.f;
+          const float* pg = p + (long)(k0 + q) * total;
+          vg[q] = k0 + q < ksplit ? (AT ? part_load(pg) : *pg) : 0.f;
+          vu[q] = k0 + q < ksplit ? (AT ? part_load(pg + h) : pg[h]) : 0.f;
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -649,7 +653,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   if constexpr (EPI == QEPI_SWIGLU) {
     __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
     if (!last_arrival(E.counters + rg_loc, 2 * ksplit, lane)) return;
-    epi_swiglu<QT>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stage[threadIdx.x >> 6], lane);
+    epi_swiglu<QT, true>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stage[threadIdx.x >> 6], lane, 0, B);
   }
 }
 
@@ -881,6 +885,18 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   }
 }
 
+// SwiGLU of the gate|up partial sums and the down layer's activation basis
+// (Phi / S), one single-wave workgroup per (64-feature group, batch row): the
+// small-batch GEMV's fused epilogue as a kernel of its own for B > 2, in place
+// of k_qswiglu + k_prep (identical results, one launch and no hidden buffer).
+template <int QT>
+__global__ void __launch_bounds__(64) k_swiglu_basis(QEpi E, const float* __restrict__ part, int ksplit, int B,
+                                                    int MP, int h, int n_groups) {
+  __shared__ _Float16 stage[64 * (kMaxK + 1)];
+  const int j = blockIdx.x, m = blockIdx.y;
+  epi_swiglu<QT, false>(E, part, ksplit, B, MP, h, j, n_groups, stage, threadIdx.x, m, m + 1);
+}
+
 // y[m][col] = sum_ks part[ks][m][col] + bias.  Block = 64 columns x 4 split
 // lanes: lane g sums the splits ks = g, g+4, ... in order, then the four
 // partial sums are added in order (deterministic).
@@ -1031,6 +1047,18 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
 #undef KQ_WG
 #undef KQ_SMALL
 #undef KQ_GEMV
+  return hipGetLastError();
+}
+
+hipError_t qswiglu_basis(int qt, const QEpi& E, const float* part, int ksplit, int B, int MP, int h,
+                         hipStream_t st) {
+  if (E.K2 < 1 || E.K2 > kMaxK || B < 1 || B > MP || !E.Phi2 || (qt == Q_INT4 && !E.S2)) return hipErrorInvalidValue;
+  const int n_groups = (h + 63) / 64;
+  const dim3 grid((unsigned)n_groups, (unsigned)B);
+  if (qt == Q_INT4)
+    hipLaunchKernelGGL(k_swiglu_basis<Q_INT4>, grid, dim3(64), 0, st, E, part, ksplit, B, MP, h, n_groups);
+  else
+    hipLaunchKernelGGL(k_swiglu_basis<Q_TERN>, grid, dim3(64), 0, st, E, part, ksplit, B, MP, h, n_groups);
   return hipGetLastError();
 }
 

@@ -40,8 +40,9 @@ namespace {
 
 constexpr int kMaxDecodeB = 32;
 
-// GatedKAN at small batches: SwiGLU and the down layer's basis in the
-// gate|up GEMV's epilogue (QEPI_SWIGLU) instead of k_qswiglu + k_prep.
+// GatedKAN: SwiGLU and the down layer's basis in one step -- the gate|up
+// GEMV's epilogue (QEPI_SWIGLU) at B <= 2, k_swiglu_basis above -- instead of
+// k_qswiglu + k_prep.
 bool g_fused_swiglu = true;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
@@ -216,8 +217,9 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
   if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
-  if (g_fused_swiglu && B <= kSmallB && ks1 <= kMaxEpiSplit) {
-    // gate|up GEMV -> (SwiGLU, down layer's basis) in its epilogue
+  if (g_fused_swiglu) {
+    // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
+    // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
     QEpi e1;
     e1.kind = QEPI_SWIGLU;
     e1.counters = (int*)g->cnt.p;
@@ -232,7 +234,12 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
     e1.C_tot2 = d->C_tot;
     e1.Phi2 = (_Float16*)d->Phi.p;
     e1.S2 = (float2*)d->S.p;
-    if ((rc = gemv_locked(g, u, B, ks1, e1, st))) return rc;
+    if (B <= kSmallB && ks1 <= kMaxEpiSplit) {
+      if ((rc = gemv_locked(g, u, B, ks1, e1, st))) return rc;
+    } else {
+      if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, st))) return rc;
+      HIP_TRY(qswiglu_basis(g->quant, e1, (const float*)g->part.p, ks1, B, mp_of(B), h, st));
+    }
     return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, st);
   }
   if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;

@@ -165,11 +165,11 @@ GATED_EDGE = [  # d, h, K of gate/up, K of down, down has base, biased
 @pytest.mark.parametrize("fmt", ["int4", "ternary"])
 @pytest.mark.parametrize("cfg", GATED_EDGE, ids=lambda c: "d{}h{}K{}-{}b{}{}".format(*c[:4], int(c[4]), int(c[5])))
 def test_gated_fused_epilogue_matches_unfused(gpu, fmt, cfg):
-    """B <= 2 computes SwiGLU and the down layer's basis in the gate|up GEMV's epilogue (the last
-    wave of each 64-feature group reduces the split-K partials): the output must equal the
-    separate-kernel path bit for bit, also on a repeated call (the arrival counters reset
-    themselves), for h not a multiple of 64, odd K, K = 1 and K = 32 in the down layer, with and
-    without its base branch, with 1 to 20 split-K waves per matrix and group."""
+    """SwiGLU and the down layer's basis in one step -- the gate|up GEMV's epilogue at B <= 2 (the
+    last wave of each 64-feature group reduces the split-K partials), k_swiglu_basis at B > 2: the
+    output must equal the separate-kernel path bit for bit, also on a repeated call (the arrival
+    counters reset themselves), for h not a multiple of 64, odd K, K = 1 and K = 32 in the down
+    layer, with and without its base branch, with 1 to 20 split-K waves per matrix and group."""
     lib = gpu
     d, hdim, Kg, Kd, base_d, biased = cfg
     layers, refs = [], []
@@ -188,7 +188,7 @@ def test_gated_fused_epilogue_matches_unfused(gpu, fmt, cfg):
         return y
 
     try:
-        for B in (1, 2):
+        for B in (1, 2, 5, 32):  # B <= 2: GEMV epilogue; B > 2: k_swiglu_basis
             x = np.random.default_rng(B + d).normal(0, 1, (B, d)).astype(np.float16)
             ref = O.gated_forward(x.astype(np.float32), *refs)
             for round16 in (0, 1, 2):
