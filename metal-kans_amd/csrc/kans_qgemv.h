@@ -36,7 +36,7 @@ struct QPrep {
   const void* X;   // [B][ldx], fp32 / fp16 / bf16
   int x_dtype;
   long ldx;
-  int B, MP;       // batch rows, padded to MP = 16 or 32 (rows >= B are written as 0)
+  int B, MP;       // batch rows (written), allocated rows MP = 16 or 32
   int D_in, K, has_base;
   int Cb, C_tot;   // superchunks of the basis segment and of basis + base
   _Float16* Phi;   // [MP][C_tot * 128]

@@ -191,7 +191,9 @@ __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, in
 }
 
 // ---------------------------------------------------------------------------
-// Activation basis.  Phi[m][p] (fp16, m < MP, p < C_tot*128): the basis segment
+// Activation basis.  Phi[m][p] (fp16, m < B of the MP allocated rows, p <
+// C_tot*128; rows B .. MP-1 are not written, the GEMVs never store what they
+// feed): the basis segment
 // (p < Cb*128) holds T_k(clamp v[m][i]) at reduction index j = i*K + k, the base
 // segment SiLU(v[m][i]) at j = i; within each 8-block the order is the unpack
 // order pi of the weight format (INT4: 0,4,1,5,2,6,3,7; ternary: identity).
@@ -995,7 +997,9 @@ hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wp
 }
 
 hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
-  dim3 grid((unsigned)((P.C_tot * 16 + 255) / 256), (unsigned)P.MP);
+  // rows B .. MP-1 are left as they are: the GEMVs read them only into
+  // accumulator rows they never store
+  dim3 grid((unsigned)((P.C_tot * 16 + 255) / 256), (unsigned)P.B);
   PrepIn in{P.X, P.x_dtype, P.ldx};
   if (qt == Q_INT4)
     hipLaunchKernelGGL((k_prep<Q_INT4>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
