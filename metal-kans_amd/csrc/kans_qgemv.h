@@ -10,13 +10,13 @@ enum QuantKind { Q_INT4 = 0, Q_TERN = 1 };
 // Reduction indices per superchunk (one wave load of a 16-row block).
 constexpr int kQSuper = 128;
 
-// Batches up to kSmallB take the small-batch GEMV (live accumulator rows only,
-// three-deep prefetch ring at two waves per SIMD); larger ones up to 32 the
-// general one (three waves per SIMD at MT = 1, one superchunk in flight).
+// Batches up to kSmallB take the small-batch GEMV k_qgemv (batch rows
+// replicated across the MFMA rows, three-deep register ring); larger ones up to
+// 32 the workgroup GEMV k_qgemv_wg (activations shared through LDS).
 constexpr int kSmallB = 2;
-// Work items (waves) per CU the split-K aims for: the small-batch kernel's
-// resident waves per CU (INT4 three, ternary four per SIMD: its register
-// footprint), the general kernel's ~10.
+// Work items (waves) per CU the split-K aims for (measured on the config-5
+// block): small batches INT4 8 (resident: 12), ternary 16 (resident: 16);
+// the workgroup kernel 10.
 inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 16) : 10; }
 
 // 16-row blocks per decode wave (64 output rows: each activation fragment
@@ -84,7 +84,7 @@ struct QGemv {
   int B, MP;
   float* part;     // [ksplit][B][N_total] partial sums (matrix 1's columns after matrix 0's)
   int N_total;
-  QEpi epi;        // B <= kSmallB only
+  QEpi epi;        // k_qgemv (B <= kSmallB) only
 };
 
 // Re-tile a packed matrix (C superchunks starting at superchunk c_off) into the records R.
