@@ -346,13 +346,16 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // B-fragments of slot s are read from LDS while the basis values of slot s+1
 // are generated into the second A-fragment buffer, then the MFMAs of slot s
 // run.  Slots are unrolled by two so the fragment buffers and the Chebyshev
-// recurrence roles are fixed at compile time.
+// recurrence roles are fixed at compile time; the B-spline table kernels
+// (BASIS_BSPLINE_TAB / _TAB0, K = 8) unroll all KP slots, so every slot's
+// basis index is a constant.
 //
 // Two shapes: WAVES = 4 (tile 4*WM x NB*32, two workgroups per CU) and
 // WAVES = 8 with WM = 32, NB = 8 (tile 256 x 256, one workgroup of 8 waves
 // per CU).  The second halves the basis values a lane generates per MFMA
 // (8 values feed 8 MFMAs); its two stages of up to 10 slots x 8 KB fill the
-// 160 KB LDS (9 slots with the RBF centre table).
+// 160 KB LDS (9 slots for the RBF and B-spline table kernels, whose lookup
+// tables also live in LDS).
 //
 // Requires KP = K + has_base <= block_slots(WAVES, BASIS) (the launcher checks).
 // ---------------------------------------------------------------------------
@@ -378,8 +381,9 @@ __host__ __device__ constexpr int block_slots(int waves, int basis) {
 }
 
 // VALU instructions of one slot's basis generation per MFMA of that slot
-// (scheduling hint): per value 1 fma (Chebyshev), fma + mul + exp2 (RBF) or
-// ~6 compares / selects (B-spline), plus the fp32 -> 16-bit packing.
+// (scheduling hint): per value 1 fma (Chebyshev), fma + mul + exp2 (RBF),
+// 2 multiplies (RBF recurrence), ~6 compares / selects (B-spline) or none
+// (B-spline table), plus the packing into 16-bit pairs.
 template <int BASIS, int NV, int MFMAS>
 constexpr int kValuPerMfma =
     ((BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST ? 1
