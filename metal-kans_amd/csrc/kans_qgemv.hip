@@ -654,7 +654,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   }
   if constexpr (EPI == QEPI_SWIGLU) {
     __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
-    if (!last_arrival(E.counters + rg_loc, 2 * ksplit, lane)) return;
+    if (!last_arrival(E.counters + rg_loc * kCntStride, 2 * ksplit, lane)) return;
     epi_swiglu<QT, true>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stage[threadIdx.x >> 6], lane, 0, B);
   }
 }

@@ -28,7 +28,8 @@ struct kans_qlayer {
   int bias_dtype = DT_F32;
   // decode workspace: activation basis, its group sums, split-K partials
   DevBuf Phi, S, part;
-  DevBuf cnt;                // arrival counters of the fused epilogues, one per row group (0 between launches)
+  DevBuf cnt;                // arrival counters of the fused epilogue, one per row group, kCntStride ints
+                             // apart (0 between launches)
 };
 
 struct kans_gated {
@@ -106,7 +107,7 @@ int alloc_tiles(kans_qlayer* L) {
   int rc = L->R.reserve(bytes);
   if (rc) return rc;
   HIP_TRY(hipMemsetAsync(L->R.p, 0, bytes, kans_default_stream()));
-  const size_t cbytes = (size_t)(L->nrb_pad / L->nw) * sizeof(int);
+  const size_t cbytes = (size_t)(L->nrb_pad / L->nw) * kCntStride * sizeof(int);
   if ((rc = L->cnt.reserve(cbytes))) return rc;
   HIP_TRY(hipMemsetAsync(L->cnt.p, 0, cbytes, kans_default_stream()));
   return 0;
