@@ -336,7 +336,8 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // N-tile) sit in one of two LDS stages.  At the start of block fb every wave
 // issues (a) the global -> LDS DMA (global_load_lds_dwordx4, 1 KB per
 // instruction) of block fb+1's weights into the other stage and (b) the load
-// of block fb+1's input rows into registers; both are waited for by the
+// of block fb+1's input rows into registers (the B-spline table kernels issue
+// the DMA one instruction per slot instead); both are waited for by the
 // barrier that closes block fb, so their latency hides behind KP slot steps.
 // The two stages are separate __shared__ arrays and the block loop is unrolled
 // by two, so the compiler can tell that the B-fragment reads of the current
@@ -542,8 +543,23 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   // re-read as soon as its last MFMA has issued.
   // gen_next(af[P ^ 1]) produces the A-fragment of slot s + 1; sn = the slot
   // whose B-fragments are read (s + 1 clamped to the block).
-  auto slot_core = [&](const uint4* cur, int sn, auto PP, auto&& gen_next) __attribute__((always_inline)) {
+  // Table kernels spread the weight DMA of the next block over the slots: the
+  // wave's DMA instruction si (of KP, since NB == WAVES) is issued in slot si
+  // from dsrc into ddst, set at the block start.  The other kernels issue it all
+  // at the block start (measured: the spread gains 2 % on the fully unrolled
+  // table kernels and loses 1-3 % in the slot loop of the others).
+  const uint4* dsrc = wtile;
+  uint4* ddst = stage1;
+  auto dma_one = [&](int si) __attribute__((always_inline)) {
+    static_assert(!kTab || (NB == WAVES), "one DMA instruction per wave and slot");
+    const int j = wave + si * WAVES;
+    const int ss = j / NB, nb = j - ss * NB;
+    __builtin_amdgcn_global_load_lds(dsrc + ((long)ss * nob_pad + nb) * 64,
+                                     (__attribute__((address_space(3))) void*)(ddst + j * 64), 16, 0, 0);
+  };
+  auto slot_core = [&](const uint4* cur, int si, int sn, auto PP, auto&& gen_next) __attribute__((always_inline)) {
     constexpr int P = decltype(PP)::value;
+    if constexpr (kTab) dma_one(si);
     gen_next(af[P ^ 1]);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -571,7 +587,7 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   };
   auto slot = [&](const uint4* cur, int s, auto PP) {
     constexpr int P = decltype(PP)::value;
-    slot_core(cur, min(s + 1, KP - 1), PP, [&](frag(&a)[RB]) __attribute__((always_inline)) {
+    slot_core(cur, s, min(s + 1, KP - 1), PP, [&](frag(&a)[RB]) __attribute__((always_inline)) {
       if constexpr (!kTab) {
         float v[NV];
         gen.template step<P ^ 1>(s + 1 - has_base, bp, v);
@@ -587,7 +603,7 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
     static_for<0, KPC>([&](auto SC) __attribute__((always_inline)) {
       constexpr int sc = decltype(SC)::value;
       constexpr int kn = sc + 1 - HB;  // basis of slot sc + 1
-      slot_core(cur, sc + 1 < KPC ? sc + 1 : KPC - 1, std::integral_constant<int, sc & 1>{},
+      slot_core(cur, sc, sc + 1 < KPC ? sc + 1 : KPC - 1, std::integral_constant<int, sc & 1>{},
                 [&](frag(&a)[RB]) __attribute__((always_inline)) {
         if constexpr (kTab && kn < kBsplineTabG + 3) gen_emit<kn>(gen, a);
       });
@@ -599,8 +615,13 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   auto block = [&](int fb, const uint4* cur, uint4* nxt) {
     float xf[NV];
     xunpack(fb, xf);
-    if (fb + 1 < fb_end) {
-      xload(fb + 1);
+    if (fb + 1 < fb_end) xload(fb + 1);
+    if constexpr (kTab) {
+      // the last block reloads its own weights into the idle stage (in bounds,
+      // branch-free; waited for by the closing barrier like the others)
+      dsrc = wtile + (long)min(fb + 1, fb_end - 1) * KP * nob_pad * 64;
+      ddst = nxt;
+    } else if (fb + 1 < fb_end) {
       dma(fb + 1, nxt);
     }
     if constexpr (kTab) {
