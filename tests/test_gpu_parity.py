@@ -121,6 +121,26 @@ def test_block_kernel_256x256_tile(gpu, dtype, kind, K, base, bias):
         assert name.value.startswith(b"kans::kan_fused_block<") and b"32, 8, 8 waves>" in name.value, name.value
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("K,base,bias", [(9, True, True), (4, False, True), (1, True, False)])
+@pytest.mark.parametrize("d_in", [200, 64, 16])
+def test_block_kernel_small_tile_stages(gpu, dtype, K, base, bias, d_in):
+    """16-bit Chebyshev on the (32, 1) tile takes the 4-wave block kernel: feature counts of 13, 4
+    and 1 blocks (one not a multiple of 16), feature splits of 1, 2, 3 and 5 (empty and one-block
+    splits), K + base from 2 to 10."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", d_in, 70, K, bias=bias, base=base, seed=31)
+    x = np.random.default_rng(9).uniform(-1.2, 1.2, (150, d_in)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    for splits in (1, 2, 3, 5):
+        L.set_tiling(32, 1, splits)
+        assert O.rel_err(L(x), y_ref) <= TOL[dtype], splits
+        name = ctypes.create_string_buffer(160)
+        assert gpu.kans_layer_kernel(L._engine().handle, 150, name, 160) == 0
+        assert name.value.startswith(b"kans::kan_fused_block<") and b"32, 1, 4 waves>" in name.value, name.value
+
+
 def test_rbf_arbitrary_centres(gpu):
     import metal_kans as mk
     L = make_layer(mk, "rbf", 48, 40, 5, seed=4)
