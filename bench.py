@@ -430,8 +430,9 @@ def main():
         ap.error(f"unknown workloads {sorted(only - set(SECONDARY))}")
     want = lambda name: not only or name in only  # noqa: E731
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(json.dumps({"error": "this build runs on one GPU only (the fused KAN forward is single-GPU; "
-                                   "multi-GPU sharding is a design note, see DESIGN.md)", "n_gpus": a.gpus}))
+        print(json.dumps({"error": "this build measures one GPU only: the layer shards along the batch "
+                                   "(rows independent, weights replicated), so N GPUs would each run this "
+                                   "benchmark's workload on B/N rows; run with --gpus 1", "n_gpus": a.gpus}))
         sys.exit(2)
     import metal_kans as mk
     lib = mk.get_metal_bridge()
