@@ -278,12 +278,20 @@ long long kans_gated_stream_bytes(const kans_gated* block, int B);
  * identical results.  Returns the previous setting (no reference counterpart: a tuning and test
  * switch). */
 int kans_gated_set_fused_swiglu(int on);
+/* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
+ * non-temporal.  Automatic uses non-temporal loads when a call's packed weights exceed the 256 MB
+ * MALL (they cannot stay cached between calls) and at B > 2 (the activations re-read from L2 keep
+ * the cache), plain loads otherwise.  Results do not depend on it.  Returns the previous mode, or a
+ * negative error code for a mode outside 0..2 (no reference counterpart: a tuning and test
+ * switch). */
+int kans_decode_set_weight_loads(int mode);
 
 /* Measured ceilings for the roofline report (no reference counterpart; measurement only).
  * kans_mfma_ceiling: TFLOP/s of back-to-back v_mfma_f32_32x32x16 (dtype DT_F16 / DT_BF16) on 16 A and
  * 16 B operand fragments given as host arrays [16][64 lanes][8 x 16-bit], at the fused block kernel's
  * occupancy; `iters` x 32 MFMAs per wave.  kans_stream_ceiling: GB/s of a read-only streaming kernel
- * over `bytes` of the device buffer `buf` (16-byte aligned). */
+ * over `bytes` of the device buffer `buf` (16-byte aligned), the faster of plain and non-temporal
+ * loads. */
 int kans_mfma_ceiling(int dtype, const void* a_frags, const void* b_frags, int iters, double* tflops);
 int kans_stream_ceiling(const void* buf, size_t bytes, double* gb_per_s);
 

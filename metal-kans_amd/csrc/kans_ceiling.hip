@@ -14,7 +14,10 @@
 //     8 accumulator tiles per CU, two waves per SIMD), nothing else issued;
 //   kans_stream_ceiling: a read-only stream over a device buffer, 16 waves per
 //     CU, four 16-byte loads per lane in flight (the best streaming shape
-//     measured on this part), nothing else done with the data.
+//     measured on this part), nothing else done with the data; timed with
+//     plain and with non-temporal loads, the faster one reported (a buffer
+//     larger than the MALL streams faster non-temporal, a smaller one re-read
+//     by every launch partly hits the MALL with plain loads).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -84,9 +87,11 @@ __global__ void __launch_bounds__(512) k_mfma_ceiling(const uint4* __restrict__ 
 
 // Wave w reads the contiguous range [w * per_wave, (w + 1) * per_wave) of
 // 16-byte words, 4 KB per iteration; the xor of everything it read goes to
-// out[w] so no load is dead.
+// out[w] so no load is dead.  NT: non-temporal loads.
+template <bool NT>
 __global__ void __launch_bounds__(256) k_stream_ceiling(const uint4* __restrict__ p, long per_wave, long n,
                                                         unsigned* __restrict__ out) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63;
   const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const long lo = w * per_wave, hi = lo + per_wave < n ? lo + per_wave : n;
@@ -96,7 +101,16 @@ __global__ void __launch_bounds__(256) k_stream_ceiling(const uint4* __restrict_
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const long j = i + u * 64 + lane;
-      v[u] = j < hi ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+      if (j < hi) {
+        if constexpr (NT) {
+          const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + j));
+          v[u] = make_uint4(t.x, t.y, t.z, t.w);
+        } else {
+          v[u] = p[j];
+        }
+      } else {
+        v[u] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -180,14 +194,21 @@ int kans_stream_ceiling(const void* buf, size_t bytes, double* gb_per_s) {
   const long per_wave = (n + waves - 1) / waves;
   DevBuf out;
   if ((rc = out.reserve((size_t)waves * sizeof(unsigned)))) return rc;
-  float ms = 0.0f;
+  float ms_plain = 0.0f, ms_nt = 0.0f;
   rc = time_median(
       [&](hipStream_t st) {
-        hipLaunchKernelGGL(k_stream_ceiling, dim3((unsigned)(waves / 4)), dim3(256), 0, st, (const uint4*)buf,
-                           per_wave, n, (unsigned*)out.p);
+        hipLaunchKernelGGL(k_stream_ceiling<false>, dim3((unsigned)(waves / 4)), dim3(256), 0, st,
+                           (const uint4*)buf, per_wave, n, (unsigned*)out.p);
       },
-      9, &ms);
+      9, &ms_plain);
   if (rc) return rc;
-  *gb_per_s = (double)(n * 16) / ((double)ms * 1e-3) / 1e9;
+  rc = time_median(
+      [&](hipStream_t st) {
+        hipLaunchKernelGGL(k_stream_ceiling<true>, dim3((unsigned)(waves / 4)), dim3(256), 0, st,
+                           (const uint4*)buf, per_wave, n, (unsigned*)out.p);
+      },
+      9, &ms_nt);
+  if (rc) return rc;
+  *gb_per_s = (double)(n * 16) / ((double)std::min(ms_plain, ms_nt) * 1e-3) / 1e9;
   return 0;
 }

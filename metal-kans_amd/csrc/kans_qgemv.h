@@ -91,6 +91,7 @@ struct QGemv {
   int B, MP;
   float* part;     // [ksplit][B][N_total] partial sums (matrix 1's columns after matrix 0's)
   int N_total;
+  int nt = 0;      // non-temporal weight-record loads (see load_rec)
   QEpi epi;        // k_qgemv (B <= kSmallB) only
 };
 
@@ -101,11 +102,11 @@ hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wp
                       int C, int c_off, int C_tot, void* R, hipStream_t st);
 hipError_t qprep(int qt, const QPrep& P, hipStream_t st);
 hipError_t qgemv(int qt, const QGemv& G, hipStream_t st);
-// out[m][n] = sum_ks part[ks][m][n] + bias[n]
 // SwiGLU of gate|up split-K partials ([ksplit][B][2h]) into the down layer's
 // Phi / S (E.Phi2, E.S2, geometry in E), as the fused epilogue does.
 hipError_t qswiglu_basis(int qt, const QEpi& E, const float* part, int ksplit, int B, int MP, int h,
                          hipStream_t st);
+// out[m][n] = sum_ks part[ks][m][n] + bias[n]
 hipError_t qreduce(const float* part, int ksplit, int B, int N, const void* bias, int bias_dtype, void* Y, int y_dtype,
                    long ldy, hipStream_t st);
 // hidden[m][i] = SiLU(gate) * up from the [gate | up] partials (+ biases), see k_qswiglu

@@ -499,6 +499,32 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
   }
 }
 
+// Load of one 8- or 16-byte word of a weight record: plain, or non-temporal
+// (NT: the caches are told the data is streamed once).  Non-temporal loads
+// leave L2 and the MALL to other data.  They stream faster when the weights
+// cannot stay cached between calls anyway (more than the MALL holds), and help
+// the workgroup kernel, whose activation fragments are re-read from L2; plain
+// loads let a block whose weights fit the MALL hit it on the next call.
+template <bool NT, typename Q>
+__device__ __forceinline__ Q load_rec(const char* p) {
+  if constexpr (!NT) {
+    return *reinterpret_cast<const Q*>(p);
+  } else {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    static_assert(sizeof(Q) == 16 || sizeof(Q) == 8, "8- or 16-byte words");
+    Q q;
+    if constexpr (sizeof(Q) == 16) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+      __builtin_memcpy(&q, &v, 16);
+    } else {
+      const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+      __builtin_memcpy(&q, &v, 8);
+    }
+    return q;
+  }
+}
+
 // Small-batch decode GEMV (B = SR <= kSmallB).  One wave = kQNW row blocks
 // (64 output rows) x one contiguous superchunk range (split-K over waves for
 // memory-level parallelism); 4 independent waves per workgroup.
@@ -513,8 +539,8 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
 // per superchunk in flight instead of 16, and one load instruction instead of
 // four.  Lanes whose MFMA row is not a batch row never load their activation
 // fragment (it stays 0); their results only reach accumulator rows that are
-// not stored.
-template <int QT, int SR, int EPI>
+// not stored.  NT: non-temporal weight loads (load_rec).
+template <int QT, int SR, int EPI, bool NT>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
                                                const float2* __restrict__ S, int B, int MP,
@@ -621,8 +647,8 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       const char* rec = rbase + (long)cc * qrec_bytes(QT);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
-        o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
-      o.sb = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + lane * 16);
+        o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
+      o.sb = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + lane * 16);
     };
     issue(c_lo, o0);
     issue(c_lo + 1, o1);
@@ -674,9 +700,9 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 // every wave is done with stage c - 1), issue superchunk c + 2 into the
 // freed stage, multiply.  A wave past the last row group streams the last
 // row group again and stores nothing, so every wave issues the same loads
-// and reaches the same barriers.
+// and reaches the same barriers.  NT: non-temporal weight loads (load_rec).
 // ---------------------------------------------------------------------------
-template <int QT, int MT>
+template <int QT, int MT, bool NT>
 __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                   int C_tot, const _Float16* __restrict__ Phi,
                                                   const float2* __restrict__ S, int B, int MP,
@@ -716,8 +742,8 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
     const char* rec = rbase + (long)c * qrec_bytes(QT);
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      o.qw[w] = *reinterpret_cast<const QWord*>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
-      o.sb[w] = *reinterpret_cast<const float4*>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
+      o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
+      o.sb[w] = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
     }
   };
   // fragment j = 4 mt + t of superchunk c: lane l holds row 16 mt + l % 16,
@@ -1010,19 +1036,19 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
+// Launch of the decode GEMV kernel for G (arguments checked by qgemv).
+template <bool NT>
+static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
   QMatDev a{(const char*)G.rec0, G.D_out0, 0};
   QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
   dim3 grid((unsigned)((items + 3) / 4));
 #define KQ_GEMV(QTV, SR, EP)                                                                                 \
-  hipLaunchKernelGGL((k_qgemv<QTV, SR, EP>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,        \
+  hipLaunchKernelGGL((k_qgemv<QTV, SR, EP, NT>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,    \
                      G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi)
   const int mt = G.MP / 16;
   const bool small = G.B <= kSmallB;
   const int ep = G.epi.kind;
-  if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
-    return hipErrorInvalidValue;
   // small batches: one kernel per row count (B = 1, 2), each with and without
   // the fused SwiGLU epilogue
 #define KQ_SMALL(QTV)                                                                                 \
@@ -1036,9 +1062,8 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   // larger batches: workgroups of four row groups sharing one superchunk range
   const dim3 grid_wg((unsigned)((G.n_rg + 3) / 4 * G.ksplit));
 #define KQ_WG(QTV, MTV)                                                                                        \
-  hipLaunchKernelGGL((k_qgemv_wg<QTV, MTV>), grid_wg, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,    \
+  hipLaunchKernelGGL((k_qgemv_wg<QTV, MTV, NT>), grid_wg, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,    \
                      G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total)
-  if (!small && G.MP > 32) return hipErrorInvalidValue;
   if (qt == Q_INT4) {
     if (small) KQ_SMALL(Q_INT4);
     else if (mt == 1) KQ_WG(Q_INT4, 1);
@@ -1051,6 +1076,16 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
 #undef KQ_WG
 #undef KQ_SMALL
 #undef KQ_GEMV
+}
+
+hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
+  const bool small = G.B <= kSmallB;
+  const int ep = G.epi.kind;
+  if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
+    return hipErrorInvalidValue;
+  if (!small && G.MP > 32) return hipErrorInvalidValue;
+  if (G.nt) qgemv_launch<true>(qt, G, st);
+  else qgemv_launch<false>(qt, G, st);
   return hipGetLastError();
 }
 

@@ -48,6 +48,28 @@ bool g_fused_swiglu = true;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
 
+// Weight-record loads of the decode GEMVs: 0 automatic (use_nt), 1 plain,
+// 2 non-temporal.
+int g_weight_loads = 0;
+// MI355X's last-level cache (MALL, "Infinity Cache").
+constexpr size_t kMallBytes = size_t(256) << 20;
+
+// Packed bytes of a layer's re-tiled records (codes + group parameters).
+size_t rec_bytes(const kans_qlayer* L) {
+  return (size_t)(L->nrb_pad / L->nw) * L->C_tot * qrec_bytes(L->quant);
+}
+
+// Non-temporal weight loads when the call's weights cannot stay in the MALL
+// between calls anyway (measured: INT4 GatedKAN block, 423 MB, 92.8 -> 87.0 us
+// at B = 1), and in the workgroup kernel (B > 2), whose activation fragments
+// are re-read from L2 (ternary block at B = 32: 123 -> 117 us).  A block that
+// fits the MALL keeps plain loads at B <= 2 and hits it on the next call
+// (ternary block, 254 MB: 71.6 us plain, 78.0 us non-temporal).
+int use_nt(size_t weight_bytes, int B) {
+  if (g_weight_loads != 0) return g_weight_loads == 2 ? 1 : 0;
+  return B > kSmallB || weight_bytes > kMallBytes ? 1 : 0;
+}
+
 // Superchunk ranges per row group: about items_per_cu work items (waves) per
 // CU, at least 4 superchunks per item.
 int choose_ksplit(int n_rg, int C_tot, int B, int quant) {
@@ -154,7 +176,7 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hip
 
 // GEMV of layer a (and b, sharing a's activations): split-K partial sums in
 // a->part ([ksplit][B][a.D_out + b.D_out]), then the epilogue `epi`.
-int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, hipStream_t st) {
+int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, int nt, hipStream_t st) {
   QGemv G;
   G.rec0 = a->R.p;
   G.D_out0 = a->D_out;
@@ -172,13 +194,14 @@ int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& e
   G.part = (float*)a->part.p;
   G.N_total = a->D_out + (b ? b->D_out : 0);
   G.epi = epi;
+  G.nt = nt;
   HIP_TRY(qgemv(a->quant, G, st));
   return 0;
 }
 
 // GEMV of layer L on its prepared Phi / S, then the split-K reduce + bias into Y.
-int gemv_reduce_locked(kans_qlayer* L, int B, int ks, void* Y, int y_dtype, long ldy, hipStream_t st) {
-  int rc = gemv_locked(L, nullptr, B, ks, QEpi{}, st);
+int gemv_reduce_locked(kans_qlayer* L, int B, int ks, void* Y, int y_dtype, long ldy, int nt, hipStream_t st) {
+  int rc = gemv_locked(L, nullptr, B, ks, QEpi{}, nt, st);
   if (rc) return rc;
   HIP_TRY(qreduce((const float*)L->part.p, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y,
                   y_dtype, ldy, st));
@@ -202,7 +225,7 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
-  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, st);
+  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L), B), st);
 }
 
 int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
@@ -218,6 +241,7 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
   if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
+  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d), B);
   if (g_fused_swiglu) {
     // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
     // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
@@ -236,19 +260,19 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
     e1.Phi2 = (_Float16*)d->Phi.p;
     e1.S2 = (float2*)d->S.p;
     if (B <= kSmallB && ks1 <= kMaxEpiSplit) {
-      if ((rc = gemv_locked(g, u, B, ks1, e1, st))) return rc;
+      if ((rc = gemv_locked(g, u, B, ks1, e1, nt, st))) return rc;
     } else {
-      if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, st))) return rc;
+      if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, st))) return rc;
       HIP_TRY(qswiglu_basis(g->quant, e1, (const float*)g->part.p, ks1, B, mp_of(B), h, st));
     }
-    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, st);
+    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, st);
   }
   if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
-  if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, st))) return rc;
+  if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, st))) return rc;
   HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr, g->bias_dtype,
                   u->has_bias ? u->bias.p : nullptr, u->bias_dtype, round16, (float*)G->hidden.p, st));
   if ((rc = prep_locked(d, G->hidden.p, DT_F32, h, B, st))) return rc;
-  return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, st);
+  return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, st);
 }
 
 size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
@@ -354,6 +378,14 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
   HIP_TRY(hipStreamSynchronize(st));
   *out = L;
   return 0;
+}
+
+int kans_decode_set_weight_loads(int mode) {
+  if (mode < 0 || mode > 2) return kans_fail(KANS_ERR_ARG, "weight-load mode must be 0, 1 or 2 (got %d)", mode);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  const int prev = g_weight_loads;
+  g_weight_loads = mode;
+  return prev;
 }
 
 int kans_gated_set_fused_swiglu(int on) {

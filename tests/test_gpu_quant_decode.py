@@ -90,6 +90,48 @@ def test_qlayer_decode(gpu, fmt, shape):
         lib.kans_qlayer_destroy(h)
 
 
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+def test_weight_load_modes_identical(gpu, fmt):
+    """Plain and non-temporal weight-record loads (kans_decode_set_weight_loads 1 / 2) change only the
+    cache policy: a single layer and a GatedKAN block give the same output bit for bit in both modes,
+    through the small-batch kernel (B = 1, 2) and the workgroup kernel (B = 5, 32).  The call
+    returns the previous mode and refuses modes outside 0..2."""
+    lib = gpu
+    d, hdim = 96, 200
+    layers = [make_qlayer(lib, fmt, di, do, 4, True, True, seed=300 + i)[0]
+              for i, (di, do) in enumerate(((d, hdim), (d, hdim), (hdim, d)))]
+    single, _ = make_qlayer(lib, fmt, 130, 70, 3, True, True, seed=310)
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0, lib.kans_last_error()
+    try:
+        assert lib.kans_decode_set_weight_loads(3) < 0 and lib.kans_decode_set_weight_loads(-1) < 0
+        for B in (1, 2, 5, 32):
+            xg = np.random.default_rng(B).normal(0, 1, (B, d)).astype(np.float16)
+            xs = np.random.default_rng(B + 1).uniform(-1.2, 1.2, (B, 130)).astype(np.float32)
+            outs = []
+            for mode in (1, 2):
+                assert lib.kans_decode_set_weight_loads(mode) in (0, 1, 2)
+                try:
+                    yg = np.empty((B, d), np.float32)
+                    assert lib.kans_gated_forward_host(blk, xg.ctypes.data, DT_F16, yg.ctypes.data, DT_F32, B,
+                                                       0) == 0, lib.kans_last_error()
+                    ys = np.empty((B, 70), np.float32)
+                    assert lib.kans_qlayer_forward_host(single, xs.ctypes.data, DT_F32, ys.ctypes.data, DT_F32,
+                                                        B) == 0, lib.kans_last_error()
+                finally:
+                    prev = lib.kans_decode_set_weight_loads(0)
+                assert prev == mode
+                outs.append((yg, ys))
+            assert np.isfinite(outs[0][0]).all() and np.isfinite(outs[0][1]).all()
+            assert np.array_equal(outs[0][0], outs[1][0]), B
+            assert np.array_equal(outs[0][1], outs[1][1]), B
+    finally:
+        lib.kans_decode_set_weight_loads(0)
+        lib.kans_gated_destroy(blk)
+        for h in layers + [single]:
+            lib.kans_qlayer_destroy(h)
+
+
 def test_qlayer_rejects(gpu):
     lib = gpu
     h, _ = make_qlayer(lib, "int4", 64, 32, 4, True, False, seed=1)
