@@ -11,13 +11,13 @@ enum QuantKind { Q_INT4 = 0, Q_TERN = 1 };
 constexpr int kQSuper = 128;
 
 // Batches up to kSmallB take the small-batch GEMV k_qgemv (batch rows
-// replicated across the MFMA rows, three-deep register ring); larger ones up to
+// replicated across the MFMA rows, three- or four-deep register ring); larger ones up to
 // 32 the workgroup GEMV k_qgemv_wg (activations shared through LDS).
 constexpr int kSmallB = 2;
 // Work items (waves) per CU the split-K aims for (measured on the config-5
-// block): small batches INT4 8 (resident: 12), ternary 16 (resident: 16);
-// the workgroup kernel 10.
-inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 16) : 10; }
+// block): small batches INT4 8 (resident: 12), ternary 12 (resident: 12, the
+// four-deep ring's occupancy); the workgroup kernel 10.
+inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 12) : 10; }
 
 // 16-row blocks per decode wave (64 output rows: each activation fragment
 // serves 4 weight tiles, and a wave reads 4 KB of INT4 codes per superchunk).

@@ -31,7 +31,8 @@
 //     the GatedKAN block together with SwiGLU(gate, up) -- at B <= 2 the
 //     gate|up GEMV's last wave per feature group does that itself;
 //   * B <= 2 (k_qgemv): each wave on its own, activations straight from L2
-//     into a three-deep register ring with the weights;
+//     into a three-deep (INT4) or four-deep (ternary) register ring with the
+//     weights;
 //   * 2 < B <= 32 (k_qgemv_wg): the four waves of a workgroup share one
 //     superchunk range and its activations, staged in LDS.
 #include "kans_common.h"
@@ -624,17 +625,21 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   };
 
   if (c_lo < c_hi) {
-    // Three-deep ring: superchunks c+1 and c+2 are in flight while c is
+    // Register ring: INT4 keeps superchunks c+1 and c+2 in flight while c is
     // consumed (~10 KB per wave: the stream needs that much in flight to
-    // cover the HBM latency at full bandwidth).  Loads past the end of the
-    // range repeat the last superchunk (an L2 hit, no extra HBM traffic), so
-    // the loop body is branch-free between the exits and compute(c) waits for
-    // exactly the operands of c (vmcnt counts in issue order).  Cleared once:
-    // lanes that never load keep zeros.
-    Ops o0, o1, o2;
+    // cover the HBM latency at full bandwidth); ternary, whose records are
+    // half the size, keeps c+1 .. c+3 (measured on the config-5 block at
+    // B = 1: ternary 72.7 -> 70.8 us with four stages, INT4 2 us slower).
+    // Loads past the end of the range repeat the last superchunk (an L2 hit,
+    // no extra HBM traffic), so the loop body is branch-free between the exits
+    // and compute(c) waits for exactly the operands of c (vmcnt counts in issue
+    // order).  Cleared once: lanes that never load keep zeros.
+    constexpr int RING = QT == Q_TERN ? 4 : 3;
+    Ops o0, o1, o2, o3;
     __builtin_memset(&o0, 0, sizeof(Ops));
     __builtin_memset(&o1, 0, sizeof(Ops));
     __builtin_memset(&o2, 0, sizeof(Ops));
+    if constexpr (RING == 4) __builtin_memset(&o3, 0, sizeof(Ops));
     auto issue = [&](int c, Ops& o) {
       const int cc = min(c, c_hi - 1);
 #pragma unroll
@@ -652,15 +657,32 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     };
     issue(c_lo, o0);
     issue(c_lo + 1, o1);
-    for (int c = c_lo; c < c_hi; c += 3) {
-      issue(c + 2, o2);
-      compute(o0);
-      if (c + 1 >= c_hi) break;
-      issue(c + 3, o0);
-      compute(o1);
-      if (c + 2 >= c_hi) break;
-      issue(c + 4, o1);
-      compute(o2);
+    if constexpr (RING == 3) {
+      for (int c = c_lo; c < c_hi; c += 3) {
+        issue(c + 2, o2);
+        compute(o0);
+        if (c + 1 >= c_hi) break;
+        issue(c + 3, o0);
+        compute(o1);
+        if (c + 2 >= c_hi) break;
+        issue(c + 4, o1);
+        compute(o2);
+      }
+    } else {
+      issue(c_lo + 2, o2);
+      for (int c = c_lo; c < c_hi; c += 4) {
+        issue(c + 3, o3);
+        compute(o0);
+        if (c + 1 >= c_hi) break;
+        issue(c + 4, o0);
+        compute(o1);
+        if (c + 2 >= c_hi) break;
+        issue(c + 5, o1);
+        compute(o2);
+        if (c + 3 >= c_hi) break;
+        issue(c + 6, o2);
+        compute(o3);
+      }
     }
   }
 
