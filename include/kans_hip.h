@@ -280,8 +280,8 @@ long long kans_gated_stream_bytes(const kans_gated* block, int B);
 int kans_gated_set_fused_swiglu(int on);
 /* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
  * non-temporal.  Automatic uses non-temporal loads when a call's packed weights exceed the 256 MB
- * MALL (they cannot stay cached between calls) and at B > 2 (the activations re-read from L2 keep
- * the cache), plain loads otherwise.  Results do not depend on it.  Returns the previous mode, or a
+ * MALL (they cannot stay cached between calls), plain loads otherwise (a smaller block hits the
+ * MALL on the next call).  Results do not depend on it.  Returns the previous mode, or a
  * negative error code for a mode outside 0..2 (no reference counterpart: a tuning and test
  * switch). */
 int kans_decode_set_weight_loads(int mode);

@@ -502,9 +502,8 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
 
 // Load of one 8- or 16-byte word of a weight record: plain, or non-temporal
 // (NT: the caches are told the data is streamed once).  Non-temporal loads
-// leave L2 and the MALL to other data.  They stream faster when the weights
-// cannot stay cached between calls anyway (more than the MALL holds), and help
-// the workgroup kernel, whose activation fragments are re-read from L2; plain
+// leave L2 and the MALL to other data and stream faster when the weights
+// cannot stay cached between calls anyway (more than the MALL holds); plain
 // loads let a block whose weights fit the MALL hit it on the next call.
 template <bool NT, typename Q>
 __device__ __forceinline__ Q load_rec(const char* p) {

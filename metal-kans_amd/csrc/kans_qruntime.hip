@@ -59,15 +59,15 @@ size_t rec_bytes(const kans_qlayer* L) {
   return (size_t)(L->nrb_pad / L->nw) * L->C_tot * qrec_bytes(L->quant);
 }
 
-// Non-temporal weight loads when the call's weights cannot stay in the MALL
-// between calls anyway (measured: INT4 GatedKAN block, 423 MB, 92.8 -> 87.0 us
-// at B = 1), and in the workgroup kernel (B > 2), whose activation fragments
-// are re-read from L2 (ternary block at B = 32: 123 -> 117 us).  A block that
-// fits the MALL keeps plain loads at B <= 2 and hits it on the next call
-// (ternary block, 254 MB: 71.6 us plain, 78.0 us non-temporal).
-int use_nt(size_t weight_bytes, int B) {
+// Non-temporal weight loads exactly when the call's weights cannot stay in the
+// MALL between calls anyway.  Measured on the config-5 blocks: INT4 (423 MB)
+// is faster non-temporal at every batch (B = 1 92.5 -> 85.7 us, B = 8
+// 105 -> 94.5, B = 32 129.6 -> 125.4); ternary (254 MB) is faster with plain
+// loads, which hit the MALL on the next call (B = 1 69.4 vs 75.2 us, B = 8
+// 79.3 vs 85.4, B = 32 110.4 vs 114.3).
+int use_nt(size_t weight_bytes) {
   if (g_weight_loads != 0) return g_weight_loads == 2 ? 1 : 0;
-  return B > kSmallB || weight_bytes > kMallBytes ? 1 : 0;
+  return weight_bytes > kMallBytes ? 1 : 0;
 }
 
 // Superchunk ranges per row group: about items_per_cu work items (waves) per
@@ -225,7 +225,7 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
-  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L), B), st);
+  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L)), st);
 }
 
 int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
@@ -241,7 +241,7 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
   if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
-  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d), B);
+  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d));
   if (g_fused_swiglu) {
     // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
     // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
