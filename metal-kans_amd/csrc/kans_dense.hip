@@ -692,7 +692,11 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int dr = rb * 32 + 8 * (r >> 2) + (r & 3);
-            if (rbase + dr < B) out[(long)dr * ldy] = from_f32<TY>(acc[rb][nb][r] + bcol);
+            // y is written once and not read here: non-temporal stores keep
+            // L2 for the inputs and weights (measured 0.5 % on the 16384 x
+            // 1024 -> 1024 shapes)
+            if (rbase + dr < B)
+              __builtin_nontemporal_store(from_f32<TY>(acc[rb][nb][r] + bcol), out + (long)dr * ldy);
           }
       }
     }
