@@ -16,7 +16,7 @@ from oracle import kan_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-DT_F32, DT_F16 = 0, 1
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 
 
 def _quant_int4(W):
@@ -86,6 +86,36 @@ def test_qlayer_decode(gpu, fmt, shape):
                 print(f"{fmt} {shape} B={B} x_dtype={xdt}: rel err {e:.2e}")
                 assert e <= 2e-2
                 assert e <= 5e-3  # fp16 basis operands: observed ~1e-3
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("B", [1, 2, 5, 32])
+def test_qlayer_decode_io_dtypes(gpu, fmt, B):
+    """Every input and output dtype of the decode path.  The split-K reduce adds the partial sums in
+    fp32 and converts once, so fp16 / bf16 outputs equal the fp32 output rounded to that type bit for
+    bit; bf16 inputs (RNE bit patterns) match the oracle on the rounded inputs."""
+    lib = gpu
+    d_in, d_out, K = 100, 70, 4
+    h, ref_l = make_qlayer(lib, fmt, d_in, d_out, K, True, True, seed=41 + B)
+    try:
+        x = np.random.default_rng(B).uniform(-1.2, 1.2, (B, d_in)).astype(np.float32)
+        y32 = np.empty((B, d_out), np.float32)
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y32.ctypes.data, DT_F32, B) == 0, \
+            lib.kans_last_error()
+        y16 = np.empty((B, d_out), np.float16)
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y16.ctypes.data, DT_F16, B) == 0
+        assert np.array_equal(y16, y32.astype(np.float16))
+        yb = np.empty((B, d_out), np.uint16)
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, yb.ctypes.data, DT_BF16, B) == 0
+        assert np.array_equal(yb, O.bf16_round(y32))
+        xb = O.bf16_round(x)
+        xbf = (xb.astype(np.uint32) << 16).view(np.float32)
+        yx = np.empty((B, d_out), np.float32)
+        assert lib.kans_qlayer_forward_host(h, xb.ctypes.data, DT_BF16, yx.ctypes.data, DT_F32, B) == 0
+        ref = O.kan_forward("cheby", xbf, ref_l["W"], ref_l["W_base"], ref_l["bias"], {"K": K})
+        assert O.rel_err(yx, ref) <= 2e-2
     finally:
         lib.kans_qlayer_destroy(h)
 
