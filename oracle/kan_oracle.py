@@ -48,8 +48,12 @@ LOG2E = 1.4426950408889634
 # ----------------------------------------------------------------------------
 
 def silu(x: np.ndarray) -> np.ndarray:
-    """x / (1 + e^-x) on the raw (unclamped) input (fused_kan.metal:13-16,132-133)."""
-    return x / (1.0 + np.exp(-x))
+    """x / (1 + e^-x) on the raw (unclamped) input (fused_kan.metal:13-16,132-133).
+
+    For very negative x, e^-x overflows to inf and the quotient is the exact limit -0, so
+    the overflow is expected and not reported."""
+    with np.errstate(over="ignore"):
+        return x / (1.0 + np.exp(-x))
 
 
 def cheby_basis(x: np.ndarray, K: int, dtype=np.float64) -> np.ndarray:
