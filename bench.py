@@ -107,16 +107,28 @@ def host_input(x: np.ndarray, dtype):
     return np.ascontiguousarray(x, dtype=np.float32)
 
 
+# Wall time every timed window is preceded by (GPU busy with the same forward): the first ~60 launches of a
+# fresh process run 3-8 % slow while the clock settles, whatever --warmup asks for.
+SETTLE_MS = 400.0
+
+
 def time_layer(lib, eng, xd, yd, B, d_in, d_out, warmup, iters):
-    ms = ctypes.c_float()
-    rc = lib.kans_layer_time_forward(eng.handle, xd.p, d_in, yd.p, d_out, B, warmup, iters, ctypes.byref(ms))
+    """(kernel_ms, wall_ms): HIP-event and wall-clock means over the same `iters` launches, after `warmup`
+    launches and a clock settle of at least SETTLE_MS (kans_layer_time_window)."""
+    kms, wms = ctypes.c_float(), ctypes.c_float()
+    if warmup:
+        rc = lib.kans_layer_time_forward(eng.handle, xd.p, d_in, yd.p, d_out, B, 0, warmup, ctypes.byref(kms))
+        if rc:
+            raise RuntimeError(lib.kans_last_error().decode())
+    rc = lib.kans_layer_time_window(eng.handle, xd.p, d_in, yd.p, d_out, B, ctypes.c_float(SETTLE_MS), iters,
+                                    ctypes.byref(kms), ctypes.byref(wms))
     if rc:
         raise RuntimeError(lib.kans_last_error().decode())
-    return ms.value
+    return kms.value, wms.value
 
 
 def run_layer_workload(lib, mk, name, kind, B, d_in, d_out, K, dtype, seed, x_fn, w_std, warmup, iters,
-                       grid_range=(-1.0, 1.0), steps=0):
+                       grid_range=(-1.0, 1.0)):
     rng = np.random.default_rng(seed)
     x = x_fn(rng, B, d_in)
     L = make_layer(mk, kind, d_in, d_out, K, dtype, rng, w_std, grid_range)
@@ -125,25 +137,17 @@ def run_layer_workload(lib, mk, name, kind, B, d_in, d_out, K, dtype, seed, x_fn
     xd = DevBuf(lib, B * d_in * es)
     yd = DevBuf(lib, B * d_out * es)
     xd.upload(host_input(x, dtype))
-    ms = time_layer(lib, eng, xd, yd, B, d_in, d_out, warmup, iters)
+    ms, wall = time_layer(lib, eng, xd, yd, B, d_in, d_out, warmup, iters)
     flops = 2.0 * B * d_out * d_in * (K + 1)
-    out = {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 2), "frac_mfma_peak": round(flops / ms / 1e9 / PEAK[dtype], 4),
+    out = {"ms": round(ms, 5), "ms_wall": round(wall, 5), "tflops": round(flops / ms / 1e9, 2),
+           "frac_mfma_peak": round(flops / ms / 1e9 / PEAK[dtype], 4),
            "shape": f"{B}x{d_in}->{d_out}", "K": K, "basis": kind, "dtype": dtype}
-    wall = None
-    if steps:
-        lib.kans_synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            rc = lib.kans_layer_forward(eng.handle, xd.p, d_in, yd.p, d_out, B, None)
-            assert rc == 0
-        lib.kans_synchronize()
-        wall = (time.perf_counter() - t0) * 1e3 / steps
     if dtype != "f32":
         ceil = mfma_ceiling_same_data(lib, L, x, kind, dtype)
         out["mfma_ceiling_same_data_tflops"] = ceil
         out["frac_of_data_ceiling"] = round(flops / ms / 1e9 / ceil, 4)
     log(f"[bench] {name}: {out}")
-    state = {"x": x, "L": L, "eng": eng, "xd": xd, "yd": yd, "flops": flops, "wall_ms": wall}
+    state = {"x": x, "L": L, "eng": eng, "xd": xd, "yd": yd, "flops": flops}
     return out, state
 
 
@@ -401,7 +405,7 @@ def run_cfg5(lib, warmup, iters):
         eng.prepare(DT_F16, L.w_cheby, L.w_base, None, ())
         xd, yd = DevBuf(lib, B * di * 2), DevBuf(lib, B * do * 2)
         xd.upload(rng.standard_normal((B, di), dtype=np.float32).astype(np.float16))
-        tot_ms += time_layer(lib, eng, xd, yd, B, di, do, warmup, iters)
+        tot_ms += time_layer(lib, eng, xd, yd, B, di, do, warmup, iters)[0]
         flops += 2.0 * B * do * di * (K + 1)
         xd.free()
         yd.free()
@@ -452,15 +456,15 @@ def main():
         return layer_norm(rng.normal(0, 1, (B, d)).astype(np.float32))
 
     head, st = run_layer_workload(lib, mk, "cfg3_fastkan_fp16", "rbf", 16384, 1024, 1024, 8, "f16", 1003,
-                                  ln_normal, np.sqrt(1.0 / (1024 * 8)), a.warmup, iters, grid_range=(-2.0, 2.0),
-                                  steps=iters)
+                                  ln_normal, np.sqrt(1.0 / (1024 * 8)), a.warmup, iters, grid_range=(-2.0, 2.0))
     F = st["flops"]
-    wall_ms = st["wall_ms"]
+    wall_ms = head["ms_wall"]
     name = ctypes.create_string_buffer(160)
     assert lib.kans_layer_kernel(st["eng"].handle, 16384, name, 160) == 0
     head_kernel = name.value.decode()
     value = F / wall_ms / 1e9
     kernel_ms = head["ms"]
+    assert kernel_ms <= wall_ms * 1.0001, (kernel_ms, wall_ms)   # same window: events inside the wall bracket
     achieved = F / kernel_ms / 1e9
     result = {
         "metric": METRIC,
@@ -482,6 +486,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["f16"], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK["f16"], 4), "traffic": measured_traffic(head_kernel),
                      "traffic_unit": "bytes per launch", "kernel": head_kernel, "kernel_ms": kernel_ms,
+                     "timing": f"value and achieved from the same {iters} launches (wall clock between stream "
+                               f"synchronisations, and HIP events on the launch stream inside it), after "
+                               f"{a.warmup} warm-up launches and >= {SETTLE_MS:.0f} ms of clock-settling launches",
                      "measured_ceiling": {"what": "back-to-back MFMAs on operand fragments sampled from this "
                                                   "layer's own basis values and weights (kans_mfma_ceiling)",
                                           "tflops": head["mfma_ceiling_same_data_tflops"],

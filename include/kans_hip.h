@@ -204,6 +204,11 @@ int kans_layer_forward_host_ex(kans_layer* layer, const void* X, int x_dtype, vo
 /* mean ms per device-resident forward, HIP events on the launch stream */
 int kans_layer_time_forward(kans_layer* layer, const void* X, long ldx, void* Y, long ldy, int B, int warmup,
                             int iters, float* ms);
+/* one timed window after the clock settles: forwards run for at least settle_ms of GPU time, then `iters`
+ * forwards are bracketed by stream synchronisation; *wall_ms is the wall-clock mean and *kernel_ms the
+ * HIP-event mean over the same launches (so *kernel_ms <= *wall_ms) */
+int kans_layer_time_window(kans_layer* layer, const void* X, long ldx, void* Y, long ldy, int B, float settle_ms,
+                           int iters, float* kernel_ms, float* wall_ms);
 
 /* multi-layer chain of layers with matching dims and one dtype (no reference counterpart
  * beyond metal_kan_chain_pipeline_cheby): ping-pong device activations kept in fp32 between

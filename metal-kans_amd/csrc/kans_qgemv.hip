@@ -367,11 +367,28 @@ struct QMatDev {
 
 // ---------------------------------------------------------------------------
 // Fused epilogue (QEpi).  The partial sums of the fused launches are written
-// through to memory with agent-scope atomic stores and read back with
-// agent-scope atomic loads, which bypass the per-XCD L2 caches; ordering them
-// against the arrival counter then takes only a wait for this wave's memory
-// operations, where agent-scope fences would write back / invalidate the whole
-// L2 of the XCD.
+// with agent-scope atomic stores and read back with agent-scope atomic loads;
+// an arrival counter picks the wave that reduces them.  The ordering argument
+// is at the ISA level (gfx942 / gfx950 memory model as LLVM implements it,
+// AMDGPUUsage "Memory Model GFX942"):
+//   * an agent-scope atomic store is `global_store ... sc1`: it is written
+//     through the XCD's L2 to the memory-side coherence point, and its
+//     vector-memory counter decrement (vmcnt) comes with that write's
+//     acknowledgement;
+//   * an agent-scope atomic load is `global_load ... sc1`: it does not hit a
+//     non-coherent L2 line, so it reads the coherence point;
+//   * each wave waits `s_waitcnt vmcnt(0)` (all of its partial stores
+//     acknowledged) before its counter RMW, which is performed at the
+//     coherence point; the last arriver issues its partial loads only after
+//     its RMW returned (the loads depend on the returned value, and a second
+//     vmcnt(0) precedes them).
+// So every partial store is visible before any partial load of the reduction
+// is issued.  The C++-level alternative (agent-scope release on the RMW and an
+// acquire fence in the last arriver) compiles to `buffer_wbl2 sc1` in every
+// arriving wave and `buffer_inv sc1` in the last one, and measured 143 us
+// instead of 85 us for the config-5 INT4 block at B = 1 (the L2 write-back
+// and invalidation of ~1700 waves); the bitwise fused-vs-separate-kernel test
+// (test_gated_fused_epilogue_matches_unfused) checks the result.
 // ---------------------------------------------------------------------------
 constexpr int kWaitVmem = 0 | (0x7 << 4) | (0xf << 8);  // s_waitcnt vmcnt(0) only
 
@@ -384,10 +401,12 @@ __device__ __forceinline__ float part_load(const float* p) {
 
 // Counts this wave's arrival at counter *c; true for the last of `need`
 // arrivals, which also resets the counter for the next launch.  Every wave of
-// the group arrives exactly once per launch and none waits for another.
+// the group arrives exactly once per launch and none waits for another.  The
+// reset needs no ordering of its own: the next launch starts after this one
+// has ended (same stream).
 __device__ __forceinline__ bool last_arrival(int* c, int need, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_waitcnt(kWaitVmem);  // this wave's partial stores are complete
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);  // this wave's partial stores are acknowledged
   int old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __shfl(old, 0);

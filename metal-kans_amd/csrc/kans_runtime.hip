@@ -638,6 +638,43 @@ int kans_layer_time_forward(kans_layer* L, const void* X, long ldx, void* Y, lon
   return 0;
 }
 
+// Clock-settled timing of one window: forwards run back to back for at least
+// settle_ms of wall time (synchronised every 16 launches, so it is GPU time),
+// then `iters` forwards are bracketed by stream synchronisation (wall clock)
+// and, inside that bracket, by HIP events on the launch stream.  Both means
+// come from the same launches, so *kernel_ms <= *wall_ms.
+int kans_layer_time_window(kans_layer* L, const void* X, long ldx, void* Y, long ldy, int B, float settle_ms,
+                           int iters, float* kernel_ms, float* wall_ms) {
+  if (!L || !X || !Y || !kernel_ms || !wall_ms || iters <= 0 || !(settle_ms >= 0.0f))
+    return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc;
+  const auto s0 = std::chrono::steady_clock::now();
+  do {
+    for (int i = 0; i < 16; ++i)
+      if ((rc = layer_forward_locked(L, X, ldx, Y, ldy, B, g_stream))) return rc;
+    HIP_TRY(hipStreamSynchronize(g_stream));
+  } while (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - s0).count() < settle_ms);
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  const auto t0 = std::chrono::steady_clock::now();
+  HIP_TRY(hipEventRecord(e0, g_stream));
+  for (int i = 0; i < iters; ++i)
+    if ((rc = layer_forward_locked(L, X, ldx, Y, ldy, B, g_stream))) return rc;
+  HIP_TRY(hipEventRecord(e1, g_stream));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  const auto t1 = std::chrono::steady_clock::now();
+  float t = 0;
+  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *kernel_ms = t / iters;
+  *wall_ms = (float)(std::chrono::duration<double, std::milli>(t1 - t0).count() / iters);
+  return 0;
+}
+
 // ---------------------------------------------------------------------------
 // Reference-named entry points (metal_kans/device.py:64-474 argtypes).
 // ---------------------------------------------------------------------------

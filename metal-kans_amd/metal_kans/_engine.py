@@ -7,11 +7,17 @@ change.  A change is detected by
 
 * identity: a different array object, data pointer, shape or dtype (covers
   ``half()``, ``float()``, ``to_int4()``, attribute assignment);
-* content, for arrays of at most ``VERIFY_BYTES`` bytes: compared byte-for-byte
-  against the last uploaded copy (covers in-place edits such as the
-  finite-difference loops in the reference's tests).
+* content, on every forward: arrays of at most ``VERIFY_BYTES`` bytes are
+  compared byte for byte against the last uploaded copy, larger writeable
+  arrays by a 128-bit hash of their bytes (xxh3, ~7 GB/s on one core), so
+  in-place edits such as an optimizer's ``param -= lr * update`` or the
+  finite-difference loops of the reference's tests are always seen.
 
-In-place edits of larger arrays must be announced with ``layer.invalidate()``.
+Two cases skip the content check of large arrays: a read-only array (numpy
+refuses in-place writes to it; the quantizers hand out their dequantized
+weights that way), and a layer whose weights were declared frozen with
+``layer.freeze_weights()`` (an explicit opt-in for inference loops, where the
+hash would cost ~5 ms per 37 MB of weights).
 """
 from __future__ import annotations
 
@@ -31,27 +37,61 @@ def dtype_code(kind: str) -> int:
     return {"float32": DT_F32, "float16": DT_F16, "bfloat16": DT_BF16}[kind]
 
 
+try:
+    import xxhash
+
+    def _digest(a: np.ndarray) -> bytes:
+        return xxhash.xxh3_128_digest(np.ascontiguousarray(a).view(np.uint8))
+except ImportError:  # pragma: no cover - xxhash ships with the image
+    import hashlib
+
+    def _digest(a: np.ndarray) -> bytes:
+        return hashlib.blake2b(np.ascontiguousarray(a).view(np.uint8), digest_size=16).digest()
+
+
+def _read_only(a: np.ndarray) -> bool:
+    """True when no numpy write can reach the array's memory: it and every array it views are read-only
+    (memory owned by anything but a numpy array counts as writeable)."""
+    while not a.flags.writeable:
+        b = a.base
+        if b is None:
+            return True
+        if not isinstance(b, np.ndarray):
+            return False
+        a = b
+    return False
+
+
 class _Snapshot:
-    __slots__ = ("ref", "ptr", "shape", "dtype", "copy")
+    """What the device copy of one host array was made from (see the module docstring)."""
+    __slots__ = ("ref", "ptr", "shape", "dtype", "copy", "digest")
 
     def __init__(self, a: Optional[np.ndarray]):
         self.ref = a
+        self.copy = self.digest = None
         if a is None:
-            self.ptr, self.shape, self.dtype, self.copy = 0, None, None, None
+            self.ptr, self.shape, self.dtype = 0, None, None
             return
         self.ptr = a.ctypes.data
         self.shape = a.shape
         self.dtype = a.dtype.str
-        self.copy = a.copy() if a.nbytes <= VERIFY_BYTES else None
+        if a.nbytes <= VERIFY_BYTES:
+            self.copy = a.copy()
+        else:
+            self.digest = _digest(a)
 
-    def same(self, a: Optional[np.ndarray]) -> bool:
+    def same(self, a: Optional[np.ndarray], verify: bool = True) -> bool:
+        """Whether ``a`` still holds what the snapshot was taken of; ``verify=False`` (frozen weights)
+        skips the content check of arrays larger than ``VERIFY_BYTES``."""
         if a is None or self.ref is None:
             return a is None and self.ref is None
         if a is not self.ref or a.ctypes.data != self.ptr or a.shape != self.shape or a.dtype.str != self.dtype:
             return False
         if self.copy is not None:
             return bool(np.array_equal(a.view(np.uint8), self.copy.view(np.uint8)))
-        return True
+        if not verify or _read_only(a):
+            return True
+        return _digest(a) == self.digest
 
 
 class LayerEngine:
@@ -108,9 +148,9 @@ class LayerEngine:
                          "kans_layer_set_tiling")
 
     def prepare_f32(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
-                    params: tuple) -> None:
+                    params: tuple, verify: bool = True) -> None:
         """As ``prepare`` with float32 host arrays converted on the device to dtype ``dt``."""
-        self.prepare(dt, W, W_base, bias, params, src_f32=True)
+        self.prepare(dt, W, W_base, bias, params, src_f32=True, verify=verify)
 
     def _set_params(self, lib, params: tuple) -> None:
         if params != self.params:
@@ -138,13 +178,14 @@ class LayerEngine:
         self.dev_key = key
 
     def prepare(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
-                params: tuple, src_f32: bool = False) -> None:
-        """Make the device copy current: handle for dtype, basis params, weights."""
+                params: tuple, src_f32: bool = False, verify: bool = True) -> None:
+        """Make the device copy current: handle for dtype, basis params, weights (``verify=False``: frozen
+        weights, large arrays are compared by identity only)."""
         lib = self._ensure_handle(dt)
         self._set_params(lib, params)
         self.dev_key = None
         arrays = (W, W_base if self.has_base else None, bias if self.has_bias else None)
-        if self.snaps is not None and all(s.same(a) for s, a in zip(self.snaps, arrays)):
+        if self.snaps is not None and all(s.same(a, verify) for s, a in zip(self.snaps, arrays)):
             return
         for a in arrays:
             if a is not None and not a.flags["C_CONTIGUOUS"]:

@@ -24,7 +24,7 @@ from typing import Optional
 
 import numpy as np
 
-from ._engine import DT_BF16, DT_F16, DT_F32, LayerEngine, from_bf16_bits, to_bf16_bits
+from ._engine import DT_BF16, DT_F16, DT_F32, LayerEngine, _Snapshot, from_bf16_bits, to_bf16_bits
 from . import device
 
 
@@ -74,9 +74,19 @@ class KANLayerBase:
         return self
 
     def invalidate(self) -> None:
-        """Announce an in-place edit of a weight array larger than 4 MB."""
+        """Force the next forward to re-upload the weights (in-place edits are detected without it)."""
         if self._engine_obj is not None:
             self._engine_obj.invalidate()
+
+    _frozen: bool = False
+
+    def freeze_weights(self, frozen: bool = True):
+        """Declare that the weight arrays will not be edited in place (opt-in, for inference loops): the
+        forward then compares arrays larger than 4 MB by identity only instead of hashing their bytes on
+        every call.  Assigning a new array is still detected; an in-place edit of a frozen layer's large
+        array must be followed by ``invalidate()``."""
+        self._frozen = bool(frozen)
+        return self
 
     def set_tiling(self, wm: int, nb: int, splits: int = 0) -> None:
         """Force the fused kernel's tile shape (tuning/testing); (0, 0) restores the heuristic."""
@@ -127,7 +137,7 @@ class KANLayerBase:
             eng.prepare_f32(DT_BF16, np.ascontiguousarray(W, dtype=np.float32),
                             None if Wb is None else np.ascontiguousarray(Wb, dtype=np.float32),
                             None if bias is None else np.ascontiguousarray(bias, dtype=np.float32),
-                            self._basis_params())
+                            self._basis_params(), verify=not self._frozen)
             yb = np.empty((B, self.out_features), dtype=np.uint16)
             eng.forward_host(x, yb)
             y = from_bf16_bits(yb).reshape(B, self.out_features)
@@ -139,7 +149,7 @@ class KANLayerBase:
                 if a is None:
                     return None
                 return a if (a.dtype == np_dt and a.flags["C_CONTIGUOUS"]) else self._converted(a, np_dt)
-            eng.prepare(dt, conv(W), conv(Wb), conv(bias), self._basis_params())
+            eng.prepare(dt, conv(W), conv(Wb), conv(bias), self._basis_params(), verify=not self._frozen)
             y = np.empty((B, self.out_features), dtype=np_dt)
             eng.forward_host(x, y)
         if len(orig_shape) > 2:
@@ -149,15 +159,17 @@ class KANLayerBase:
     __call__ = forward
 
     def _converted(self, a: np.ndarray, np_dt) -> np.ndarray:
-        """Cached dtype conversion of a parameter array (keyed on the source object)."""
+        """Cached dtype conversion of a parameter array, redone when the source array changes (identity
+        or content, as the device upload checks it)."""
         cache = self.__dict__.setdefault("_conv_cache", {})
-        key = id(a)
+        key = (id(a), np.dtype(np_dt).str)
         hit = cache.get(key)
-        if hit is not None and hit[0] is a and hit[1] == a.ctypes.data and (
-                a.nbytes > (4 << 20) or np.array_equal(hit[2], a)):
-            return hit[3]
+        if hit is not None and hit[0].same(a, not self._frozen):
+            return hit[1]
         conv = np.ascontiguousarray(a, dtype=np_dt)
-        cache[key] = (a, a.ctypes.data, a.copy() if a.nbytes <= (4 << 20) else None, conv)
+        if len(cache) >= 8:  # entries hold their source arrays: keep only recent ones
+            cache.clear()
+        cache[key] = (_Snapshot(a), conv)
         return conv
 
     def backward(self, *args, **kwargs):

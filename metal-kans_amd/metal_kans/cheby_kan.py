@@ -43,6 +43,11 @@ class ChebyKAN(KANLayerBase):
         self.w_base = (np.random.uniform(-bound, bound, (out_features, in_features)).astype(np.float32)
                        if use_base else np.zeros((1,), dtype=np.float32))
         self.bias = (np.zeros((out_features,), dtype=np.float32) if bias else np.zeros((1,), dtype=np.float32))
+        # gradient arrays exist from construction, as in the reference (cheby_kan.py:44-46), so an
+        # optimizer can pair them with the parameters before the first backward
+        self.grad_w_cheby = np.zeros_like(self.w_cheby)
+        self.grad_w_base = np.zeros_like(self.w_base) if use_base else None
+        self.grad_bias = np.zeros_like(self.bias) if bias else None
         self._saved_x: Optional[np.ndarray] = None
         self._compute = "float32"
 

@@ -83,6 +83,8 @@ SIGNATURES = {
     "kans_layer_forward_host": (c_int, [P, P, P, c_int]),
     "kans_layer_forward_host_ex": (c_int, [P, P, c_int, P, c_int]),
     "kans_layer_time_forward": (c_int, [P, P, c_long, P, c_long, c_int, c_int, c_int, ctypes.POINTER(c_float)]),
+    "kans_layer_time_window": (c_int, [P, P, c_long, P, c_long, c_int, c_float, c_int, ctypes.POINTER(c_float),
+                                       ctypes.POINTER(c_float)]),
     "metal_kan_chain_pipeline_cheby": (c_int, [P, P, c_int, c_int, P, P, P, P, P]),
     "kans_chain_create": (c_int, [P, c_int, ctypes.POINTER(c_void_p)]),
     "kans_chain_destroy": (c_int, [P]),

@@ -77,7 +77,7 @@ class GatedKAN:
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
         self._saved_x = x_2d
-        if x_2d.shape[0] <= MAX_DECODE_B:
+        if 0 < x_2d.shape[0] <= MAX_DECODE_B:
             eng = self._decode_engine()
             if eng is not None:
                 out = eng.forward_host(x_2d if x_2d.dtype == np.float16 else x_2d.astype(np.float32), np.float16, 1)

@@ -148,11 +148,11 @@ class MetalKAN:
             bias = layer.bias if layer.has_bias else None
             if compute == "bfloat16":
                 f32 = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
-                eng.prepare_f32(dt, f32(W), f32(Wb), f32(bias), layer._basis_params())
+                eng.prepare_f32(dt, f32(W), f32(Wb), f32(bias), layer._basis_params(), verify=not layer._frozen)
             else:
                 conv = lambda a: None if a is None else (  # noqa: E731
                     a if (a.dtype == io and a.flags["C_CONTIGUOUS"]) else layer._converted(a, io))
-                eng.prepare(dt, conv(W), conv(Wb), conv(bias), layer._basis_params())
+                eng.prepare(dt, conv(W), conv(Wb), conv(bias), layer._basis_params(), verify=not layer._frozen)
             handles.append(eng.handle.value)
         lib = device.get_metal_bridge()
         key = tuple(handles)

@@ -304,15 +304,27 @@ def quantize_affine(weight: np.ndarray, bits: int, group_size: int):
 
 def dequantize_affine(qweight: np.ndarray, scales: np.ndarray, biases: np.ndarray, bits: int,
                       group_size: int, shape: Tuple[int, int], padded_in: int) -> np.ndarray:
-    """q * scale + bias with two separate fp32 roundings (quantization.py:136-148)."""
+    """q * scale + bias with two separate fp32 roundings (quantization.py:136-148).
+
+    Evaluated in place on one fp32 array (multiply, then add: the same two roundings as
+    ``q * scales + biases``), so full-size matrices need no large temporaries."""
+    ng = qweight.shape[0]
     if bits == 8:
         q = qweight.astype(np.float32)
+    elif bits == 4:
+        nib = np.empty((ng, group_size // 2, 2), dtype=np.uint8)
+        np.bitwise_and(qweight, 0x0F, out=nib[:, :, 0])     # even index: low nibble
+        np.right_shift(qweight, 4, out=nib[:, :, 1])        # odd index: high nibble
+        q = nib.reshape(ng, group_size).astype(np.float32)
+        del nib
     else:
-        q = np.empty((qweight.shape[0], group_size), dtype=np.float32)
-        q[:, 0::2] = (qweight & 0x0F).astype(np.float32)
-        q[:, 1::2] = ((qweight >> 4) & 0x0F).astype(np.float32)
-    restored = (q * scales + biases).reshape(-1, padded_in)
-    return restored[: shape[0], : shape[1]].astype(np.float32)
+        raise ValueError(bits)
+    np.multiply(q, np.asarray(scales, np.float32).reshape(ng, 1), out=q)
+    np.add(q, np.asarray(biases, np.float32).reshape(ng, 1), out=q)
+    restored = q.reshape(-1, padded_in)
+    if restored.shape == tuple(shape):
+        return restored
+    return np.ascontiguousarray(restored[: shape[0], : shape[1]])
 
 
 def quantize_ternary(weight: np.ndarray, group_size: int = 32):
@@ -369,14 +381,31 @@ def ternary_codes(w_packed: np.ndarray, K_dim: int) -> np.ndarray:
     return c.reshape(D_out, words * 16)[:, :K_dim]
 
 
+# value of each 2-bit code {0: -1, 1: 0, 2: +1, 3: 0}, for the four codes of every byte value
+# (code of bits 2t..2t+1 at column t: little-endian uint32 words hold codes 4b..4b+3 in byte b)
+_TERN_LUT = np.array([[(-1.0, 0.0, 1.0, 0.0)[(v >> (2 * t)) & 3] for t in range(4)] for v in range(256)],
+                     dtype=np.float32)
+
+
 def dequantize_ternary(w_packed: np.ndarray, scales: np.ndarray, shape: Tuple[int, int],
                        group_size: int = 32) -> np.ndarray:
-    """{0:-1, 1:0, 2:+1, 3:0}[code] * scale in fp32 (quantization.py:275-286)."""
+    """{0:-1, 1:0, 2:+1, 3:0}[code] * scale in fp32 (quantization.py:275-286).
+
+    Codes are expanded through a per-byte table (``_TERN_LUT``); the product with the scale is exact
+    (the value is -1, 0 or +1)."""
     D_out, K_dim = shape
-    c = ternary_codes(w_packed, K_dim)
-    val = np.where(c < 3, c.astype(np.float32) - np.float32(1.0), np.float32(0.0)).astype(np.float32)
+    wp = np.ascontiguousarray(w_packed, dtype=np.uint32)
+    words = wp.shape[1]
+    val = _TERN_LUT[wp.view(np.uint8).reshape(D_out, words * 4)].reshape(D_out, words * 16)
+    if words * 16 != K_dim:
+        val = np.ascontiguousarray(val[:, :K_dim])
+    sc = np.asarray(scales, np.float32)
+    if K_dim % group_size == 0:
+        v3 = val.reshape(D_out, K_dim // group_size, group_size)
+        np.multiply(v3, sc[:, :, None], out=v3)
+        return val
     g = np.arange(K_dim) // group_size
-    return (val * scales[:, g]).astype(np.float32)
+    return (val * sc[:, g]).astype(np.float32)
 
 
 def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:

@@ -241,6 +241,41 @@ def test_in_place_weight_edit_is_seen(gpu):
     assert not np.array_equal(y0, y1)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_in_place_edit_of_large_weights_is_seen(gpu, dtype):
+    """An optimizer step edits parameters in place (the reference's optim.py: param -= lr * update):
+    arrays over 4 MB are checked by a hash of their bytes, so the next forward sees the edit.  With
+    freeze_weights() (opt-in) only identity is checked until invalidate()."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 512, 512, 5, seed=4)     # w_cheby 512 x 2560 fp32 = 5.2 MB
+    cast(L, dtype)
+    assert getattr(L, L._weight_attr).nbytes > (4 << 20) or dtype == "float16"
+    x = np.random.default_rng(1).uniform(-1, 1, (64, 512)).astype(np.float32)
+    y0 = np.array(L(x), np.float32)
+    L.w_cheby -= (0.05 * np.sign(L.w_cheby)).astype(L.w_cheby.dtype)
+    y1 = np.array(L(x), np.float32)
+    assert not np.array_equal(y0, y1)
+    assert O.rel_err(y1, oracle_of(L, x)) <= TOL[dtype]
+    L.freeze_weights()
+    L.w_cheby *= np.asarray(0.5, L.w_cheby.dtype)
+    y_frozen = np.array(L(x), np.float32)
+    if L.w_cheby.nbytes > (4 << 20):
+        np.testing.assert_array_equal(y_frozen, y1)        # frozen: the large array is not re-read
+    L.invalidate()
+    assert O.rel_err(np.array(L(x), np.float32), oracle_of(L, x)) <= TOL[dtype]
+    L.freeze_weights(False)
+
+
+def test_gradients_exist_from_construction(gpu):
+    """cheby_kan.py:44-46: gradient arrays are zeros before the first backward."""
+    import metal_kans as mk
+    L = mk.ChebyKAN(6, 4, degree=3)
+    assert L.grad_w_cheby.shape == L.w_cheby.shape and not L.grad_w_cheby.any()
+    assert L.grad_w_base.shape == L.w_base.shape and L.grad_bias.shape == (4,)
+    L2 = mk.ChebyKAN(6, 4, degree=3, bias=False, use_base=False)
+    assert L2.grad_w_base is None and L2.grad_bias is None
+
+
 # ---------------------------------------------------------------- reference tests, on this build
 def test_reference_fp16_vs_fp32(gpu):
     """tests/test_metal_kans.py:257-308: fp16 output within atol 1e-2 of fp32."""
@@ -442,6 +477,65 @@ def test_reference_named_entry_points(gpu):
     ms = lib.benchmark_metal_cheby(x.ctypes.data, W.ctypes.data, Wb.ctypes.data, bias.ctypes.data, y.ctypes.data,
                                    B, Di, Do, 5, 1, 1, 1, 3)
     assert ms > 0
+
+
+def test_reference_named_16bit_entry_points(gpu):
+    """The fp16 entry points of the reference (device.py:227-237,263-267; metal_kan_bridge.mm:1890-2151) and
+    their bf16 counterparts, called through the C-ABI with 16-bit bit patterns, against the float64 oracle on
+    the original fp32 arrays at the 16-bit bar: the FastKAN grid travels as fp16 bits (_fp16) or fp32 (_bf16),
+    the B-spline grid as host fp32 [grid_min, inv_h] in both."""
+    from metal_kans._engine import from_bf16_bits, to_bf16_bits
+    lib = gpu
+    rng = np.random.default_rng(16)
+    B, Di, Do = 70, 40, 45
+    x = rng.uniform(-1.15, 1.15, (B, Di)).astype(np.float32)
+    Wb = rng.normal(0, 0.2, (Do, Di)).astype(np.float32)
+    bias = rng.normal(0, 0.1, Do).astype(np.float32)
+    grid, inv = O.rbf_grid((-1.2, 1.2), 7)
+    gp = O.bspline_params(5)
+    cases = {
+        "cheby": (5, {"K": 5}),
+        "rbf": (7, {"grid": grid, "inv_den": inv}),
+        "bspline": (8, {"G": 5, "grid_min": float(gp[0]), "inv_h": float(gp[1])}),
+    }
+    for kind, (K, params) in cases.items():
+        W = rng.normal(0, 0.15, (Do, Di * K)).astype(np.float32)
+        ref = O.kan_forward(kind, x, W, Wb, bias, params)
+        for dt in ("fp16", "bf16"):
+            if dt == "fp16":
+                enc = lambda a: np.ascontiguousarray(a, np.float16).view(np.uint16)  # noqa: E731
+                dec = lambda a: a.view(np.float16).astype(np.float32)  # noqa: E731
+            else:
+                enc = lambda a: to_bf16_bits(a)  # noqa: E731
+                dec = lambda a: from_bf16_bits(a)  # noqa: E731
+            hx, hW, hWb, hb = (enc(a) for a in (x, W, Wb, bias))
+            y = np.zeros((B, Do), np.uint16)
+            args = (hx.ctypes.data, hW.ctypes.data, hWb.ctypes.data)
+            if kind == "cheby":
+                fn = getattr(lib, f"metal_kan_cheby_forward_{dt}")
+                rc = fn(*args, hb.ctypes.data, y.ctypes.data, B, Di, Do, K, 1, 1)
+            elif kind == "rbf":
+                g = enc(grid) if dt == "fp16" else np.ascontiguousarray(grid, np.float32)
+                fn = getattr(lib, f"metal_kan_fastkan_forward_{dt}")
+                rc = fn(*args, g.ctypes.data, hb.ctypes.data, y.ctypes.data, B, Di, Do, K, ctypes.c_float(inv), 1, 1)
+            else:
+                fn = getattr(lib, f"metal_kan_bspline_forward_{dt}")
+                rc = fn(*args, gp.ctypes.data, hb.ctypes.data, y.ctypes.data, B, Di, Do, 5, 3, 1, 1)
+            assert rc == 0, (kind, dt, lib.kans_last_error())
+            e = O.rel_err(dec(y), ref)
+            print(f"{kind} {dt}: rel err {e:.2e}")
+            assert e <= 2e-2, (kind, dt, e)
+            # without the base / bias branches (dummy pointers are not read)
+            ref0 = O.kan_forward(kind, x, W, None, None, params)
+            y0 = np.zeros((B, Do), np.uint16)
+            if kind == "cheby":
+                rc = fn(*args, hb.ctypes.data, y0.ctypes.data, B, Di, Do, K, 0, 0)
+            elif kind == "rbf":
+                rc = fn(*args, g.ctypes.data, hb.ctypes.data, y0.ctypes.data, B, Di, Do, K, ctypes.c_float(inv), 0, 0)
+            else:
+                rc = fn(*args, gp.ctypes.data, hb.ctypes.data, y0.ctypes.data, B, Di, Do, 5, 3, 0, 0)
+            assert rc == 0
+            assert O.rel_err(dec(y0), ref0) <= 2e-2, (kind, dt)
 
 
 def test_reference_chain_entry_point(gpu):

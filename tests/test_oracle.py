@@ -8,6 +8,8 @@ by the reference's own NumPy-fallback quantizers (tests/golden/).
 """
 import os
 
+import math
+
 import numpy as np
 import pytest
 
@@ -196,8 +198,41 @@ def test_gated_forward_against_affine_closed_form():
         W = Lw["W"]
         return W[:, 0::2].sum(1) + np.clip(z, -1, 1) @ W[:, 1::2].T
     g, u = aff(L["g"], x), aff(L["u"], x)
-    hidden = g / (1 + np.exp(-np.clip(g, -20, 20))) * u
+    # hidden = SiLU(g) * u, SiLU from the tanh identity x * sigmoid(x) = x/2 (1 + tanh(x/2)) (|g| < 20 here)
+    assert np.abs(g).max() < 20
+    hidden = 0.5 * g * (1.0 + np.tanh(0.5 * g)) * u
     np.testing.assert_allclose(O.gated_forward(x, L["g"], L["u"], L["d"]), aff(L["d"], hidden), atol=1e-10)
+
+
+def _silu_tanh(x):
+    """x * sigmoid(x) through the identity sigmoid(x) = (1 + tanh(x/2)) / 2, in float64."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(0.5 * x))
+
+
+def test_silu_clipped_and_swiglu_closed_forms():
+    """gated_kan.py:15-16 and fused_kan.metal:2284-2296 clip the exponent argument at +-20, not g itself:
+    inside [-20, 20] both equal x * sigmoid(x) (tanh identity, independent of the exp form), beyond it the
+    exact saturated forms g / (1 + e^-+20) hold, and SwiGLU(0, u) = 0.  A clip of g itself, a clip at another
+    bound, a sign error in the exponent or a dropped factor u fails one of these."""
+    rng = np.random.default_rng(11)
+    g = np.concatenate([rng.uniform(-20, 20, 4000), [-20.0, -19.99, -1e-3, 0.0, 1e-3, 19.99, 20.0]])
+    u = rng.normal(0, 2, g.size)
+    # (absolute bar: 1 + tanh(x/2) cancels near x = -20, where the values are ~1e-7)
+    np.testing.assert_allclose(O.silu_clipped(g), _silu_tanh(g), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(O.swiglu(g, u), (_silu_tanh(g) * u).astype(np.float32), rtol=3e-6, atol=1e-12)
+    # beyond the clip: SiLU_clipped(g) = g / (1 + e^-20) for g > 20 and g / (1 + e^20) for g < -20
+    hi = rng.uniform(20.001, 500, 500)
+    lo = -rng.uniform(20.001, 500, 500)
+    uu = rng.normal(0, 2, 500)
+    np.testing.assert_allclose(O.silu_clipped(hi), hi / (1.0 + math.exp(-20.0)), rtol=1e-15)
+    np.testing.assert_allclose(O.silu_clipped(lo), lo / (1.0 + math.exp(20.0)), rtol=1e-15)
+    np.testing.assert_allclose(O.swiglu(hi, uu), (hi * uu / (1.0 + math.exp(-20.0))).astype(np.float32), rtol=3e-6)
+    np.testing.assert_allclose(O.swiglu(lo, uu), (lo * uu / (1.0 + math.exp(20.0))).astype(np.float32), rtol=3e-6)
+    # not the unclipped SiLU: at g = -30 the unclipped value is -30 e^-30 ~ -2.8e-12, the clipped one -6.2e-8
+    assert abs(O.silu_clipped(np.array([-30.0]))[0] - (-30.0 / (1.0 + math.exp(20.0)))) < 1e-20
+    assert O.swiglu(np.zeros(7), rng.normal(size=7)).tolist() == [0.0] * 7
+    assert O.swiglu(np.array([3.0]), np.array([0.0]))[0] == 0.0
 
 
 # ---------------------------------------------------------------- quantizers
