@@ -316,17 +316,18 @@ def _quantized_layer(lib, fmt, W, Wb, K):
     """kans_qlayer from a float32 (W, W_base) pair packed in the reference format (native quantizers)."""
     d_out, d_in = Wb.shape
     h = ctypes.c_void_p()
-    if fmt == "int4":
+    if fmt in ("int4", "int8"):
         arrs = []
         for A in (W, Wb):
             ng = A.size // 64
-            q = np.empty((ng, 32), np.uint8)
+            q = np.empty((ng, 32 if fmt == "int4" else 64), np.uint8)
             s_ = np.empty(ng, np.float32)
             b_ = np.empty(ng, np.float32)
-            assert lib.metal_kan_quantize_int4(A.ctypes.data, q.ctypes.data, s_.ctypes.data, b_.ctypes.data, ng, 64) == 0
+            qfn = lib.metal_kan_quantize_int4 if fmt == "int4" else lib.metal_kan_quantize_int8
+            assert qfn(A.ctypes.data, q.ctypes.data, s_.ctypes.data, b_.ctypes.data, ng, 64) == 0
             arrs += [q, s_, b_]
-        rc = lib.kans_qlayer_create_int4(d_in, d_out, K, 1, 0, 64, *[a.ctypes.data for a in arrs], None, 0,
-                                         ctypes.byref(h))
+        cfn = lib.kans_qlayer_create_int4 if fmt == "int4" else lib.kans_qlayer_create_int8
+        rc = cfn(d_in, d_out, K, 1, 0, 64, *[a.ctypes.data for a in arrs], None, 0, ctypes.byref(h))
     else:
         arrs = []
         for A in (W, Wb):
@@ -344,14 +345,16 @@ def _quantized_layer(lib, fmt, W, Wb, K):
 
 def run_cfg5(lib, warmup, iters):
     """GatedKAN d=4096, h=11008, K=4 (base on, no bias), all six weight matrices
-    ~N(0, 0.02) then INT4 (group 64) or ternary (group 32); x ~ N(0,1) fp16.  Decode B in {1, 32}
-    through the fused quantized block (one HIP graph, packed weights streamed from HBM): GB/s =
-    algorithmic bytes (packed codes + group parameters + x + y) / time.  Prefill B = 8192 through the
-    per-layer fused kernel on the dequantized weights (fp16): TFLOP/s."""
+    ~N(0, 0.02) then INT4 (group 64) or ternary (group 32), plus the north star's INT8 (group 64); x ~ N(0,1)
+    fp16.  Every line is one whole block forward (gate, up, SwiGLU, down) replayed as one HIP graph on
+    device-resident x / y, timed with HIP events.  Decode B in {1, 32} (INT4 / ternary GEMVs over the packed
+    weights): GB/s = algorithmic bytes (packed codes + group parameters + x + y) / time.  Prefill B = 8192
+    (fused kernels decoding the packed weights into fp16 MFMA tiles, gate|up in one launch with the SwiGLU
+    epilogue): TFLOP/s of 2*B*(2*h*d + d*h)*(K + 1), and the packed bytes per forward."""
     d, hdim, K = 4096, 11008, 4
     rng = np.random.default_rng(1005)
     t0 = time.perf_counter()
-    xs = {B: rng.standard_normal((B, d), dtype=np.float32).astype(np.float16) for B in (1, 32)}
+    xs = {B: rng.standard_normal((B, d), dtype=np.float32).astype(np.float16) for B in (1, 32, 8192)}
     mats = []
     for (di, do) in ((d, hdim), (d, hdim), (hdim, d)):
         W = rng.standard_normal((do, di * K), dtype=np.float32) * np.float32(0.02)
@@ -359,60 +362,49 @@ def run_cfg5(lib, warmup, iters):
         mats.append((W, Wb))
     out = {}
     stream_ceiling = {}
-    for fmt in ("int4", "ternary"):
+    prefill_flops = 2.0 * 8192 * (2 * hdim * d + d * hdim) * (K + 1)
+    for fmt in ("int4", "ternary", "int8"):
         layers = [_quantized_layer(lib, fmt, W, Wb, K) for (W, Wb) in mats]
         blk = ctypes.c_void_p()
         assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0
         for B, x in xs.items():
+            if fmt == "int8" and B != 8192:
+                continue  # INT8 has no decode GEMV: its small batches run the prefill kernel
             xd, yd = DevBuf(lib, x.nbytes), DevBuf(lib, x.nbytes)
             xd.upload(x)
             ms = ctypes.c_float()
-            rc = lib.kans_gated_time(blk, xd.p, 1, yd.p, 1, B, warmup, iters, 1, ctypes.byref(ms))
+            it = iters if B < 8192 else max(5, iters // 10)
+            rc = lib.kans_gated_time(blk, xd.p, 1, yd.p, 1, B, min(warmup, it), it, 1, ctypes.byref(ms))
             if rc:
                 raise RuntimeError(lib.kans_last_error().decode())
             nbytes = lib.kans_gated_stream_bytes(blk, B)
             gbs = nbytes / ms.value / 1e6
-            if fmt not in stream_ceiling:
-                # one read-only streaming kernel over the same number of bytes (kans_stream_ceiling)
-                sb = DevBuf(lib, (nbytes + 15) // 16 * 16)
-                g = ctypes.c_double()
-                assert lib.kans_stream_ceiling(sb.p, (nbytes + 15) // 16 * 16, ctypes.byref(g)) == 0, \
-                    lib.kans_last_error()
-                sb.free()
-                stream_ceiling[fmt] = round(g.value, 1)
-            out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
-                                              "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                                              "stream_ceiling_GB_per_s": stream_ceiling[fmt],
-                                              "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
-                                              "bytes": int(nbytes), "batch": B}
+            if B == 8192:
+                out[f"cfg5_{fmt}_prefill_b8192"] = {
+                    "ms": round(ms.value, 4), "tflops": round(prefill_flops / ms.value / 1e9, 2),
+                    "frac_mfma_peak": round(prefill_flops / ms.value / 1e9 / PEAK["f16"], 4),
+                    "packed_weight_bytes": int(nbytes - 2 * 2 * B * d), "batch": B,
+                    "path": "fused prefill: packed weights decoded into fp16 MFMA tiles; gate|up one launch "
+                            "with the SwiGLU epilogue, then down"}
+            else:
+                if fmt not in stream_ceiling:
+                    # one read-only streaming kernel over the same number of bytes (kans_stream_ceiling)
+                    sb = DevBuf(lib, (nbytes + 15) // 16 * 16)
+                    g = ctypes.c_double()
+                    assert lib.kans_stream_ceiling(sb.p, (nbytes + 15) // 16 * 16, ctypes.byref(g)) == 0, \
+                        lib.kans_last_error()
+                    sb.free()
+                    stream_ceiling[fmt] = round(g.value, 1)
+                out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
+                                                  "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                                  "stream_ceiling_GB_per_s": stream_ceiling[fmt],
+                                                  "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
+                                                  "bytes": int(nbytes), "batch": B}
             xd.free()
             yd.free()
         lib.kans_gated_destroy(blk)
         for hnd in layers:
             lib.kans_qlayer_destroy(hnd)
-    # prefill: per-layer fused fp16 kernel on the INT4-dequantized weights
-    B = 8192
-    import metal_kans as mk
-    tot_ms, flops = 0.0, 0.0
-    for i, (W, Wb) in enumerate(mats):
-        do, di = Wb.shape
-        L = mk.ChebyKAN(di, do, degree=K, bias=False)
-        L.w_cheby, L.w_base = W, Wb
-        mk.to_int4(L)
-        L.half()
-        eng = L._engine()
-        from metal_kans._engine import DT_F16
-        eng.prepare(DT_F16, L.w_cheby, L.w_base, None, ())
-        xd, yd = DevBuf(lib, B * di * 2), DevBuf(lib, B * do * 2)
-        xd.upload(rng.standard_normal((B, di), dtype=np.float32).astype(np.float16))
-        tot_ms += time_layer(lib, eng, xd, yd, B, di, do, warmup, iters)[0]
-        flops += 2.0 * B * do * di * (K + 1)
-        xd.free()
-        yd.free()
-        del L, eng
-    out["cfg5_int4_prefill_b8192"] = {"ms_three_layers": round(tot_ms, 4), "tflops": round(flops / tot_ms / 1e9, 2),
-                                      "frac_mfma_peak": round(flops / tot_ms / 1e9 / PEAK["f16"], 4),
-                                      "path": "per-layer fused fp16 kernel on dequantized INT4 weights"}
     log(f"[bench] cfg5 ({time.perf_counter() - t0:.1f} s): {out}")
     return out
 

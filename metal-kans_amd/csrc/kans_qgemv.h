@@ -5,7 +5,7 @@
 
 namespace kans {
 
-enum QuantKind { Q_INT4 = 0, Q_TERN = 1 };
+enum QuantKind { Q_INT4 = 0, Q_TERN = 1, Q_INT8 = 2 };
 
 // Reduction indices per superchunk (one wave load of a 16-row block).
 constexpr int kQSuper = 128;

@@ -1,7 +1,9 @@
-// Runtime objects of the quantized decode path: a Chebyshev KAN layer held in
-// the reference's packed INT4 / ternary formats (kans_qlayer) and the GatedKAN
-// block of three such layers (kans_gated), plus the reference-named fused
-// ternary entry point.  Kernels: kans_qgemv.hip.
+// Runtime objects of the quantized paths: a Chebyshev KAN layer held in the
+// reference's packed INT8 / INT4 / ternary formats (kans_qlayer) and the
+// GatedKAN block of three such layers (kans_gated), plus the reference-named
+// fused ternary entry point.  Batches of at most 32 rows take the decode GEMVs
+// (kans_qgemv.hip, INT4 and ternary); larger batches, and every INT8 batch,
+// the fused prefill kernel (kans_qprefill.hip).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -10,6 +12,7 @@
 
 #include "kans_api_internal.h"
 #include "kans_qgemv.h"
+#include "kans_qprefill.h"
 
 using namespace kans;
 
@@ -19,22 +22,31 @@ int dequant_ternary_device(const uint32_t* p, const float* s, float* out, int D_
 }
 
 struct kans_qlayer {
-  int quant;                 // Q_INT4 / Q_TERN
+  int quant;                 // Q_INT4 / Q_TERN / Q_INT8
   int D_in, D_out, K, has_base, has_bias, group;
   int Cb, Cw, C_tot;         // superchunks: basis, base, total
   int nw;                    // 16-row blocks per decode row group (qrow_blocks)
   int nrb_pad;               // 16-row blocks, padded to a multiple of nw
+  bool decode = false;       // decode records built (INT4 / ternary)
   DevBuf R, bias;            // re-tiled records (codes + group parameters), bias (bias_dtype)
   int bias_dtype = DT_F32;
   // decode workspace: activation basis, its group sums, split-K partials
   DevBuf Phi, S, part;
   DevBuf cnt;                // arrival counters of the fused epilogue, one per row group, kCntStride ints
                              // apart (0 between launches)
+  // prefill tiles (kans_qprefill.h): codes and group parameters of the basis and base segments
+  bool prefill = false;
+  int p_nfb = 0, p_nob_pad = 0;
+  DevBuf PCb, PCw, PPb, PPw;
+  DevBuf p_part;             // prefill split workspace
+  DevBuf hx, hy;             // staging of the host-pointer forward (grow-only)
 };
 
 struct kans_gated {
   kans_qlayer *gate, *up, *down;
-  DevBuf hidden;  // SwiGLU(gate, up) [B][h] fp32
+  DevBuf hidden;  // SwiGLU(gate, up): [B][h] fp32 (decode, separate kernels) or [B][ld_h] (prefill)
+  DevBuf p_part;  // prefill split workspace
+  DevBuf hx, hy;  // staging of the host-pointer forward (grow-only)
 };
 
 namespace {
@@ -47,6 +59,8 @@ constexpr int kMaxDecodeB = 32;
 bool g_fused_swiglu = true;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
+
+size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
 
 // Weight-record loads of the decode GEMVs: 0 automatic (use_nt), 1 plain,
 // 2 non-temporal.
@@ -109,8 +123,9 @@ int validate_q(int D_in, int D_out, int K, int has_base, int has_bias, int group
     return kans_fail(KANS_ERR_ARG, "bad dims D_in=%d D_out=%d K=%d", D_in, D_out, K);
   if ((has_base != 0 && has_base != 1) || (has_bias != 0 && has_bias != 1))
     return kans_fail(KANS_ERR_ARG, "has_base/has_bias must be 0 or 1");
-  if (quant == Q_INT4 && group != 64)
-    return kans_fail(KANS_ERR_UNSUPPORTED, "fused INT4 path needs group_size 64 (got %d)", group);
+  if ((quant == Q_INT4 || quant == Q_INT8) && group != 64)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "fused INT%d path needs group_size 64 (got %d)", quant == Q_INT8 ? 8 : 4,
+                     group);
   if (quant == Q_TERN && group != 32)
     return kans_fail(KANS_ERR_UNSUPPORTED, "fused ternary path needs group_size 32 (got %d)", group);
   return 0;
@@ -122,6 +137,50 @@ int upload_tmp(DevBuf& d, const void* src, size_t bytes, hipStream_t st) {
   if (rc) return rc;
   if (bytes) HIP_TRY(hipMemcpyAsync(d.p, src, bytes, hipMemcpyHostToDevice, st));
   return 0;
+}
+
+// Prefill tiles of one segment (seg 0: basis, K per feature; seg 1: base, one per feature) from
+// the reference arrays already on the device.
+int build_ptiles(kans_qlayer* L, int seg, const void* codes, long rowbytes, const float* scales,
+                 const float* biases, int gpr, hipStream_t st) {
+  const int Kseg = seg ? 1 : L->K;
+  const int CB = qp_chunk_bytes(L->quant), GS = qp_group(L->quant), PF = qp_param_floats(L->quant);
+  const size_t cbytes = (size_t)L->p_nfb * L->p_nob_pad * 64 * Kseg * CB;
+  const int G_alloc = (16 * L->p_nfb * Kseg + GS - 1) / GS;
+  const long ldp = (long)L->p_nob_pad * 32;
+  DevBuf& C = seg ? L->PCw : L->PCb;
+  DevBuf& P = seg ? L->PPw : L->PPb;
+  int rc = C.reserve(cbytes);
+  if (rc) return rc;
+  if ((rc = P.reserve((size_t)G_alloc * ldp * PF * sizeof(float)))) return rc;
+  hipError_t e;
+  if (L->quant == Q_TERN)
+    e = qp_tile_tern((const unsigned*)codes, (int)rowbytes, scales, gpr, L->D_out, L->D_in, Kseg, L->p_nfb,
+                     L->p_nob_pad, G_alloc, C.p, (float*)P.p, st);
+  else
+    e = qp_tile_affine(L->quant == Q_INT8 ? 8 : 4, (const unsigned char*)codes, rowbytes, scales, biases, gpr,
+                       L->D_out, L->D_in, Kseg, L->p_nfb, L->p_nob_pad, G_alloc, C.p, (float*)P.p, st);
+  if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "prefill re-tiling failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+void prefill_geometry(kans_qlayer* L) {
+  L->prefill = qp_supported(L->quant, L->K);
+  L->p_nfb = (L->D_in + 15) / 16;
+  L->p_nob_pad = round_up((L->D_out + 31) / 32, 8);
+}
+
+QPMat qp_mat(const kans_qlayer* L) {
+  QPMat m;
+  m.cb = (const unsigned char*)L->PCb.p;
+  m.cw = (const unsigned char*)L->PCw.p;
+  m.pb = (const float*)L->PPb.p;
+  m.pw = (const float*)L->PPw.p;
+  m.ldp = (long)L->p_nob_pad * 32;
+  m.nob_pad = L->p_nob_pad;
+  m.D_out = L->D_out;
+  m.bias = L->has_bias ? L->bias.p : nullptr;
+  return m;
 }
 
 int alloc_tiles(kans_qlayer* L) {
@@ -216,25 +275,146 @@ int check_x(const void* X, int x_dtype, long ldx, int D_in, int B) {
   return 0;
 }
 
+// Input of the fused prefill kernel: fp16 or fp32 rows, 16-byte aligned, ldx a
+// multiple of 8 and >= round_up(D_in, 8) (the kernel reads whole 8-feature
+// chunks and ignores the columns past D_in).
+int check_prefill_x(const void* X, int x_dtype, long ldx, int D_in) {
+  if (!X) return kans_fail(KANS_ERR_ARG, "null X");
+  if (x_dtype != DT_F16 && x_dtype != DT_F32)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "prefill path reads fp16 or fp32 inputs (x dtype %d)", x_dtype);
+  if (ldx < round_up(D_in, 8) || ldx % 8 != 0)
+    return kans_fail(KANS_ERR_ARG, "prefill path needs ldx %% 8 == 0 and ldx >= %d (got %ld)", round_up(D_in, 8), ldx);
+  if (((uintptr_t)X & 15) != 0) return kans_fail(KANS_ERR_ARG, "prefill path needs a 16-byte aligned X");
+  return 0;
+}
+
+int check_y(const void* Y, int y_dtype, long ldy, int D_out) {
+  if (!Y || ldy < D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
+  if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
+  return 0;
+}
+
+// Fused prefill forward of one layer (kans_qprefill.hip), any batch.
+int prefill_layer_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                         hipStream_t st) {
+  if (!L->prefill)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4} (K = %d)", L->K);
+  int rc = check_prefill_x(X, x_dtype, ldx, L->D_in);
+  if (rc) return rc;
+  QPLaunch P{};
+  P.qt = L->quant;
+  P.K = L->K;
+  P.has_base = L->has_base;
+  P.X = X;
+  P.ldx = ldx;
+  P.x_dtype = x_dtype;
+  P.m[0] = qp_mat(L);
+  P.m[1] = P.m[0];
+  P.grp = 8;
+  P.bias_dtype = L->bias_dtype;
+  P.Y = Y;
+  P.ldy = ldy;
+  P.y_dtype = y_dtype;
+  P.B = B;
+  P.D_in = L->D_in;
+  P.splits = qp_choose_splits(B, L->D_in, L->D_out, 8);
+  P.epi = QP_EPI_PLAIN;
+  const long pf = qp_part_floats(P);
+  if (pf > 0) {
+    if ((rc = L->p_part.reserve((size_t)pf * sizeof(float)))) return rc;
+    P.part = (float*)L->p_part.p;
+  }
+  HIP_TRY(qp_launch(P, st));
+  return 0;
+}
+
 int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
                           hipStream_t st) {
-  int rc = check_x(X, x_dtype, ldx, L->D_in, B);
+  int rc = check_y(Y, y_dtype, ldy, L->D_out);
   if (rc) return rc;
-  if (!Y || ldy < L->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
-  if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (B == 0) return 0;
+  if (B > kMaxDecodeB || !L->decode) return prefill_layer_locked(L, X, x_dtype, ldx, Y, y_dtype, ldy, B, st);
+  if ((rc = check_x(X, x_dtype, ldx, L->D_in, B))) return rc;
   const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
   return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L)), st);
 }
 
+// GatedKAN prefill: one launch for gate | up with the SwiGLU epilogue into the
+// hidden buffer (fp16 when round16 = 1, fp32 otherwise), one for down.
+int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                         int round16, hipStream_t st) {
+  kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
+  if (!g->prefill || !u->prefill || !d->prefill)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4} (K = %d, %d)", g->K,
+                     d->K);
+  if (g->has_bias && u->has_bias && g->bias_dtype != u->bias_dtype)
+    return kans_fail(KANS_ERR_UNSUPPORTED, "gate and up biases of different dtypes");
+  int rc = check_prefill_x(X, x_dtype, ldx, g->D_in);
+  if (rc) return rc;
+  const int h = g->D_out;
+  const long ldh = round_up(h, 8);
+  const int hdt = round16 == 1 ? DT_F16 : DT_F32;
+  if ((rc = G->hidden.reserve((size_t)B * ldh * dt_bytes(hdt)))) return rc;
+  QPLaunch P1{};
+  P1.qt = g->quant;
+  P1.K = g->K;
+  P1.has_base = g->has_base;
+  P1.X = X;
+  P1.ldx = ldx;
+  P1.x_dtype = x_dtype;
+  P1.m[0] = qp_mat(g);
+  P1.m[1] = qp_mat(u);
+  P1.grp = 4;
+  P1.bias_dtype = g->has_bias ? g->bias_dtype : u->bias_dtype;
+  P1.Y = G->hidden.p;
+  P1.ldy = ldh;
+  P1.y_dtype = hdt;
+  P1.B = B;
+  P1.D_in = g->D_in;
+  P1.splits = qp_choose_splits(B, g->D_in, h, 4);
+  P1.epi = QP_EPI_SWIGLU;
+  P1.round16 = round16;
+  QPLaunch P2{};
+  P2.qt = d->quant;
+  P2.K = d->K;
+  P2.has_base = d->has_base;
+  P2.X = G->hidden.p;
+  P2.ldx = ldh;
+  P2.x_dtype = hdt;
+  P2.m[0] = qp_mat(d);
+  P2.m[1] = P2.m[0];
+  P2.grp = 8;
+  P2.bias_dtype = d->bias_dtype;
+  P2.Y = Y;
+  P2.ldy = ldy;
+  P2.y_dtype = y_dtype;
+  P2.B = B;
+  P2.D_in = h;
+  P2.splits = qp_choose_splits(B, h, d->D_out, 8);
+  P2.epi = QP_EPI_PLAIN;
+  const long pf = std::max(qp_part_floats(P1), qp_part_floats(P2));
+  if (pf > 0) {
+    if ((rc = G->p_part.reserve((size_t)pf * sizeof(float)))) return rc;
+    P1.part = P2.part = (float*)G->p_part.p;
+  }
+  HIP_TRY(qp_launch(P1, st));
+  HIP_TRY(qp_launch(P2, st));
+  return 0;
+}
+
 int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
                          int round16, hipStream_t st) {
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
-  int rc = check_x(X, x_dtype, ldx, g->D_in, B);
+  int rc = check_y(Y, y_dtype, ldy, d->D_out);
   if (rc) return rc;
-  if (!Y || ldy < d->D_out) return kans_fail(KANS_ERR_ARG, "bad Y / ldy");
-  if (y_dtype < DT_F32 || y_dtype > DT_BF16) return kans_fail(KANS_ERR_ARG, "bad y dtype %d", y_dtype);
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (B == 0) return 0;
+  if (B > kMaxDecodeB || !g->decode)
+    return prefill_gated_locked(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, st);
+  if ((rc = check_x(X, x_dtype, ldx, g->D_in, B))) return rc;
   const int h = g->D_out;
   const int ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot, B, g->quant);
   const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot, B, d->quant);
@@ -275,7 +455,83 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, st);
 }
 
-size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
+// Host-pointer forward through grow-only device staging: X [B][D_in] is copied
+// to rows of round_up(D_in, 8) elements (what the prefill kernel reads).
+template <typename Fwd>
+int host_forward(DevBuf& hx, DevBuf& hy, const void* X, int x_dtype, int D_in, void* Y, int y_dtype, int D_out, int B,
+                 Fwd&& fwd) {
+  hipStream_t st = kans_default_stream();
+  const long ldx = round_up(D_in, 8);
+  const size_t xe = dt_bytes(x_dtype), ye = dt_bytes(y_dtype);
+  int rc;
+  if ((rc = hx.reserve((size_t)B * ldx * xe)) || (rc = hy.reserve((size_t)B * D_out * ye))) return rc;
+  HIP_TRY(hipMemcpy2DAsync(hx.p, ldx * xe, X, (size_t)D_in * xe, (size_t)D_in * xe, B, hipMemcpyHostToDevice, st));
+  if ((rc = fwd(hx.p, ldx, hy.p))) return rc;
+  HIP_TRY(hipMemcpyAsync(Y, hy.p, (size_t)B * D_out * ye, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return 0;
+}
+
+// INT4 / INT8 layer from the reference arrays: decode records (INT4 only) and
+// prefill tiles (K in {1, 2, 4}) built from one upload of each array.
+int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                  const void* qweight, const float* scales, const float* biases, const void* qweight_base,
+                  const float* scales_base, const float* biases_base, const void* bias, int bias_dtype,
+                  kans_qlayer** out) {
+  const int quant = bits == 8 ? Q_INT8 : Q_INT4;
+  if (!out || !qweight || !scales || !biases) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (has_base && (!qweight_base || !scales_base || !biases_base))
+    return kans_fail(KANS_ERR_ARG, "has_base set but base arrays are null");
+  int rc = validate_q(D_in, D_out, K, has_base, has_bias, group_size, quant);
+  if (rc) return rc;
+  if (quant == Q_INT8 && !qp_supported(quant, K))
+    return kans_fail(KANS_ERR_UNSUPPORTED, "fused INT8 path takes K in {1, 2, 4} (K = %d)", K);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  if ((rc = kans_ensure_init())) return rc;
+  hipStream_t st = kans_default_stream();
+  auto* L = new kans_qlayer();
+  L->quant = quant;
+  L->D_in = D_in;
+  L->D_out = D_out;
+  L->K = K;
+  L->has_base = has_base;
+  L->has_bias = has_bias;
+  L->group = group_size;
+  layer_geometry(L);
+  prefill_geometry(L);
+  L->decode = quant == Q_INT4;
+  auto fail = [&](int code) { delete L; return code; };
+  if (L->decode && (rc = alloc_tiles(L))) return fail(rc);
+  // one matrix (basis: D_out x D_in*K; base: D_out x D_in), rows padded to the group:
+  // rows of pad / 2 (INT4) or pad (INT8) bytes, pad / 64 groups
+  auto segment = [&](int seg, const void* q, const float* sc, const float* bi) -> int {
+    const long kd = seg ? (long)D_in : (long)D_in * K;
+    const long pad = (kd + group_size - 1) / group_size * group_size;
+    const long gpr = pad / group_size;
+    const long rowbytes = bits == 8 ? pad : pad / 2;
+    DevBuf tq, ts, tb;
+    int r;
+    if ((r = upload_tmp(tq, q, (size_t)D_out * rowbytes, st))) return r;
+    if ((r = upload_tmp(ts, sc, (size_t)D_out * gpr * 4, st))) return r;
+    if ((r = upload_tmp(tb, bi, (size_t)D_out * gpr * 4, st))) return r;
+    if (L->decode) {
+      hipError_t e = qtile_int4((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, rowbytes,
+                                (int)gpr, L->nrb_pad, seg ? L->Cw : L->Cb, seg ? L->Cb : 0, L->C_tot, L->R.p, st);
+      if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e));
+    }
+    if (L->prefill &&
+        (r = build_ptiles(L, seg, tq.p, rowbytes, (const float*)ts.p, (const float*)tb.p, (int)gpr, st)))
+      return r;
+    HIP_TRY(hipStreamSynchronize(st));  // the temporaries die here
+    return 0;
+  };
+  if ((rc = segment(0, qweight, scales, biases))) return fail(rc);
+  if (has_base && (rc = segment(1, qweight_base, scales_base, biases_base))) return fail(rc);
+  if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
+  HIP_TRY(hipStreamSynchronize(st));
+  *out = L;
+  return 0;
+}
 
 }  // namespace
 
@@ -285,53 +541,16 @@ int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bi
                             const void* qweight, const float* scales, const float* biases, const void* qweight_base,
                             const float* scales_base, const float* biases_base, const void* bias, int bias_dtype,
                             kans_qlayer** out) {
-  if (!out || !qweight || !scales || !biases) return kans_fail(KANS_ERR_ARG, "null argument");
-  if (has_base && (!qweight_base || !scales_base || !biases_base))
-    return kans_fail(KANS_ERR_ARG, "has_base set but base arrays are null");
-  int rc = validate_q(D_in, D_out, K, has_base, has_bias, group_size, Q_INT4);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(kans_mutex());
-  if ((rc = kans_ensure_init())) return rc;
-  hipStream_t st = kans_default_stream();
-  auto* L = new kans_qlayer();
-  L->quant = Q_INT4;
-  L->D_in = D_in;
-  L->D_out = D_out;
-  L->K = K;
-  L->has_base = has_base;
-  L->has_bias = has_bias;
-  L->group = group_size;
-  layer_geometry(L);
-  auto fail = [&](int code) { delete L; return code; };
-  if ((rc = alloc_tiles(L))) return fail(rc);
-  // basis matrix W (D_out x D_in*K): padded rows of pad_b nibbles
-  const long pad_b = ((long)D_in * K + group_size - 1) / group_size * group_size;
-  const long gpr_b = pad_b / group_size;
-  DevBuf tq, ts, tb;
-  if ((rc = upload_tmp(tq, qweight, (size_t)D_out * pad_b / 2, st))) return fail(rc);
-  if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
-  if ((rc = upload_tmp(tb, biases, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
-  hipError_t e = qtile_int4((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, pad_b / 2,
-                            (int)gpr_b, L->nrb_pad, L->Cb, 0, L->C_tot, L->R.p, st);
-  if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
-  if (has_base) {
-    const long pad_w = ((long)D_in + group_size - 1) / group_size * group_size;
-    const long gpr_w = pad_w / group_size;
-    DevBuf wq, ws, wb;
-    if ((rc = upload_tmp(wq, qweight_base, (size_t)D_out * pad_w / 2, st))) return fail(rc);
-    if ((rc = upload_tmp(ws, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
-    if ((rc = upload_tmp(wb, biases_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
-    e = qtile_int4((const unsigned char*)wq.p, (const float*)ws.p, (const float*)wb.p, D_out, pad_w / 2, (int)gpr_w,
-                   L->nrb_pad, L->Cw, L->Cb, L->C_tot, L->R.p, st);
-    if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e)));
-    if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
-    HIP_TRY(hipStreamSynchronize(st));  // temporaries die here
-  } else {
-    if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
-    HIP_TRY(hipStreamSynchronize(st));
-  }
-  *out = L;
-  return 0;
+  return create_affine(4, D_in, D_out, K, has_base, has_bias, group_size, qweight, scales, biases, qweight_base,
+                       scales_base, biases_base, bias, bias_dtype, out);
+}
+
+int kans_qlayer_create_int8(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
+                            const void* qweight, const float* scales, const float* biases, const void* qweight_base,
+                            const float* scales_base, const float* biases_base, const void* bias, int bias_dtype,
+                            kans_qlayer** out) {
+  return create_affine(8, D_in, D_out, K, has_base, has_bias, group_size, qweight, scales, biases, qweight_base,
+                       scales_base, biases_base, bias, bias_dtype, out);
 }
 
 int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
@@ -354,26 +573,28 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
   L->has_bias = has_bias;
   L->group = group_size;
   layer_geometry(L);
+  prefill_geometry(L);
+  L->decode = true;
   auto fail = [&](int code) { delete L; return code; };
   if ((rc = alloc_tiles(L))) return fail(rc);
-  const long kb = (long)D_in * K;
-  const int wpr_b = (int)((kb + 15) / 16), gpr_b = (int)((kb + group_size - 1) / group_size);
-  DevBuf tw, ts;
-  if ((rc = upload_tmp(tw, w_packed, (size_t)D_out * wpr_b * 4, st))) return fail(rc);
-  if ((rc = upload_tmp(ts, scales, (size_t)D_out * gpr_b * 4, st))) return fail(rc);
-  hipError_t e = qtile_tern((const unsigned*)tw.p, (const float*)ts.p, D_out, wpr_b, kb, gpr_b, L->nrb_pad, L->Cb, 0,
-                            L->C_tot, L->R.p, st);
-  if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
-  DevBuf bw, bs;
-  if (has_base) {
-    const long kw = D_in;
-    const int wpr_w = (int)((kw + 15) / 16), gpr_w = (int)((kw + group_size - 1) / group_size);
-    if ((rc = upload_tmp(bw, w_packed_base, (size_t)D_out * wpr_w * 4, st))) return fail(rc);
-    if ((rc = upload_tmp(bs, scales_base, (size_t)D_out * gpr_w * 4, st))) return fail(rc);
-    e = qtile_tern((const unsigned*)bw.p, (const float*)bs.p, D_out, wpr_w, kw, gpr_w, L->nrb_pad, L->Cw, L->Cb,
-                   L->C_tot, L->R.p, st);
-    if (e != hipSuccess) return fail(kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e)));
-  }
+  // one matrix (basis: D_out x D_in*K; base: D_out x D_in): rows of ceil(kd / 16) words,
+  // ceil(kd / 32) scales
+  auto segment = [&](int seg, const uint32_t* wp, const float* sc) -> int {
+    const long kd = seg ? (long)D_in : (long)D_in * K;
+    const int wpr = (int)((kd + 15) / 16), gpr = (int)((kd + group_size - 1) / group_size);
+    DevBuf tw, ts;
+    int r;
+    if ((r = upload_tmp(tw, wp, (size_t)D_out * wpr * 4, st))) return r;
+    if ((r = upload_tmp(ts, sc, (size_t)D_out * gpr * 4, st))) return r;
+    hipError_t e = qtile_tern((const unsigned*)tw.p, (const float*)ts.p, D_out, wpr, kd, gpr, L->nrb_pad,
+                              seg ? L->Cw : L->Cb, seg ? L->Cb : 0, L->C_tot, L->R.p, st);
+    if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "ternary re-tiling failed: %s", hipGetErrorString(e));
+    if (L->prefill && (r = build_ptiles(L, seg, tw.p, wpr, (const float*)ts.p, nullptr, gpr, st))) return r;
+    HIP_TRY(hipStreamSynchronize(st));  // the temporaries die here
+    return 0;
+  };
+  if ((rc = segment(0, w_packed, scales))) return fail(rc);
+  if (has_base && (rc = segment(1, w_packed_base, scales_base))) return fail(rc);
   if ((rc = upload_bias(L, bias, bias_dtype))) return fail(rc);
   HIP_TRY(hipStreamSynchronize(st));
   *out = L;
@@ -414,20 +635,18 @@ int kans_qlayer_forward(kans_qlayer* L, const void* X, int x_dtype, long ldx, vo
 }
 
 int kans_qlayer_forward_host(kans_qlayer* L, const void* X, int x_dtype, void* Y, int y_dtype, int B) {
-  if (!L || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
-  if (B <= 0 || B > kMaxDecodeB) return kans_fail(KANS_ERR_ARG, "decode path takes 1 <= B <= %d", kMaxDecodeB);
+  if (!L || (B > 0 && (!X || !Y))) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (x_dtype < DT_F32 || x_dtype > DT_BF16 || y_dtype < DT_F32 || y_dtype > DT_BF16)
+    return kans_fail(KANS_ERR_ARG, "bad x / y dtype");
+  if (B == 0) return 0;
   std::lock_guard<std::mutex> lk(kans_mutex());
   int rc = kans_ensure_init();
   if (rc) return rc;
   hipStream_t st = kans_default_stream();
-  const size_t xb = (size_t)B * L->D_in * dt_bytes(x_dtype), yb = (size_t)B * L->D_out * dt_bytes(y_dtype);
-  DevBuf dx, dy;
-  if ((rc = dx.reserve(xb)) || (rc = dy.reserve(yb))) return rc;
-  HIP_TRY(hipMemcpyAsync(dx.p, X, xb, hipMemcpyHostToDevice, st));
-  if ((rc = qlayer_forward_locked(L, dx.p, x_dtype, L->D_in, dy.p, y_dtype, L->D_out, B, st))) return rc;
-  HIP_TRY(hipMemcpyAsync(Y, dy.p, yb, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return 0;
+  return host_forward(L->hx, L->hy, X, x_dtype, L->D_in, Y, y_dtype, L->D_out, B, [&](void* dx, long ldx, void* dy) {
+    return qlayer_forward_locked(L, dx, x_dtype, ldx, dy, y_dtype, L->D_out, B, st);
+  });
 }
 
 int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out) {
@@ -465,21 +684,19 @@ int kans_gated_forward(kans_gated* G, const void* X, int x_dtype, long ldx, void
 }
 
 int kans_gated_forward_host(kans_gated* G, const void* X, int x_dtype, void* Y, int y_dtype, int B, int round16) {
-  if (!G || !X || !Y) return kans_fail(KANS_ERR_ARG, "null argument");
-  if (B <= 0 || B > kMaxDecodeB) return kans_fail(KANS_ERR_ARG, "decode path takes 1 <= B <= %d", kMaxDecodeB);
+  if (!G || (B > 0 && (!X || !Y))) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (x_dtype < DT_F32 || x_dtype > DT_BF16 || y_dtype < DT_F32 || y_dtype > DT_BF16)
+    return kans_fail(KANS_ERR_ARG, "bad x / y dtype");
+  if (B == 0) return 0;
   std::lock_guard<std::mutex> lk(kans_mutex());
   int rc = kans_ensure_init();
   if (rc) return rc;
   hipStream_t st = kans_default_stream();
   const int d = G->gate->D_in;
-  const size_t xb = (size_t)B * d * dt_bytes(x_dtype), yb = (size_t)B * d * dt_bytes(y_dtype);
-  DevBuf dx, dy;
-  if ((rc = dx.reserve(xb)) || (rc = dy.reserve(yb))) return rc;
-  HIP_TRY(hipMemcpyAsync(dx.p, X, xb, hipMemcpyHostToDevice, st));
-  if ((rc = gated_forward_locked(G, dx.p, x_dtype, d, dy.p, y_dtype, d, B, round16, st))) return rc;
-  HIP_TRY(hipMemcpyAsync(Y, dy.p, yb, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return 0;
+  return host_forward(G->hx, G->hy, X, x_dtype, d, Y, y_dtype, d, B, [&](void* dx, long ldx, void* dy) {
+    return gated_forward_locked(G, dx, x_dtype, ldx, dy, y_dtype, d, B, round16, st);
+  });
 }
 
 // Mean time of one block forward on device-resident X / Y; use_graph replays
@@ -541,9 +758,9 @@ long long kans_gated_stream_bytes(const kans_gated* G, int B) {
     const long kb = (long)L->D_in * L->K;
     for (int part = 0; part < 1 + L->has_base; ++part) {
       const long kdim = part == 0 ? kb : L->D_in;
-      if (L->quant == Q_INT4) {
+      if (L->quant == Q_INT4 || L->quant == Q_INT8) {
         const long pad = (kdim + L->group - 1) / L->group * L->group;
-        total += (long long)L->D_out * (pad / 2 + (pad / L->group) * 8);
+        total += (long long)L->D_out * ((L->quant == Q_INT8 ? pad : pad / 2) + (pad / L->group) * 8);
       } else {
         total += (long long)L->D_out * (((kdim + 15) / 16) * 4 + ((kdim + L->group - 1) / L->group) * 4);
       }

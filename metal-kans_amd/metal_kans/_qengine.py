@@ -1,12 +1,14 @@
-"""Device-resident quantized Chebyshev layers and GatedKAN blocks (decode path).
+"""Device-resident quantized Chebyshev layers and GatedKAN blocks.
 
-A layer quantized with ``to_int4`` (group 64) or ``to_ternary`` (group 32)
-keeps its packed weights in ``_w_cheby_quantized`` / ``_w_cheby_ternary`` (and
-the ``w_base`` counterparts), in the reference's formats (quantization.py:13-99,
-191-246).  ``QLayerEngine`` uploads those packed arrays once and runs the fused
-decode kernel on them, which streams the packed bytes instead of dequantized
-fp32 weights.  The engine is rebuilt when the packed objects change (a new
-``to_int4`` / ``to_ternary``).
+A layer quantized with ``to_int8`` / ``to_int4`` (group 64) or ``to_ternary``
+(group 32) keeps its packed weights in ``_w_cheby_quantized`` /
+``_w_cheby_ternary`` (and the ``w_base`` counterparts), in the reference's
+formats (quantization.py:13-99, 191-246).  ``QLayerEngine`` uploads those packed
+arrays once and runs the fused kernels on them, which move the packed bytes
+instead of dequantized fp32 weights: the decode GEMVs for batches of at most
+``MAX_DECODE_B`` rows (INT4, ternary) and the fused prefill kernel for larger
+batches and for INT8 (Chebyshev degree K in ``PREFILL_K``).  The engine is
+rebuilt when the packed objects change (a new ``to_int4`` / ``to_ternary``).
 """
 from __future__ import annotations
 
@@ -19,11 +21,24 @@ from . import device
 from ._engine import DT_BF16, DT_F16, DT_F32
 
 MAX_DECODE_B = 32
+# Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for
+PREFILL_K = (1, 2, 4)
+KANS_ERR_UNSUPPORTED = -5
+
+
+def fused_batch_ok(fmt: str, K: int, B: int) -> bool:
+    """Whether a batch of B rows of a layer / block in packed format ``fmt`` with K coefficients runs on the
+    fused quantized kernels (else the caller uses the dequantized weights)."""
+    if B <= 0:
+        return False
+    if B <= MAX_DECODE_B and fmt != "int8":
+        return True
+    return K in PREFILL_K
 
 
 def packed_format(layer) -> Optional[str]:
-    """'int4' / 'ternary' when every weight matrix of a Chebyshev layer is packed in a format the fused
-    decode kernel reads (INT4 with group 64, ternary with group 32), else None."""
+    """'int8' / 'int4' / 'ternary' when every weight matrix of a Chebyshev layer is packed in a format the fused
+    kernels read (INT8 / INT4 with group 64, ternary with group 32), else None."""
     from .quantization import QuantizedWeight, TernaryQuantizedWeight
 
     def fmt(attr):
@@ -35,8 +50,8 @@ def packed_format(layer) -> Optional[str]:
             snap = getattr(obj, "_deq_snapshot", None)
             return snap is not None and snap.same(cur)
         q = getattr(layer, f"_{attr}_quantized", None)
-        if isinstance(q, QuantizedWeight) and q.bits == 4 and q.group_size == 64 and live(q):
-            return "int4"
+        if isinstance(q, QuantizedWeight) and q.group_size == 64 and live(q):
+            return "int4" if q.bits == 4 else "int8"
         t = getattr(layer, f"_{attr}_ternary", None)
         if isinstance(t, TernaryQuantizedWeight) and t.group_size == 32 and live(t):
             return "ternary"
@@ -51,7 +66,7 @@ def packed_format(layer) -> Optional[str]:
 
 
 def _key(layer, fmt):
-    suffix = "_quantized" if fmt == "int4" else "_ternary"
+    suffix = "_ternary" if fmt == "ternary" else "_quantized"
     objs = [getattr(layer, "_w_cheby" + suffix, None), getattr(layer, "_w_base" + suffix, None),
             getattr(layer, "bias", None) if layer.has_bias else None]
     return tuple(id(o) for o in objs)
@@ -72,7 +87,8 @@ class QLayerEngine:
         if has_bias:
             bias = np.ascontiguousarray(layer.bias, dtype=np.float32)
         bias_ptr = bias.ctypes.data if bias is not None else None
-        if fmt == "int4":
+        self.K = K
+        if fmt in ("int4", "int8"):
             w = layer._w_cheby_quantized
             wb = layer._w_base_quantized if has_base else None
             arrs = [np.ascontiguousarray(w.qweight), np.ascontiguousarray(w.scales, dtype=np.float32),
@@ -80,9 +96,9 @@ class QLayerEngine:
             barrs = ([np.ascontiguousarray(wb.qweight), np.ascontiguousarray(wb.scales, dtype=np.float32),
                       np.ascontiguousarray(wb.biases, dtype=np.float32)] if wb is not None else [None, None, None])
             ptr = [a.ctypes.data if a is not None else None for a in arrs + barrs]
-            device.check(lib.kans_qlayer_create_int4(self.d_in, self.d_out, K, has_base, has_bias, 64, *ptr,
-                                                     bias_ptr, DT_F32, ctypes.byref(self.handle)),
-                         "kans_qlayer_create_int4")
+            name = f"kans_qlayer_create_{fmt}"
+            device.check(getattr(lib, name)(self.d_in, self.d_out, K, has_base, has_bias, 64, *ptr, bias_ptr, DT_F32,
+                                            ctypes.byref(self.handle)), name)
         else:
             w = layer._w_cheby_ternary
             wb = layer._w_base_ternary if has_base else None
@@ -117,11 +133,28 @@ class QLayerEngine:
         return y
 
 
+def layer_engine(layer) -> Optional["QLayerEngine"]:
+    """The fused quantized engine of a Chebyshev layer that computes in fp16 after ``to_int8`` / ``to_int4`` /
+    ``to_ternary`` (cached on the layer, rebuilt when its packed weights change), else None."""
+    if getattr(layer, "_basis", "") != "cheby" or getattr(layer, "_quantized_from", None) != "float16" \
+            or layer._resolve_compute() != "float16":
+        return None
+    fmt = packed_format(layer)
+    if fmt is None or (fmt == "int8" and int(layer.degree) not in PREFILL_K):
+        return None
+    eng = layer.__dict__.get("_qlayer_engine")
+    if eng is None or not eng.current(layer):
+        eng = QLayerEngine(layer, fmt)
+        layer._qlayer_engine = eng
+    return eng
+
+
 class GatedEngine:
     """Owns the three ``kans_qlayer`` handles and the ``kans_gated`` block of a quantized GatedKAN."""
 
     def __init__(self, block, fmt: str):
         self.fmt = fmt
+        self.K = int(block.degree)
         self.layers = [QLayerEngine(k, fmt) for k in (block.gate_kan, block.up_kan, block.down_kan)]
         self.handle = ctypes.c_void_p()
         device.check(device.get_metal_bridge().kans_gated_create(self.layers[0].handle, self.layers[1].handle,

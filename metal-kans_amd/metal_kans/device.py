@@ -101,6 +101,7 @@ SIGNATURES = {
     "kans_copy_device": (c_int, [P, P, c_size_t, P]),
     # quantized decode path
     "kans_qlayer_create_int4": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P, c_int, P]),
+    "kans_qlayer_create_int8": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P, c_int, P]),
     "kans_qlayer_create_ternary": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P]),
     "kans_qlayer_destroy": (c_int, [P]),
     "kans_qlayer_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, P]),

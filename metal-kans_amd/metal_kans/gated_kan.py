@@ -7,11 +7,13 @@ up = Up(x), hidden = SiLU(gate) * up with the +-20 clip, out = Down(hidden),
 (B, S, d) inputs flattened), ``to_int8`` / ``to_int4`` / ``to_ternary``
 (:239-258), ``parameter_count``.  SwiGLU runs on the GPU for every dtype.
 
-Decode path: a float16 block quantized with ``to_int4()`` (group 64) or
-``to_ternary()`` (group 32) runs batches of at most 32 rows through the fused
-quantized block (``_qengine.GatedEngine``): the packed weights are streamed
-from HBM once per forward instead of being dequantized, and gate/up, SwiGLU and
-down run back to back on the device.  Other cases use the three layers.
+Quantized path: a float16 block quantized with ``to_int8()`` / ``to_int4()``
+(group 64) or ``to_ternary()`` (group 32) runs through the fused quantized block
+(``_qengine.GatedEngine``): the packed weights are read from HBM once per
+forward instead of being dequantized, and gate/up, SwiGLU and down run back to
+back on the device (decode GEMVs up to 32 rows, the fused prefill kernels -- one
+launch for gate|up with the SwiGLU epilogue, one for down -- above, and for
+INT8).  Other cases use the three layers.
 """
 from __future__ import annotations
 
@@ -22,7 +24,7 @@ import numpy as np
 from . import device
 from .cheby_kan import ChebyKAN
 from .quantization import to_int4, to_int8, to_ternary
-from ._qengine import MAX_DECODE_B, GatedEngine, packed_format
+from ._qengine import PREFILL_K, GatedEngine, fused_batch_ok, packed_format
 
 
 class GatedKAN:
@@ -61,11 +63,13 @@ class GatedKAN:
         return out.astype(gate.dtype, copy=False)
 
     def _decode_engine(self) -> Optional[GatedEngine]:
-        """The fused quantized block, when this forward can use it (see module docstring)."""
+        """The fused quantized block, when this block's weights allow it (see module docstring)."""
         if self.dtype != np.float16:
             return None
         fmt = packed_format(self.gate_kan)
         if fmt is None or packed_format(self.up_kan) != fmt or packed_format(self.down_kan) != fmt:
+            return None
+        if fmt == "int8" and self.degree not in PREFILL_K:
             return None
         eng = self.__dict__.get("_qblock")
         if eng is None or eng.fmt != fmt or not eng.current(self):
@@ -77,9 +81,9 @@ class GatedKAN:
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
         self._saved_x = x_2d
-        if 0 < x_2d.shape[0] <= MAX_DECODE_B:
+        if x_2d.shape[0] > 0:
             eng = self._decode_engine()
-            if eng is not None:
+            if eng is not None and fused_batch_ok(eng.fmt, self.degree, x_2d.shape[0]):
                 out = eng.forward_host(x_2d if x_2d.dtype == np.float16 else x_2d.astype(np.float32), np.float16, 1)
                 self._saved_gate = self._saved_up = self._saved_hidden = None
                 if len(orig_shape) > 2:

@@ -1,0 +1,272 @@
+"""GPU parity of the fused quantized prefill path (batches above 32 rows, and INT8 at every batch).
+
+The quantized forward of the reference is forward(x, dequant(quant(W))) in fp32
+(quantization.py:152-188); the fused kernel decodes the packed codes into fp16
+MFMA operands on the GPU.  Each case is checked two ways against the float64
+oracle on the oracle-dequantized weights:
+
+* at the 16-bit bar, max|y - y_ref| / max|y_ref| <= 2e-2;
+* tightly (<= 2e-3) against the oracle that rounds exactly the operands the
+  kernel feeds its MFMAs to fp16 (the dequantized weights, T_k(clamp x) and
+  SiLU(x)): a wrong code, nibble order, group parameter, slot or feature index
+  moves the output by far more than that.
+
+Shapes cover ragged D_in (the last feature block is partly padding, inside an
+affine group), ragged D_out (N-tile padding), several feature blocks per
+split, feature splits (few row tiles), K in {1, 2, 4}, with and without the
+base / bias branches, fp16 and fp32 inputs and fp32 / fp16 / bf16 outputs.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kan_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT = {"float32": 0, "float16": 1, "bfloat16": 2}
+
+
+def quantize(lib, fmt, W):
+    """Packed arrays of W (D_out x kd) in the reference format (native host quantizers), and the
+    oracle's dequantization of them."""
+    rows, kd = W.shape
+    if fmt in ("int4", "int8"):
+        bits = 4 if fmt == "int4" else 8
+        pad = (kd + 63) // 64 * 64
+        Wp = np.zeros((rows, pad), np.float32)
+        Wp[:, :kd] = W
+        ng = rows * pad // 64
+        q = np.empty((ng, 64 * bits // 8), np.uint8)
+        s = np.empty(ng, np.float32)
+        b = np.empty(ng, np.float32)
+        fn = lib.metal_kan_quantize_int4 if bits == 4 else lib.metal_kan_quantize_int8
+        assert fn(Wp.ctypes.data, q.ctypes.data, s.ctypes.data, b.ctypes.data, ng, 64) == 0
+        dq = O.dequantize_affine(q, s.reshape(-1, 1), b.reshape(-1, 1), bits, 64, W.shape, pad)
+        return (q, s, b), dq
+    p = np.zeros((rows, (kd + 15) // 16), np.uint32)
+    s = np.zeros((rows, (kd + 31) // 32), np.float32)
+    assert lib.metal_kan_quantize_ternary(W.ctypes.data, p.ctypes.data, s.ctypes.data, rows, kd, 32) == 0
+    return (p, s), O.dequantize_ternary(p, s, W.shape, 32)
+
+
+def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed):
+    rng = np.random.default_rng(seed)
+    W = rng.normal(0, 0.5 / np.sqrt(d_in * K), (d_out, d_in * K)).astype(np.float32)
+    Wb = rng.normal(0, 0.5 / np.sqrt(d_in), (d_out, d_in)).astype(np.float32)
+    bv = rng.normal(0, 0.1, d_out).astype(np.float32)
+    pw, dw = quantize(lib, fmt, W)
+    pb, db = quantize(lib, fmt, Wb) if base else ((None,) * len(pw), None)
+    h = ctypes.c_void_p()
+    ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+    if fmt == "ternary":
+        rc = lib.kans_qlayer_create_ternary(d_in, d_out, K, int(base), int(bias), 32, ptr(pw[0]), ptr(pw[1]),
+                                            ptr(pb[0]), ptr(pb[1]), ptr(bv) if bias else None, 0, ctypes.byref(h))
+    else:
+        fn = lib.kans_qlayer_create_int4 if fmt == "int4" else lib.kans_qlayer_create_int8
+        rc = fn(d_in, d_out, K, int(base), int(bias), 64, *[ptr(a) for a in pw], *[ptr(a) for a in pb],
+                ptr(bv) if bias else None, 0, ctypes.byref(h))
+    assert rc == 0, lib.kans_last_error()
+    return h, {"W": dw, "W_base": db, "bias": bv if bias else None, "K": K}
+
+
+def oracle(L, x):
+    """float64 forward on the original inputs and the dequantized weights."""
+    return O.kan_forward("cheby", x, L["W"], L["W_base"], L["bias"], {"K": L["K"]})
+
+
+def _oracle_rounded(L, x):
+    """float64 forward with the fp16 MFMA operands: dequantized weights, T_k(clamp x) and SiLU(x) rounded to
+    fp16 (the basis evaluated from x in fp32, as the kernel does)."""
+    r16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)  # noqa: E731
+    x32 = np.asarray(x, np.float32)
+    B, d_in = x32.shape
+    phi = r16(O.cheby_basis(x32, L["K"], np.float32).reshape(B, -1))
+    y = phi @ r16(L["W"]).T
+    if L["W_base"] is not None:
+        y += r16(O.silu(x32)) @ r16(L["W_base"]).T
+    if L["bias"] is not None:
+        y += L["bias"].astype(np.float64)
+    return y
+
+
+def run(lib, h, x, d_out, y_dt="float32"):
+    B = x.shape[0]
+    xdt = DT["float16"] if x.dtype == np.float16 else DT["float32"]
+    y = np.zeros((B, d_out), np.float32 if y_dt == "float32" else np.uint16)
+    rc = lib.kans_qlayer_forward_host(h, x.ctypes.data, xdt, y.ctypes.data, DT[y_dt], B)
+    assert rc == 0, lib.kans_last_error()
+    if y_dt == "float16":
+        return y.view(np.float16).astype(np.float32)
+    if y_dt == "bfloat16":
+        return O.bf16_to_f32(y)
+    return y
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+@pytest.mark.parametrize("K", [1, 2, 4])
+@pytest.mark.parametrize("base,bias", [(True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300), (600, 48, 33)])
+def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
+    lib = gpu
+    print(f"case {fmt} K={K} base={base} bias={bias} B={B} {d_in}->{d_out}", flush=True)
+    h, L = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=B + d_in + K)
+    try:
+        x = np.random.default_rng(K * 7 + d_out).uniform(-1.3, 1.3, (B, d_in)).astype(np.float32)
+        y = run(lib, h, x, d_out)
+        e16 = O.rel_err(y, oracle(L, x))
+        eop = O.rel_err(y, _oracle_rounded(L, x))
+        print(f"  rel err {e16:.2e} (16-bit bar), {eop:.2e} vs operand-rounded oracle")
+        assert e16 <= 2e-2 and eop <= 2e-3, (e16, eop)
+        y2 = run(lib, h, x, d_out)
+        np.testing.assert_array_equal(y.view(np.uint32), y2.view(np.uint32))
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+def test_qlayer_prefill_io_dtypes(gpu, fmt):
+    """fp16 input used as given, fp32 input unrounded; fp16 / bf16 outputs are the fp32 output rounded."""
+    lib = gpu
+    h, L = make_qlayer(lib, fmt, 72, 96, 4, True, True, seed=5)
+    try:
+        x = np.random.default_rng(1).uniform(-1.1, 1.1, (130, 72)).astype(np.float32)
+        y32 = run(lib, h, x, 96)
+        assert O.rel_err(y32, _oracle_rounded(L, x)) <= 2e-3
+        x16 = x.astype(np.float16)
+        y16in = run(lib, h, x16, 96)
+        assert O.rel_err(y16in, _oracle_rounded(L, x16.astype(np.float32))) <= 2e-3
+        yh = run(lib, h, x, 96, "float16")
+        np.testing.assert_array_equal(yh.astype(np.float16), y32.astype(np.float16))
+        yb = run(lib, h, x, 96, "bfloat16")
+        np.testing.assert_array_equal(O.bf16_round(yb), O.bf16_round(y32))
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+def test_qlayer_prefill_rejects_unsupported_K(gpu):
+    """K outside {1, 2, 4}: INT8 layers cannot be built; INT4 / ternary layers decode small batches and report
+    KANS_ERR_UNSUPPORTED (-5) for batches the prefill kernel would take."""
+    lib = gpu
+    rng = np.random.default_rng(0)
+    W = rng.normal(0, 0.1, (40, 24 * 3)).astype(np.float32)
+    (q, s, b), _ = quantize(lib, "int8", W)
+    h = ctypes.c_void_p()
+    assert lib.kans_qlayer_create_int8(24, 40, 3, 0, 0, 64, q.ctypes.data, s.ctypes.data, b.ctypes.data, None, None,
+                                       None, None, 0, ctypes.byref(h)) == -5
+    h4, L = make_qlayer(lib, "int4", 24, 40, 3, True, False, seed=1)
+    try:
+        x = rng.uniform(-1, 1, (33, 24)).astype(np.float32)
+        y = np.zeros((33, 40), np.float32)
+        assert lib.kans_qlayer_forward_host(h4, x.ctypes.data, 0, y.ctypes.data, 0, 33) == -5
+        y8 = run(lib, h4, x[:8], 40)          # decode path: any K
+        assert O.rel_err(y8, _oracle_rounded(L, x[:8])) <= 2e-3
+    finally:
+        lib.kans_qlayer_destroy(h4)
+
+
+# ---------------------------------------------------------------- GatedKAN block
+def make_block(lib, fmt, d, hdim, K=4, bias=False, seed=0):
+    layers, specs = [], []
+    for i, (di, do) in enumerate(((d, hdim), (d, hdim), (hdim, d))):
+        hnd, L = make_qlayer(lib, fmt, di, do, K, True, bias, seed=seed + 17 * i)
+        layers.append(hnd)
+        specs.append(L)
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0
+    return blk, layers, specs
+
+
+def gated_oracle(specs, x, round16):
+    """float64 oracle block on the dequantized weights; with round16 the gate / up / hidden activations are
+    rounded to fp16, as a 16-bit model stores them."""
+    r = (lambda a: a.astype(np.float16).astype(np.float64)) if round16 else (lambda a: a)  # noqa: E731
+    f = lambda L, z: O.kan_forward("cheby", z, L["W"], L["W_base"], L["bias"], {"K": L["K"]})  # noqa: E731
+    g, u = r(f(specs[0], x)), r(f(specs[1], x))
+    return f(specs[2], r(O.silu_clipped(g) * u))
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+@pytest.mark.parametrize("B", [33, 300])
+@pytest.mark.parametrize("d,hdim,bias", [(64, 160, False), (96, 150, True), (256, 520, False)])
+@pytest.mark.parametrize("round16", [1, 0])
+def test_gated_prefill(gpu, fmt, B, d, hdim, bias, round16):
+    """gate|up in one launch (column-paired tile, SwiGLU epilogue), then down: against the oracle block."""
+    lib = gpu
+    print(f"case gated {fmt} B={B} d={d} h={hdim} bias={bias} round16={round16}", flush=True)
+    blk, layers, specs = make_block(lib, fmt, d, hdim, bias=bias, seed=B + d)
+    try:
+        x = np.random.default_rng(B).normal(0, 1, (B, d)).astype(np.float16)
+        y = np.zeros((B, d), np.float16)
+        assert lib.kans_gated_forward_host(blk, x.ctypes.data, 1, y.ctypes.data, 1, B, round16) == 0, \
+            lib.kans_last_error()
+        ref = gated_oracle(specs, x.astype(np.float64), round16)
+        e = O.rel_err(y.astype(np.float32), ref)
+        print(f"  rel err {e:.2e}")
+        assert np.isfinite(y.astype(np.float32)).all()
+        assert e <= 2e-2
+        y2 = np.zeros_like(y)
+        assert lib.kans_gated_forward_host(blk, x.ctypes.data, 1, y2.ctypes.data, 1, B, round16) == 0
+        np.testing.assert_array_equal(y.view(np.uint16), y2.view(np.uint16))
+    finally:
+        lib.kans_gated_destroy(blk)
+        for hnd in layers:
+            lib.kans_qlayer_destroy(hnd)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+def test_gated_decode_and_prefill_agree(gpu, fmt):
+    """The same rows through the decode block (B = 32) and the prefill block (B = 33, one extra row) give the
+    same outputs to fp16 rounding."""
+    lib = gpu
+    blk, layers, specs = make_block(lib, fmt, 128, 256, seed=9)
+    try:
+        x = np.random.default_rng(3).normal(0, 1, (33, 128)).astype(np.float16)
+        yd = np.zeros((32, 128), np.float16)
+        yp = np.zeros((33, 128), np.float16)
+        assert lib.kans_gated_forward_host(blk, x.ctypes.data, 1, yd.ctypes.data, 1, 32, 1) == 0
+        assert lib.kans_gated_forward_host(blk, x.ctypes.data, 1, yp.ctypes.data, 1, 33, 1) == 0
+        assert O.rel_err(yp[:32].astype(np.float32), yd.astype(np.float32)) <= 5e-3
+    finally:
+        lib.kans_gated_destroy(blk)
+        for hnd in layers:
+            lib.kans_qlayer_destroy(hnd)
+
+
+# ---------------------------------------------------------------- Python layer API
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+def test_python_quantized_fp16_layer_uses_packed_weights(gpu, quant):
+    """ChebyKAN(...).half().to_<quant>() keeps fp16 compute and runs on its packed weights at every batch
+    (decode GEMV up to 32 rows for INT4 / ternary, the prefill kernel above and for INT8)."""
+    import metal_kans as mk
+    np.random.seed(7)
+    L = mk.ChebyKAN(80, 50, degree=4)
+    L.bias = np.random.normal(0, 0.1, 50).astype(np.float32)
+    L.half()
+    getattr(mk, f"to_{quant}")(L)
+    spec = {"W": L.w_cheby, "W_base": L.w_base, "bias": L.bias.astype(np.float32), "K": 4}
+    for B in (5, 300):
+        x = np.random.default_rng(B).uniform(-1.1, 1.1, (B, 80)).astype(np.float32)
+        y = L(x)
+        assert y.dtype == np.float16 and y.shape == (B, 50)
+        assert L.__dict__.get("_qlayer_engine") is not None
+        assert O.rel_err(y.astype(np.float32), _oracle_rounded(spec, x)) <= 2e-3
+        assert O.rel_err(y.astype(np.float32), oracle(spec, x)) <= 2e-2
+
+
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+def test_python_gatedkan_prefill(gpu, quant):
+    """GatedKAN(dtype=float16).to_<quant>() at B > 32 runs the fused prefill block."""
+    import metal_kans as mk
+    np.random.seed(4)
+    blk = mk.GatedKAN(d_model=96, d_ffn=200, degree=4, dtype=np.float16)
+    getattr(blk, f"to_{quant}")()
+    x = np.random.default_rng(2).normal(0, 1, (3, 50, 96)).astype(np.float16)
+    out = blk(x)
+    assert blk.__dict__.get("_qblock") is not None
+    assert out.shape == (3, 50, 96) and out.dtype == np.float16
+    specs = [{"W": k.w_cheby, "W_base": k.w_base, "bias": None, "K": 4}
+             for k in (blk.gate_kan, blk.up_kan, blk.down_kan)]
+    ref = gated_oracle(specs, x.reshape(-1, 96).astype(np.float64), 1)
+    assert O.rel_err(out.reshape(-1, 96).astype(np.float32), ref) <= 2e-2
