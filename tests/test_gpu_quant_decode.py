@@ -168,8 +168,11 @@ def test_qlayer_rejects(gpu):
     try:
         x = np.zeros((33, 64), np.float32)
         y = np.empty((33, 32), np.float32)
-        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 33) < 0  # B > 32
-        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 0) < 0
+        # B > 32 runs the prefill kernel, B = 0 does nothing, B < 0 and bad dtypes are refused
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 33) == 0
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, 0) == 0
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, DT_F32, y.ctypes.data, DT_F32, -1) < 0
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 7, y.ctypes.data, DT_F32, 4) < 0
     finally:
         lib.kans_qlayer_destroy(h)
     out = ctypes.c_void_p()
