@@ -286,6 +286,14 @@ int kans_gated_forward(kans_gated* block, const void* X, int x_dtype, long ldx, 
                        int B, int round16, void* stream);
 int kans_gated_forward_host(kans_gated* block, const void* X, int x_dtype, void* Y, int y_dtype, int B,
                             int round16);
+/* As kans_gated_forward, allocating nothing: every workspace (activation basis, split-K partials, arrival
+ * counters, prefill hidden state) is carved from one 64 MiB device array per GPU that the library holds
+ * until the process ends.  No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  A call whose
+ * workspace exceeds 64 MiB returns KANS_ERR_ARG (the config-5 block needs ~49 MB at B = 32).  Calls on one
+ * GPU share the array: calls that overlap (other streams or threads) race. */
+int kans_gated_forward_noalloc(kans_gated* block, const void* X, int x_dtype, long ldx, void* Y, int y_dtype,
+                               long ldy, int B, int round16, void* stream);
 /* mean ms per block forward on device X / Y (use_graph: replay one captured HIP graph) */
 int kans_gated_time(kans_gated* block, const void* X, int x_dtype, void* Y, int y_dtype, int B, int warmup,
                     int iters, int use_graph, float* ms);

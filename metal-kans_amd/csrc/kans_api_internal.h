@@ -24,6 +24,9 @@ struct DenseLaunch {
 }  // namespace kans
 
 int kans_fail(int code, const char* fmt, ...);
+// Per-device set-up of kans_gated_forward_noalloc's scratch (kans_qruntime.hip);
+// called by the library's initialisation with `device` current.
+int kans_noalloc_setup(int device);
 hipStream_t kans_default_stream();
 
 // Library lock (serialises every entry point that touches device state), lazy

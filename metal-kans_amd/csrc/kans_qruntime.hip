@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
 #include <cstring>
 #include <vector>
 
@@ -206,16 +207,34 @@ int upload_bias(kans_qlayer* L, const void* bias, int bias_dtype) {
   return 0;
 }
 
+// Device workspace of one decode forward: the activation basis (Phi, S) and the
+// split-K partial sums of each GEMV (the layer's, or gate|up then down), the
+// fused epilogue's arrival counters (0 between launches) and, with the
+// separate-kernel SwiGLU, the hidden state.
+struct DecodeWS {
+  _Float16* phi = nullptr;
+  float2* s = nullptr;
+  float* part = nullptr;
+  _Float16* phi2 = nullptr;
+  float2* s2 = nullptr;
+  float* part2 = nullptr;
+  int* cnt = nullptr;
+  float* hidden = nullptr;
+};
+
+size_t phi_bytes(const kans_qlayer* L, int B) { return (size_t)mp_of(B) * L->C_tot * kQSuper * sizeof(_Float16); }
+size_t s_bytes(const kans_qlayer* L, int B) { return (size_t)L->C_tot * mp_of(B) * sizeof(float2); }
+size_t part_bytes(int B, int ksplit, int N_total) { return (size_t)ksplit * B * N_total * sizeof(float); }
+
 int reserve_decode(kans_qlayer* L, int B, int ksplit, int N_total) {
-  const int MP = mp_of(B);
-  int rc = L->Phi.reserve((size_t)MP * L->C_tot * kQSuper * sizeof(_Float16));
+  int rc = L->Phi.reserve(phi_bytes(L, B));
   if (rc) return rc;
-  rc = L->S.reserve((size_t)L->C_tot * MP * sizeof(float2));
-  if (rc) return rc;
-  return L->part.reserve((size_t)ksplit * B * N_total * sizeof(float));
+  if ((rc = L->S.reserve(s_bytes(L, B)))) return rc;
+  return L->part.reserve(part_bytes(B, ksplit, N_total));
 }
 
-int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hipStream_t st) {
+int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, _Float16* phi, float2* S,
+                hipStream_t st) {
   QPrep P;
   P.X = X;
   P.x_dtype = x_dtype;
@@ -227,15 +246,16 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, hip
   P.has_base = L->has_base;
   P.Cb = L->Cb;
   P.C_tot = L->C_tot;
-  P.Phi = (_Float16*)L->Phi.p;
-  P.S = (float2*)L->S.p;
+  P.Phi = phi;
+  P.S = S;
   HIP_TRY(qprep(L->quant, P, st));
   return 0;
 }
 
-// GEMV of layer a (and b, sharing a's activations): split-K partial sums in
-// a->part ([ksplit][B][a.D_out + b.D_out]), then the epilogue `epi`.
-int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, int nt, hipStream_t st) {
+// GEMV of layer a (and b, sharing a's activations phi / S): split-K partial sums
+// in part ([ksplit][B][a.D_out + b.D_out]), then the epilogue `epi`.
+int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, int nt, const _Float16* phi,
+                const float2* S, float* part, hipStream_t st) {
   QGemv G;
   G.rec0 = a->R.p;
   G.D_out0 = a->D_out;
@@ -246,11 +266,11 @@ int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& e
   G.n_rg = G.rg_split + (b ? b->nrb_pad / b->nw : 0);
   G.ksplit = ksplit;
   G.C_tot = a->C_tot;
-  G.Phi = (const _Float16*)a->Phi.p;
-  G.S = (const float2*)a->S.p;
+  G.Phi = phi;
+  G.S = S;
   G.B = B;
   G.MP = mp_of(B);
-  G.part = (float*)a->part.p;
+  G.part = part;
   G.N_total = a->D_out + (b ? b->D_out : 0);
   G.epi = epi;
   G.nt = nt;
@@ -258,12 +278,12 @@ int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& e
   return 0;
 }
 
-// GEMV of layer L on its prepared Phi / S, then the split-K reduce + bias into Y.
-int gemv_reduce_locked(kans_qlayer* L, int B, int ks, void* Y, int y_dtype, long ldy, int nt, hipStream_t st) {
-  int rc = gemv_locked(L, nullptr, B, ks, QEpi{}, nt, st);
+// GEMV of layer L on its prepared phi / S, then the split-K reduce + bias into Y.
+int gemv_reduce_locked(kans_qlayer* L, int B, int ks, void* Y, int y_dtype, long ldy, int nt, const _Float16* phi,
+                       const float2* S, float* part, hipStream_t st) {
+  int rc = gemv_locked(L, nullptr, B, ks, QEpi{}, nt, phi, S, part, st);
   if (rc) return rc;
-  HIP_TRY(qreduce((const float*)L->part.p, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y,
-                  y_dtype, ldy, st));
+  HIP_TRY(qreduce(part, ks, B, L->D_out, L->has_bias ? L->bias.p : nullptr, L->bias_dtype, Y, y_dtype, ldy, st));
   return 0;
 }
 
@@ -338,14 +358,22 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   if ((rc = check_x(X, x_dtype, ldx, L->D_in, B))) return rc;
   const int ks = choose_ksplit(L->nrb_pad / L->nw, L->C_tot, B, L->quant);
   if ((rc = reserve_decode(L, B, ks, L->D_out))) return rc;
-  if ((rc = prep_locked(L, X, x_dtype, ldx, B, st))) return rc;
-  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L)), st);
+  _Float16* phi = (_Float16*)L->Phi.p;
+  float2* S = (float2*)L->S.p;
+  if ((rc = prep_locked(L, X, x_dtype, ldx, B, phi, S, st))) return rc;
+  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L)), phi, S, (float*)L->part.p, st);
 }
 
 // GatedKAN prefill: one launch for gate | up with the SwiGLU epilogue into the
 // hidden buffer (fp16 when round16 = 1, fp32 otherwise), one for down.
-int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
-                         int round16, hipStream_t st) {
+// The two launches of a GatedKAN prefill forward, and the workspace they need.
+struct GatedPrefill {
+  QPLaunch P1, P2;
+  size_t hidden_bytes = 0, part_bytes = 0;
+};
+
+int plan_gated_prefill(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                       int round16, GatedPrefill& GP) {
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
   if (!g->prefill || !u->prefill || !d->prefill)
     return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4} (K = %d, %d)", g->K,
@@ -357,8 +385,9 @@ int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   const int h = g->D_out;
   const long ldh = round_up(h, 8);
   const int hdt = round16 == 1 ? DT_F16 : DT_F32;
-  if ((rc = G->hidden.reserve((size_t)B * ldh * dt_bytes(hdt)))) return rc;
-  QPLaunch P1{};
+  QPLaunch& P1 = GP.P1;
+  QPLaunch& P2 = GP.P2;
+  P1 = QPLaunch{};
   P1.qt = g->quant;
   P1.K = g->K;
   P1.has_base = g->has_base;
@@ -369,7 +398,6 @@ int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   P1.m[1] = qp_mat(u);
   P1.grp = 4;
   P1.bias_dtype = g->has_bias ? g->bias_dtype : u->bias_dtype;
-  P1.Y = G->hidden.p;
   P1.ldy = ldh;
   P1.y_dtype = hdt;
   P1.B = B;
@@ -377,11 +405,10 @@ int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   P1.splits = qp_choose_splits(B, g->D_in, h, 4);
   P1.epi = QP_EPI_SWIGLU;
   P1.round16 = round16;
-  QPLaunch P2{};
+  P2 = QPLaunch{};
   P2.qt = d->quant;
   P2.K = d->K;
   P2.has_base = d->has_base;
-  P2.X = G->hidden.p;
   P2.ldx = ldh;
   P2.x_dtype = hdt;
   P2.m[0] = qp_mat(d);
@@ -395,14 +422,76 @@ int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   P2.D_in = h;
   P2.splits = qp_choose_splits(B, h, d->D_out, 8);
   P2.epi = QP_EPI_PLAIN;
-  const long pf = std::max(qp_part_floats(P1), qp_part_floats(P2));
-  if (pf > 0) {
-    if ((rc = G->p_part.reserve((size_t)pf * sizeof(float)))) return rc;
-    P1.part = P2.part = (float*)G->p_part.p;
-  }
-  HIP_TRY(qp_launch(P1, st));
-  HIP_TRY(qp_launch(P2, st));
+  GP.hidden_bytes = (size_t)B * ldh * dt_bytes(hdt);
+  GP.part_bytes = (size_t)std::max(qp_part_floats(P1), qp_part_floats(P2)) * sizeof(float);
   return 0;
+}
+
+// Enqueue a planned prefill forward with its workspace (part may be null when unsplit).
+int run_gated_prefill(GatedPrefill& GP, void* hidden, float* part, hipStream_t st) {
+  GP.P1.Y = hidden;
+  GP.P2.X = hidden;
+  GP.P1.part = GP.P2.part = part;
+  HIP_TRY(qp_launch(GP.P1, st));
+  HIP_TRY(qp_launch(GP.P2, st));
+  return 0;
+}
+
+int prefill_gated_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                         int round16, hipStream_t st) {
+  GatedPrefill GP;
+  int rc = plan_gated_prefill(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, GP);
+  if (rc) return rc;
+  if ((rc = G->hidden.reserve(GP.hidden_bytes))) return rc;
+  if (GP.part_bytes && (rc = G->p_part.reserve(GP.part_bytes))) return rc;
+  return run_gated_prefill(GP, G->hidden.p, GP.part_bytes ? (float*)G->p_part.p : nullptr, st);
+}
+
+// Decode GEMV split-K of the gated block's two GEMVs for batch B.
+void gated_ksplits(const kans_gated* G, int B, int* ks1, int* ks2) {
+  const kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
+  *ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot, B, g->quant);
+  *ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot, B, d->quant);
+}
+
+// The decode forward of a gated block (1 <= B <= 32) on the workspace ws (sized for B, ks1, ks2).
+int gated_decode(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
+                 int round16, int ks1, int ks2, const DecodeWS& ws, hipStream_t st) {
+  kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
+  const int h = g->D_out;
+  int rc;
+  if ((rc = prep_locked(g, X, x_dtype, ldx, B, ws.phi, ws.s, st))) return rc;
+  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d));
+  if (g_fused_swiglu) {
+    // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
+    // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
+    QEpi e1;
+    e1.kind = QEPI_SWIGLU;
+    e1.counters = ws.cnt;
+    e1.bias = g->has_bias ? g->bias.p : nullptr;
+    e1.bias_dtype = g->bias_dtype;
+    e1.bias_u = u->has_bias ? u->bias.p : nullptr;
+    e1.bias_u_dtype = u->bias_dtype;
+    e1.round16 = round16;
+    e1.K2 = d->K;
+    e1.has_base2 = d->has_base;
+    e1.Cb2 = d->Cb;
+    e1.C_tot2 = d->C_tot;
+    e1.Phi2 = ws.phi2;
+    e1.S2 = ws.s2;
+    if (B <= kSmallB && ks1 <= kMaxEpiSplit) {
+      if ((rc = gemv_locked(g, u, B, ks1, e1, nt, ws.phi, ws.s, ws.part, st))) return rc;
+    } else {
+      if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, ws.phi, ws.s, ws.part, st))) return rc;
+      HIP_TRY(qswiglu_basis(g->quant, e1, ws.part, ks1, B, mp_of(B), h, st));
+    }
+    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, ws.phi2, ws.s2, ws.part2, st);
+  }
+  if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, ws.phi, ws.s, ws.part, st))) return rc;
+  HIP_TRY(qswiglu(ws.part, ks1, B, h, g->has_bias ? g->bias.p : nullptr, g->bias_dtype,
+                  u->has_bias ? u->bias.p : nullptr, u->bias_dtype, round16, ws.hidden, st));
+  if ((rc = prep_locked(d, ws.hidden, DT_F32, h, B, ws.phi2, ws.s2, st))) return rc;
+  return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, ws.phi2, ws.s2, ws.part2, st);
 }
 
 int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
@@ -415,45 +504,74 @@ int gated_forward_locked(kans_gated* G, const void* X, int x_dtype, long ldx, vo
   if (B > kMaxDecodeB || !g->decode)
     return prefill_gated_locked(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, st);
   if ((rc = check_x(X, x_dtype, ldx, g->D_in, B))) return rc;
-  const int h = g->D_out;
-  const int ks1 = choose_ksplit((g->nrb_pad + u->nrb_pad) / g->nw, g->C_tot, B, g->quant);
-  const int ks2 = choose_ksplit(d->nrb_pad / d->nw, d->C_tot, B, d->quant);
-  if ((rc = reserve_decode(g, B, ks1, 2 * h))) return rc;
+  int ks1, ks2;
+  gated_ksplits(G, B, &ks1, &ks2);
+  if ((rc = reserve_decode(g, B, ks1, 2 * g->D_out))) return rc;
   if ((rc = reserve_decode(d, B, ks2, d->D_out))) return rc;
-  if ((rc = prep_locked(g, X, x_dtype, ldx, B, st))) return rc;
-  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d));
-  if (g_fused_swiglu) {
-    // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
-    // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
-    QEpi e1;
-    e1.kind = QEPI_SWIGLU;
-    e1.counters = (int*)g->cnt.p;
-    e1.bias = g->has_bias ? g->bias.p : nullptr;
-    e1.bias_dtype = g->bias_dtype;
-    e1.bias_u = u->has_bias ? u->bias.p : nullptr;
-    e1.bias_u_dtype = u->bias_dtype;
-    e1.round16 = round16;
-    e1.K2 = d->K;
-    e1.has_base2 = d->has_base;
-    e1.Cb2 = d->Cb;
-    e1.C_tot2 = d->C_tot;
-    e1.Phi2 = (_Float16*)d->Phi.p;
-    e1.S2 = (float2*)d->S.p;
-    if (B <= kSmallB && ks1 <= kMaxEpiSplit) {
-      if ((rc = gemv_locked(g, u, B, ks1, e1, nt, st))) return rc;
-    } else {
-      if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, st))) return rc;
-      HIP_TRY(qswiglu_basis(g->quant, e1, (const float*)g->part.p, ks1, B, mp_of(B), h, st));
-    }
-    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, st);
-  }
-  if ((rc = G->hidden.reserve((size_t)B * h * sizeof(float)))) return rc;
-  if ((rc = gemv_locked(g, u, B, ks1, QEpi{}, nt, st))) return rc;
-  HIP_TRY(qswiglu((const float*)g->part.p, ks1, B, h, g->has_bias ? g->bias.p : nullptr, g->bias_dtype,
-                  u->has_bias ? u->bias.p : nullptr, u->bias_dtype, round16, (float*)G->hidden.p, st));
-  if ((rc = prep_locked(d, G->hidden.p, DT_F32, h, B, st))) return rc;
-  return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, st);
+  if (!g_fused_swiglu && (rc = G->hidden.reserve((size_t)B * g->D_out * sizeof(float)))) return rc;
+  DecodeWS ws;
+  ws.phi = (_Float16*)g->Phi.p;
+  ws.s = (float2*)g->S.p;
+  ws.part = (float*)g->part.p;
+  ws.phi2 = (_Float16*)d->Phi.p;
+  ws.s2 = (float2*)d->S.p;
+  ws.part2 = (float*)d->part.p;
+  ws.cnt = (int*)g->cnt.p;
+  ws.hidden = (float*)G->hidden.p;
+  return gated_decode(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, ks1, ks2, ws, st);
 }
+
+// ---------------------------------------------------------------------------
+// Workspace of kans_gated_forward_noalloc: one file-scope device array, held by
+// every GPU the library runs on until the process ends.  Its first kScratchCnt
+// bytes are the fused epilogue's arrival counters (zeroed once at set-up; every
+// launch leaves them at zero again); one call's buffers are carved after them.
+// Calls on one GPU share the array, so calls that overlap (other streams or
+// threads) race.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the per-device address from hipGetSymbolAddress is used
+// instead.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr size_t kScratchCnt = size_t(256) << 10;  // 2048 row groups x kCntStride ints
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::map<int, char*> g_scratch;  // device -> address of that device's scratch (kans_mutex held)
+
+__global__ void k_zero_words(unsigned* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Carves 256-byte aligned buffers from the scratch after the counters.
+struct ScratchCarve {
+  char* base;
+  size_t off = kScratchCnt, need = kScratchCnt;
+  template <typename T>
+  T* take(size_t bytes) {
+    T* p = reinterpret_cast<T*>(base + off);
+    off += (bytes + 255) / 256 * 256;
+    need = off;
+    return p;
+  }
+};
+
+}  // namespace
+
+// Set-up of the scratch on `device` (current): its address, and zeroed counters.
+// Called once per device from the library's initialisation.
+int kans_noalloc_setup(int device) {
+  if (g_scratch.count(device)) return 0;
+  void* ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr)
+    return kans_fail(KANS_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+  hipStream_t st = kans_default_stream();
+  hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, st, (unsigned*)ptr, (long)(kScratchCnt / 4));
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(st));
+  g_scratch[device] = (char*)ptr;
+  return 0;
+}
+
+namespace {
 
 // Host-pointer forward through grow-only device staging: X [B][D_in] is copied
 // to rows of round_up(D_in, 8) elements (what the prefill kernel reads).
@@ -697,6 +815,56 @@ int kans_gated_forward_host(kans_gated* G, const void* X, int x_dtype, void* Y, 
   return host_forward(G->hx, G->hy, X, x_dtype, d, Y, y_dtype, d, B, [&](void* dx, long ldx, void* dy) {
     return gated_forward_locked(G, dx, x_dtype, ldx, dy, y_dtype, d, B, round16, st);
   });
+}
+
+// As kans_gated_forward, with every workspace carved from the library's
+// per-GPU scratch array (no allocation on this path).
+int kans_gated_forward_noalloc(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy,
+                               int B, int round16, void* stream) {
+  if (!G) return kans_fail(KANS_ERR_ARG, "null block");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  auto it = g_scratch.find(dev);
+  if (it == g_scratch.end()) return kans_fail(KANS_ERR_STATE, "no scratch set up on device %d", dev);
+  hipStream_t st = stream ? (hipStream_t)stream : kans_default_stream();
+  kans_qlayer *g = G->gate, *d = G->down;
+  if ((rc = check_y(Y, y_dtype, ldy, d->D_out))) return rc;
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  if (B == 0) return 0;
+  ScratchCarve sc{it->second};
+  auto too_big = [&](size_t need) {
+    return kans_fail(KANS_ERR_ARG,
+                     "kans_gated_forward_noalloc: B=%d needs %zu bytes of workspace, above the %zu-byte scratch "
+                     "(use kans_gated_forward)", B, need, kScratchBytes);
+  };
+  if (B > kMaxDecodeB || !g->decode) {
+    GatedPrefill GP;
+    if ((rc = plan_gated_prefill(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, GP))) return rc;
+    void* hidden = sc.take<char>(GP.hidden_bytes);
+    float* part = GP.part_bytes ? sc.take<float>(GP.part_bytes) : nullptr;
+    if (sc.need > kScratchBytes) return too_big(sc.need);
+    return run_gated_prefill(GP, hidden, part, st);
+  }
+  if ((rc = check_x(X, x_dtype, ldx, g->D_in, B))) return rc;
+  if ((size_t)(g->nrb_pad / g->nw) * kCntStride * sizeof(int) > kScratchCnt)
+    return kans_fail(KANS_ERR_ARG, "kans_gated_forward_noalloc: %d gate row groups exceed the scratch counters",
+                     g->nrb_pad / g->nw);
+  int ks1, ks2;
+  gated_ksplits(G, B, &ks1, &ks2);
+  DecodeWS ws;
+  ws.cnt = (int*)it->second;
+  ws.phi = sc.take<_Float16>(phi_bytes(g, B));
+  ws.s = sc.take<float2>(s_bytes(g, B));
+  ws.part = sc.take<float>(part_bytes(B, ks1, 2 * g->D_out));
+  ws.phi2 = sc.take<_Float16>(phi_bytes(d, B));
+  ws.s2 = sc.take<float2>(s_bytes(d, B));
+  ws.part2 = sc.take<float>(part_bytes(B, ks2, d->D_out));
+  if (!g_fused_swiglu) ws.hidden = sc.take<float>((size_t)B * g->D_out * sizeof(float));
+  if (sc.need > kScratchBytes) return too_big(sc.need);
+  return gated_decode(G, X, x_dtype, ldx, Y, y_dtype, ldy, B, round16, ks1, ks2, ws, st);
 }
 
 // Mean time of one block forward on device-resident X / Y; use_graph replays

@@ -92,6 +92,8 @@ static int ensure_init() {
     return kans_fail(KANS_ERR_NODEV, "device %d is %s; this library is built for gfx950 only", g_device,
                      prop.gcnArchName);
   HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  int rc = kans_noalloc_setup(g_device);
+  if (rc) return rc;
   g_ready = true;
   return 0;
 }

@@ -109,6 +109,7 @@ SIGNATURES = {
     "kans_gated_create": (c_int, [P, P, P, P]),
     "kans_gated_destroy": (c_int, [P]),
     "kans_gated_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, c_int, P]),
+    "kans_gated_forward_noalloc": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, c_int, P]),
     "kans_gated_forward_host": (c_int, [P, P, c_int, P, c_int, c_int, c_int]),
     "kans_gated_time": (c_int, [P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, P]),
     "kans_gated_stream_bytes": (c_longlong, [P, c_int]),
