@@ -224,6 +224,22 @@ int kans_chain_forward(kans_chain* chain, const void* X, long ldx, void* Y, long
 /* mean ms per graph replay (include_copies: also the pinned H2D/D2H copies) */
 int kans_chain_time(kans_chain* chain, int B, int warmup, int iters, int include_copies, float* ms);
 
+/* Dense GatedKAN block out = down(SiLU(gate(x)) * up(x)) (gated_kan.py:86-138) on device activations, for
+ * layers of one dtype with gate/up d -> h and down h -> d (replaces the reference's four blocking submissions
+ * with host round trips between them).  Activations are kept in the block dtype; SwiGLU uses the +-20 clip
+ * and the arithmetic of metal_kan_swiglu_forward.  The host path replays one HIP graph per batch size (one
+ * H2D and one D2H copy) and honours metal_kan_set_async.  Layers must outlive the block. */
+typedef struct kans_gated_dense kans_gated_dense;
+int kans_gated_dense_create(kans_layer* gate, kans_layer* up, kans_layer* down, kans_gated_dense** out);
+int kans_gated_dense_destroy(kans_gated_dense* block);
+/* device X [B][ldx] (x_dtype: block dtype, or fp32 for a 16-bit block), Y [B][ldy] block dtype */
+int kans_gated_dense_forward(kans_gated_dense* block, const void* X, int x_dtype, long ldx, void* Y, long ldy, int B,
+                             void* stream);
+/* host X [B][d] -> Y [B][d] */
+int kans_gated_dense_forward_host(kans_gated_dense* block, const void* X, int x_dtype, void* Y, int B);
+/* mean ms per graph replay (include_copies: also the pinned H2D / D2H copies) */
+int kans_gated_dense_time(kans_gated_dense* block, int B, int warmup, int iters, int include_copies, float* ms);
+
 /* Chebyshev layer backward on device fp32 arrays (no reference counterpart for device pointers; the
  * host form is metal_kan_cheby_backward_fused), enqueued on `stream` (NULL = kans_stream()). */
 int kans_cheby_backward(const float* dY, const float* X, const float* W, const float* W_base, float* dW,

@@ -1186,3 +1186,263 @@ int metal_kan_chain_pipeline_cheby(const float* X, float* Y, int B, int num_laye
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Dense GatedKAN block (gated_kan.py:86-138): gate(x), up(x), SiLU(gate)*up
+// with the +-20 clip, down(hidden), all on device activations in the layers'
+// dtype (a 16-bit block stores its gate / up / hidden activations in 16 bits,
+// as its layers' outputs are).  The host path is one captured HIP graph per
+// batch size: the pinned H2D copy of x, four kernels (the layers' fused
+// forwards and the SwiGLU pass) and the D2H copy of y; async mode replays the
+// kernels only and defers the copy into the caller's array to
+// metal_kan_sync(), as the chain does.  Replaces the reference's four blocking
+// submissions with host round trips between them.
+// ---------------------------------------------------------------------------
+namespace {
+
+// hidden = (g * sigmoid(clamp(g, -20, 20))) * u in fp32 (fused_kan.metal:2284-2296,
+// the arithmetic of metal_kan_swiglu_forward), stored in T.
+template <typename T>
+__global__ void k_gated_swiglu(const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ out, long ld,
+                               int rows, int cols) {
+  const long n = (long)rows * cols;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / cols, c = i - r * cols;
+    const long k = r * ld + c;
+    const float gv = to_f32(g[k]);
+    const float cl = fminf(fmaxf(gv, -20.0f), 20.0f);
+    const float sig = 1.0f / (1.0f + expf(-cl));
+    out[k] = from_f32<T>((gv * sig) * to_f32(u[k]));
+  }
+}
+
+hipError_t launch_gated_swiglu(int dtype, const void* g, const void* u, void* out, long ld, int rows, int cols,
+                               hipStream_t st) {
+  const long n = (long)rows * cols;
+  const int blocks = (int)std::min<long>((n + 255) / 256, 8192);
+  if (dtype == DT_F16)
+    hipLaunchKernelGGL(k_gated_swiglu<_Float16>, dim3(blocks), dim3(256), 0, st, (const _Float16*)g,
+                       (const _Float16*)u, (_Float16*)out, ld, rows, cols);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL(k_gated_swiglu<__bf16>, dim3(blocks), dim3(256), 0, st, (const __bf16*)g, (const __bf16*)u,
+                       (__bf16*)out, ld, rows, cols);
+  else
+    hipLaunchKernelGGL(k_gated_swiglu<float>, dim3(blocks), dim3(256), 0, st, (const float*)g, (const float*)u,
+                       (float*)out, ld, rows, cols);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+struct kans_gated_dense {
+  kans_layer *gate, *up, *down;
+  int dtype, d, h;
+  long ld_in, ld_h, ld_out;
+  int cap_B = 0;
+  DevBuf x_d, g_d, u_d, h_d, y_d;
+  Pinned pin_in, pin_out;
+  int in_dtype = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int graph_B = -1, graph_in = -1;
+  unsigned graph_gen = 0;
+  bool graph_copies = false;
+  ~kans_gated_dense() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (pin_in.p) (void)hipHostFree(pin_in.p);
+    if (pin_out.p) (void)hipHostFree(pin_out.p);
+  }
+};
+
+static unsigned dgated_gen(const kans_gated_dense* D) {
+  return (D->gate->gen * 31u + D->up->gen) * 31u + D->down->gen;
+}
+
+static int dgated_reserve(kans_gated_dense* D, int B) {
+  int rc;
+  if (B > D->cap_B) {
+    const size_t es = dtype_size(D->dtype);
+    void* olds[5] = {D->x_d.p, D->g_d.p, D->u_d.p, D->h_d.p, D->y_d.p};
+    if ((rc = D->x_d.reserve((size_t)B * D->ld_in * 4))) return rc;  // room for an fp32 input
+    if ((rc = D->g_d.reserve((size_t)B * D->ld_h * es))) return rc;
+    if ((rc = D->u_d.reserve((size_t)B * D->ld_h * es))) return rc;
+    if ((rc = D->h_d.reserve((size_t)B * D->ld_h * es))) return rc;
+    if ((rc = D->y_d.reserve((size_t)B * D->ld_out * es))) return rc;
+    // padding columns read as inputs: zero them once, outside any graph
+    HIP_TRY(hipMemsetAsync(D->x_d.p, 0, D->x_d.cap, g_stream));
+    HIP_TRY(hipMemsetAsync(D->h_d.p, 0, D->h_d.cap, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    if ((rc = pinned_reserve(D->pin_in, (size_t)B * D->ld_in * 4))) return rc;
+    if ((rc = pinned_reserve(D->pin_out, (size_t)B * D->ld_out * es))) return rc;
+    D->cap_B = B;
+    void* news[5] = {D->x_d.p, D->g_d.p, D->u_d.p, D->h_d.p, D->y_d.p};
+    for (int i = 0; i < 5; ++i)
+      if (olds[i] != news[i]) D->graph_B = -1;
+  }
+  for (kans_layer* L : {D->gate, D->up, D->down})
+    if ((rc = layer_reserve_locked(L, B))) return rc;
+  return 0;
+}
+
+// Enqueue gate, up, SwiGLU and down: X (x_dtype, ldx) -> Y (block dtype, ldy).
+static int dgated_launch(kans_gated_dense* D, const void* X, int x_dtype, long ldx, void* Y, long ldy, int B,
+                         hipStream_t st) {
+  int rc;
+  if ((rc = layer_launch_locked(D->gate, X, ldx, D->g_d.p, D->ld_h, B, st, x_dtype, D->dtype))) return rc;
+  if ((rc = layer_launch_locked(D->up, X, ldx, D->u_d.p, D->ld_h, B, st, x_dtype, D->dtype))) return rc;
+  HIP_TRY(launch_gated_swiglu(D->dtype, D->g_d.p, D->u_d.p, D->h_d.p, D->ld_h, B, D->h, st));
+  return layer_launch_locked(D->down, D->h_d.p, D->ld_h, Y, ldy, B, st, D->dtype, D->dtype);
+}
+
+static int dgated_capture(kans_gated_dense* D, int B, bool copies) {
+  if (D->exec) { (void)hipGraphExecDestroy(D->exec); D->exec = nullptr; }
+  if (D->graph) { (void)hipGraphDestroy(D->graph); D->graph = nullptr; }
+  const size_t es = dtype_size(D->dtype), ies = dtype_size(D->in_dtype);
+  HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+  int rc = 0;
+  if (copies) {
+    hipError_t e = hipMemcpyAsync(D->x_d.p, D->pin_in.p, (size_t)B * D->ld_in * ies, hipMemcpyHostToDevice, g_stream);
+    if (e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "capture H2D: %s", hipGetErrorString(e));
+  }
+  if (!rc) rc = dgated_launch(D, D->x_d.p, D->in_dtype, D->ld_in, D->y_d.p, D->ld_out, B, g_stream);
+  if (!rc && copies) {
+    hipError_t e = hipMemcpyAsync(D->pin_out.p, D->y_d.p, (size_t)B * D->ld_out * es, hipMemcpyDeviceToHost,
+                                  g_stream);
+    if (e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "capture D2H: %s", hipGetErrorString(e));
+  }
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+  if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  D->graph = g;
+  HIP_TRY(hipGraphInstantiate(&D->exec, D->graph, nullptr, nullptr, 0));
+  D->graph_B = B;
+  D->graph_in = D->in_dtype;
+  D->graph_gen = dgated_gen(D);
+  D->graph_copies = copies;
+  return 0;
+}
+
+static int dgated_graph_ready(kans_gated_dense* D, int B, bool copies) {
+  int rc = dgated_reserve(D, B);
+  if (rc) return rc;
+  if (D->exec && D->graph_B == B && D->graph_in == D->in_dtype && D->graph_gen == dgated_gen(D) &&
+      D->graph_copies == copies)
+    return 0;
+  return dgated_capture(D, B, copies);
+}
+
+extern "C" {
+
+int kans_gated_dense_create(kans_layer* gate, kans_layer* up, kans_layer* down, kans_gated_dense** out) {
+  if (!gate || !up || !down || !out) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (gate->dtype != up->dtype || gate->dtype != down->dtype)
+    return kans_fail(KANS_ERR_ARG, "gate, up and down must share one dtype");
+  if (gate->D_in != up->D_in || gate->D_out != up->D_out || down->D_in != gate->D_out || down->D_out != gate->D_in)
+    return kans_fail(KANS_ERR_ARG, "shape mismatch: gate %dx%d, up %dx%d, down %dx%d", gate->D_in, gate->D_out,
+                     up->D_in, up->D_out, down->D_in, down->D_out);
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = ensure_init();
+  if (rc) return rc;
+  auto* D = new kans_gated_dense();
+  D->gate = gate;
+  D->up = up;
+  D->down = down;
+  D->dtype = gate->dtype;
+  D->in_dtype = D->dtype;
+  D->d = gate->D_in;
+  D->h = gate->D_out;
+  D->ld_in = gate->D_in8;
+  D->ld_h = round_up(D->h, 8);
+  D->ld_out = D->d;
+  *out = D;
+  return 0;
+}
+
+int kans_gated_dense_destroy(kans_gated_dense* D) {
+  if (!D) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ready) (void)hipStreamSynchronize(g_stream);
+  delete D;
+  return 0;
+}
+
+// Device arrays: X [B][ldx] (x_dtype: the block dtype, or fp32 for a 16-bit block; ldx >= round_up(d, 8),
+// a multiple of 8), Y [B][ldy] in the block dtype; eager launches on `stream`.
+int kans_gated_dense_forward(kans_gated_dense* D, const void* X, int x_dtype, long ldx, void* Y, long ldy, int B,
+                             void* stream) {
+  if (!D || !X || !Y || B < 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  if (x_dtype != D->dtype && x_dtype != DT_F32) return kans_fail(KANS_ERR_ARG, "x_dtype must be the block dtype or fp32");
+  if (B == 0) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = dgated_reserve(D, B);
+  if (rc) return rc;
+  return dgated_launch(D, X, x_dtype, ldx, Y, ldy, B, stream ? (hipStream_t)stream : g_stream);
+}
+
+// Host arrays [B][d] (x_dtype: the block dtype, or fp32 for a 16-bit block) -> [B][d] (block dtype):
+// one graph replay (one H2D and one D2H copy).
+int kans_gated_dense_forward_host(kans_gated_dense* D, const void* X, int x_dtype, void* Y, int B) {
+  if (!D || (B > 0 && (!X || !Y)) || B < 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  if (x_dtype != D->dtype && x_dtype != DT_F32) return kans_fail(KANS_ERR_ARG, "x_dtype must be the block dtype or fp32");
+  if (B == 0) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  D->in_dtype = x_dtype;
+  const bool async = g_async != 0;
+  int rc = dgated_graph_ready(D, B, !async);
+  if (rc) return rc;
+  const size_t es = dtype_size(D->dtype), xes = dtype_size(x_dtype);
+  const size_t in_bytes = (size_t)B * D->ld_in * xes, out_bytes = (size_t)B * D->ld_out * es;
+  void* pin_in = D->pin_in.p;
+  void* pin_out = D->pin_out.p;
+  if (async) {
+    HIP_TRY(hipHostMalloc(&pin_in, in_bytes, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault));
+  }
+  if (D->ld_in == D->d) {
+    memcpy(pin_in, X, (size_t)B * D->d * xes);
+  } else {
+    for (int r = 0; r < B; ++r) {
+      memcpy((char*)pin_in + (size_t)r * D->ld_in * xes, (const char*)X + (size_t)r * D->d * xes, (size_t)D->d * xes);
+      memset((char*)pin_in + ((size_t)r * D->ld_in + D->d) * xes, 0, (size_t)(D->ld_in - D->d) * xes);
+    }
+  }
+  if (async) {
+    HIP_TRY(hipMemcpyAsync(D->x_d.p, pin_in, in_bytes, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipGraphLaunch(D->exec, g_stream));
+    HIP_TRY(hipMemcpyAsync(pin_out, D->y_d.p, out_bytes, hipMemcpyDeviceToHost, g_stream));
+    g_pending.push_back({pin_out, Y, out_bytes});
+    g_pending.push_back({pin_in, nullptr, 0});
+    return 0;
+  }
+  HIP_TRY(hipGraphLaunch(D->exec, g_stream));
+  HIP_TRY(hipStreamSynchronize(g_stream));
+  memcpy(Y, pin_out, out_bytes);
+  return 0;
+}
+
+// Mean ms per graph replay on the block's device buffers (include_copies: with the pinned H2D / D2H copies;
+// the input dtype of the last host call).
+int kans_gated_dense_time(kans_gated_dense* D, int B, int warmup, int iters, int include_copies, float* ms) {
+  if (!D || B <= 0 || iters <= 0 || !ms) return kans_fail(KANS_ERR_ARG, "bad argument");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = dgated_graph_ready(D, B, include_copies != 0);
+  if (rc) return rc;
+  for (int i = 0; i < warmup; ++i) HIP_TRY(hipGraphLaunch(D->exec, g_stream));
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipEventRecord(e0, g_stream));
+  for (int i = 0; i < iters; ++i) HIP_TRY(hipGraphLaunch(D->exec, g_stream));
+  HIP_TRY(hipEventRecord(e1, g_stream));
+  HIP_TRY(hipEventSynchronize(e1));
+  float t = 0;
+  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms = t / iters;
+  return 0;
+}
+
+}  // extern "C"

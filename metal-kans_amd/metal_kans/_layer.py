@@ -183,3 +183,22 @@ class KANLayerBase:
 
     def backward(self, *args, **kwargs):
         raise NotImplementedError("training (backward) is outside this build's forward-only scope")
+
+
+def device_layer_handle(layer: KANLayerBase, compute: str) -> int:
+    """Make the layer's device weights current for compute dtype ``compute`` and return its ``kans_layer``
+    handle (used by the multi-layer chain and the GatedKAN block, which launch the layers themselves)."""
+    dt = {"float32": DT_F32, "float16": DT_F16, "bfloat16": DT_BF16}[compute]
+    eng = layer._engine()
+    W = getattr(layer, layer._weight_attr)
+    Wb = layer.w_base if layer.has_base else None
+    bias = layer.bias if layer.has_bias else None
+    if compute == "bfloat16":
+        f32 = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+        eng.prepare_f32(dt, f32(W), f32(Wb), f32(bias), layer._basis_params(), verify=not layer._frozen)
+    else:
+        io = np.float16 if compute == "float16" else np.float32
+        conv = lambda a: None if a is None else (  # noqa: E731
+            a if (a.dtype == io and a.flags["C_CONTIGUOUS"]) else layer._converted(a, io))
+        eng.prepare(dt, conv(W), conv(Wb), conv(bias), layer._basis_params(), verify=not layer._frozen)
+    return eng.handle.value

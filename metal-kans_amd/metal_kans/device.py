@@ -110,6 +110,11 @@ SIGNATURES = {
     "kans_gated_destroy": (c_int, [P]),
     "kans_gated_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, c_int, P]),
     "kans_gated_forward_noalloc": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, c_int, P]),
+    "kans_gated_dense_create": (c_int, [P, P, P, P]),
+    "kans_gated_dense_destroy": (c_int, [P]),
+    "kans_gated_dense_forward": (c_int, [P, P, c_int, c_long, P, c_long, c_int, P]),
+    "kans_gated_dense_forward_host": (c_int, [P, P, c_int, P, c_int]),
+    "kans_gated_dense_time": (c_int, [P, c_int, c_int, c_int, c_int, ctypes.POINTER(c_float)]),
     "kans_gated_forward_host": (c_int, [P, P, c_int, P, c_int, c_int, c_int]),
     "kans_gated_time": (c_int, [P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, P]),
     "kans_gated_stream_bytes": (c_longlong, [P, c_int]),

@@ -7,6 +7,11 @@ up = Up(x), hidden = SiLU(gate) * up with the +-20 clip, out = Down(hidden),
 (B, S, d) inputs flattened), ``to_int8`` / ``to_int4`` / ``to_ternary``
 (:239-258), ``parameter_count``.  SwiGLU runs on the GPU for every dtype.
 
+Unquantized blocks (and fp32 quantized ones, which run on their dequantized
+weights as in the reference) keep gate, up, SwiGLU and down on the device: one
+HIP graph per batch size with one host-to-device and one device-to-host copy
+(``kans_gated_dense_*``).
+
 Quantized path: a float16 block quantized with ``to_int8()`` / ``to_int4()``
 (group 64) or ``to_ternary()`` (group 32) runs through the fused quantized block
 (``_qengine.GatedEngine``): the packed weights are read from HBM once per
@@ -17,11 +22,14 @@ INT8).  Other cases use the three layers.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import numpy as np
 
 from . import device
+from ._engine import DT_F16, DT_F32, from_bf16_bits
+from ._layer import device_layer_handle
 from .cheby_kan import ChebyKAN
 from .quantization import to_int4, to_int8, to_ternary
 from ._qengine import PREFILL_K, GatedEngine, fused_batch_ok, packed_format
@@ -53,15 +61,6 @@ class GatedKAN:
         self._saved_up = None
         self._saved_hidden = None
 
-    def _swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
-        g = np.ascontiguousarray(gate, dtype=np.float32)
-        u = np.ascontiguousarray(up, dtype=np.float32)
-        out = np.empty_like(g)
-        device.check(device.get_metal_bridge().metal_kan_swiglu_forward(g.ctypes.data, u.ctypes.data,
-                                                                       out.ctypes.data, g.size),
-                     "metal_kan_swiglu_forward")
-        return out.astype(gate.dtype, copy=False)
-
     def _decode_engine(self) -> Optional[GatedEngine]:
         """The fused quantized block, when this block's weights allow it (see module docstring)."""
         if self.dtype != np.float16:
@@ -77,6 +76,52 @@ class GatedKAN:
             self._qblock = eng
         return eng
 
+    def _block_compute(self) -> str:
+        kinds = {k._resolve_compute() for k in (self.gate_kan, self.up_kan, self.down_kan)}
+        if len(kinds) != 1:
+            raise ValueError(f"gate, up and down disagree on compute dtype: {sorted(kinds)}")
+        return kinds.pop()
+
+    def _dense_forward(self, x_2d: np.ndarray) -> np.ndarray:
+        """gate, up, SwiGLU and down on device activations: one HIP graph per batch size with one H2D and
+        one D2H copy (kans_gated_dense_*), in the layers' compute dtype."""
+        compute = self._block_compute()
+        x_in = np.float16 if (compute == "float16" and x_2d.dtype == np.float16) else np.float32
+        x2 = np.ascontiguousarray(x_2d, dtype=x_in)
+        if x2.shape[1] != self.d_model:
+            raise ValueError(f"Expected d_model={self.d_model}, got {x2.shape[1]}")
+        handles = tuple(device_layer_handle(k, compute) for k in (self.gate_kan, self.up_kan, self.down_kan))
+        lib = device.get_metal_bridge()
+        if self.__dict__.get("_dense_key") != handles:
+            self._drop_dense()
+            h = ctypes.c_void_p()
+            device.check(lib.kans_gated_dense_create(*handles, ctypes.byref(h)), "kans_gated_dense_create")
+            self._dense_block = h
+            self._dense_key = handles
+        B = x2.shape[0]
+        x_dt = DT_F16 if x2.dtype == np.float16 else DT_F32
+        if compute == "bfloat16":
+            yb = np.empty((B, self.d_model), dtype=np.uint16)
+            device.check(lib.kans_gated_dense_forward_host(self._dense_block, x2.ctypes.data, x_dt, yb.ctypes.data, B),
+                         "kans_gated_dense_forward_host")
+            return from_bf16_bits(yb).reshape(B, self.d_model)
+        y = np.empty((B, self.d_model), dtype=np.float16 if compute == "float16" else np.float32)
+        device.check(lib.kans_gated_dense_forward_host(self._dense_block, x2.ctypes.data, x_dt, y.ctypes.data, B),
+                     "kans_gated_dense_forward_host")
+        return y
+
+    def _drop_dense(self) -> None:
+        h = self.__dict__.pop("_dense_block", None)
+        self.__dict__.pop("_dense_key", None)
+        if h:
+            try:
+                device.load_library().kans_gated_dense_destroy(h)
+            except Exception:
+                pass
+
+    def __del__(self):
+        self._drop_dense()
+
     def forward(self, x: np.ndarray) -> np.ndarray:
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
@@ -89,13 +134,11 @@ class GatedKAN:
                 if len(orig_shape) > 2:
                     return out.reshape(*orig_shape[:-1], self.d_model)
                 return out
-        gate = self.gate_kan(x_2d)
-        up = self.up_kan(x_2d)
-        self._saved_gate = gate
-        self._saved_up = up
-        hidden = self._swiglu(gate, up)
-        self._saved_hidden = hidden
-        out = self.down_kan(hidden)
+        if x_2d.shape[0] == 0:
+            out = self.down_kan(np.zeros((0, self.d_ffn), dtype=x_2d.dtype))
+        else:
+            out = self._dense_forward(x_2d)
+        self._saved_gate = self._saved_up = self._saved_hidden = None
         if len(orig_shape) > 2:
             return out.reshape(*orig_shape[:-1], self.d_model)
         return out

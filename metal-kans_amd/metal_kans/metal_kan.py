@@ -24,6 +24,7 @@ import numpy as np
 
 from . import device
 from ._engine import DT_BF16, DT_F16, DT_F32, from_bf16_bits
+from ._layer import device_layer_handle
 from .bspline_kan import BSplineKAN
 from .cheby_kan import ChebyKAN
 from .fast_kan import FastKAN
@@ -139,21 +140,7 @@ class MetalKAN:
         orig_shape = x.shape
         x2 = np.ascontiguousarray(x.reshape(-1, self.layers_hidden[0]))
         B = x2.shape[0]
-        dt = {"float32": DT_F32, "float16": DT_F16, "bfloat16": DT_BF16}[compute]
-        handles = []
-        for layer in self.layers:
-            eng = layer._engine()
-            W = getattr(layer, layer._weight_attr)
-            Wb = layer.w_base if layer.has_base else None
-            bias = layer.bias if layer.has_bias else None
-            if compute == "bfloat16":
-                f32 = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
-                eng.prepare_f32(dt, f32(W), f32(Wb), f32(bias), layer._basis_params(), verify=not layer._frozen)
-            else:
-                conv = lambda a: None if a is None else (  # noqa: E731
-                    a if (a.dtype == io and a.flags["C_CONTIGUOUS"]) else layer._converted(a, io))
-                eng.prepare(dt, conv(W), conv(Wb), conv(bias), layer._basis_params(), verify=not layer._frozen)
-            handles.append(eng.handle.value)
+        handles = [device_layer_handle(layer, compute) for layer in self.layers]
         lib = device.get_metal_bridge()
         key = tuple(handles)
         if self._chain_key != key:

@@ -627,3 +627,59 @@ def test_full_size_sampled_rows(gpu, kind, K):
     y2 = L(x)
     np.testing.assert_array_equal(y.view(np.uint16), y2.view(np.uint16))
     assert O.rel_err(y[rows], y_ref) <= 2e-2
+
+
+# ---------------------------------------------------------------- GatedKAN on device activations
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("B", [1, 40, 300])
+def test_gated_kan_dense_block(gpu, dtype, B):
+    """Unquantized GatedKAN: gate, up, SwiGLU and down on device activations in one graph
+    (kans_gated_dense_forward_host), against the float64 oracle block on the same weights; the 16-bit
+    blocks store gate / up / hidden in their dtype, as the reference's layers output them."""
+    import metal_kans as mk
+    np.random.seed(B)
+    blk = mk.GatedKAN(d_model=72, d_ffn=130, degree=4, has_bias=True, dtype=np.float32)
+    for k in (blk.gate_kan, blk.up_kan, blk.down_kan):
+        k.bias = np.random.normal(0, 0.1, k.out_features).astype(np.float32)
+    specs = [{"W": k.w_cheby, "W_base": k.w_base, "bias": k.bias, "K": 4}
+             for k in (blk.gate_kan, blk.up_kan, blk.down_kan)]
+    if dtype == "float16":
+        for k in (blk.gate_kan, blk.up_kan, blk.down_kan):
+            k.half()
+        blk.dtype = np.dtype(np.float16)
+    elif dtype == "bfloat16":
+        for k in (blk.gate_kan, blk.up_kan, blk.down_kan):
+            k.bfloat16()
+    x = np.random.default_rng(B).uniform(-1.5, 1.5, (B, 72)).astype(np.float32)
+    ref = O.gated_forward(x, *specs)
+    out = blk(x)
+    assert out.shape == (B, 72)
+    assert blk.__dict__.get("_dense_block") is not None
+    e = O.rel_err(np.asarray(out, np.float32), ref)
+    print(f"gated dense {dtype} B={B}: rel err {e:.2e}")
+    assert e <= TOL[dtype]
+    out2 = blk(x)   # graph replay
+    np.testing.assert_array_equal(np.asarray(out), np.asarray(out2))
+    if dtype == "float32":
+        # the same as the per-layer composition with the reference-named SwiGLU entry point
+        g, u = blk.gate_kan(x), blk.up_kan(x)
+        hid = np.empty_like(g)
+        assert gpu.metal_kan_swiglu_forward(g.ctypes.data, u.ctypes.data, hid.ctypes.data, g.size) == 0
+        np.testing.assert_array_equal(out, blk.down_kan(hid))
+
+
+def test_gated_kan_dense_block_async(gpu):
+    """Async mode (metal_kan_set_async): results land at metal_kan_sync(), equal to the synchronous ones."""
+    import metal_kans as mk
+    np.random.seed(3)
+    blk = mk.GatedKAN(d_model=40, d_ffn=64, degree=4)
+    xs = [np.random.uniform(-1, 1, (50, 40)).astype(np.float32) for _ in range(4)]
+    sync = [blk(x) for x in xs]
+    mk.set_async(True)
+    try:
+        outs = [blk(x) for x in xs]
+        mk.sync()
+    finally:
+        mk.set_async(False)
+    for a, b in zip(outs, sync):
+        np.testing.assert_array_equal(a, b)
