@@ -312,12 +312,10 @@ def run_chain_cfg2(lib, mk, warmup, iters):
     return out
 
 
-def _quantized_layer(lib, fmt, W, Wb, K):
-    """kans_qlayer from a float32 (W, W_base) pair packed in the reference format (native quantizers)."""
-    d_out, d_in = Wb.shape
-    h = ctypes.c_void_p()
+def _pack(lib, fmt, W, Wb):
+    """A float32 (W, W_base) pair packed in the reference format by the native quantizers."""
+    arrs = []
     if fmt in ("int4", "int8"):
-        arrs = []
         for A in (W, Wb):
             ng = A.size // 64
             q = np.empty((ng, 32 if fmt == "int4" else 64), np.uint8)
@@ -326,16 +324,28 @@ def _quantized_layer(lib, fmt, W, Wb, K):
             qfn = lib.metal_kan_quantize_int4 if fmt == "int4" else lib.metal_kan_quantize_int8
             assert qfn(A.ctypes.data, q.ctypes.data, s_.ctypes.data, b_.ctypes.data, ng, 64) == 0
             arrs += [q, s_, b_]
-        cfn = lib.kans_qlayer_create_int4 if fmt == "int4" else lib.kans_qlayer_create_int8
-        rc = cfn(d_in, d_out, K, 1, 0, 64, *[a.ctypes.data for a in arrs], None, 0, ctypes.byref(h))
     else:
-        arrs = []
         for A in (W, Wb):
             kd = A.shape[1]
             p_ = np.zeros((A.shape[0], (kd + 15) // 16), np.uint32)
             s_ = np.zeros((A.shape[0], (kd + 31) // 32), np.float32)
             assert lib.metal_kan_quantize_ternary(A.ctypes.data, p_.ctypes.data, s_.ctypes.data, A.shape[0], kd, 32) == 0
             arrs += [p_, s_]
+    return arrs
+
+
+def _quantized_layer(lib, fmt, W, Wb, K):
+    """kans_qlayer from a float32 (W, W_base) pair packed in the reference format (native quantizers)."""
+    return _create_qlayer(lib, fmt, Wb.shape, K, _pack(lib, fmt, W, Wb))
+
+
+def _create_qlayer(lib, fmt, shape, K, arrs):
+    d_out, d_in = shape
+    h = ctypes.c_void_p()
+    if fmt in ("int4", "int8"):
+        cfn = lib.kans_qlayer_create_int4 if fmt == "int4" else lib.kans_qlayer_create_int8
+        rc = cfn(d_in, d_out, K, 1, 0, 64, *[a.ctypes.data for a in arrs], None, 0, ctypes.byref(h))
+    else:
         rc = lib.kans_qlayer_create_ternary(d_in, d_out, K, 1, 0, 32, *[a.ctypes.data for a in arrs], None, 0,
                                             ctypes.byref(h))
     if rc:
@@ -343,14 +353,22 @@ def _quantized_layer(lib, fmt, W, Wb, K):
     return h
 
 
+# Weight copies the decode lines rotate over: each call's weights were last read COPIES - 1 calls earlier,
+# so even the ternary block (254 MB, within the 256 MB MALL) streams from HBM, as in a model whose layers
+# together exceed the MALL.
+COPIES = 3
+
+
 def run_cfg5(lib, warmup, iters):
     """GatedKAN d=4096, h=11008, K=4 (base on, no bias), all six weight matrices
     ~N(0, 0.02) then INT4 (group 64) or ternary (group 32), plus the north star's INT8 (group 64); x ~ N(0,1)
     fp16.  Every line is one whole block forward (gate, up, SwiGLU, down) replayed as one HIP graph on
     device-resident x / y, timed with HIP events.  Decode B in {1, 32} (INT4 / ternary GEMVs over the packed
-    weights): GB/s = algorithmic bytes (packed codes + group parameters + x + y) / time.  Prefill B = 8192
-    (fused kernels decoding the packed weights into fp16 MFMA tiles, gate|up in one launch with the SwiGLU
-    epilogue): TFLOP/s of 2*B*(2*h*d + d*h)*(K + 1), and the packed bytes per forward."""
+    weights): COPIES blocks with separate device weights, calls cycling through them (weights from HBM, not
+    the MALL); GB/s = algorithmic bytes (packed codes + group parameters + x + y) / time; the same block
+    replayed alone is reported beside it as the MALL-warm rate.  Prefill B = 8192 (fused kernels decoding
+    the packed weights into fp16 MFMA tiles, gate|up in one launch with the SwiGLU epilogue): TFLOP/s of
+    2*B*(2*h*d + d*h)*(K + 1), and the packed bytes per forward."""
     d, hdim, K = 4096, 11008, 4
     rng = np.random.default_rng(1005)
     t0 = time.perf_counter()
@@ -364,12 +382,17 @@ def run_cfg5(lib, warmup, iters):
     stream_ceiling = {}
     prefill_flops = 2.0 * 8192 * (2 * hdim * d + d * hdim) * (K + 1)
     for fmt in ("int4", "ternary", "int8"):
-        layers = [_quantized_layer(lib, fmt, W, Wb, K) for (W, Wb) in mats]
-        blk = ctypes.c_void_p()
-        assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0
+        packed = [_pack(lib, fmt, W, Wb) for (W, Wb) in mats]
+        ncopy = COPIES
+        layers, blocks = [], []
+        for _ in range(ncopy):
+            ls = [_create_qlayer(lib, fmt, Wb.shape, K, arrs) for (W, Wb), arrs in zip(mats, packed)]
+            blk = ctypes.c_void_p()
+            assert lib.kans_gated_create(*ls, ctypes.byref(blk)) == 0
+            layers += ls
+            blocks.append(blk)
+        blk = blocks[0]
         for B, x in xs.items():
-            if fmt == "int8" and B != 8192:
-                continue  # INT8 has no decode GEMV: its small batches run the prefill kernel
             xd, yd = DevBuf(lib, x.nbytes), DevBuf(lib, x.nbytes)
             xd.upload(x)
             ms = ctypes.c_float()
@@ -378,7 +401,6 @@ def run_cfg5(lib, warmup, iters):
             if rc:
                 raise RuntimeError(lib.kans_last_error().decode())
             nbytes = lib.kans_gated_stream_bytes(blk, B)
-            gbs = nbytes / ms.value / 1e6
             if B == 8192:
                 out[f"cfg5_{fmt}_prefill_b8192"] = {
                     "ms": round(ms.value, 4), "tflops": round(prefill_flops / ms.value / 1e9, 2),
@@ -387,22 +409,34 @@ def run_cfg5(lib, warmup, iters):
                     "path": "fused prefill: packed weights decoded into fp16 MFMA tiles; gate|up one launch "
                             "with the SwiGLU epilogue, then down"}
             else:
+                warm = ms.value
+                arr = (ctypes.c_void_p * ncopy)(*[b.value for b in blocks])
+                rc = lib.kans_gated_time_rotate(arr, ncopy, xd.p, 1, yd.p, 1, B, max(ncopy, min(warmup, it)), it,
+                                                ctypes.byref(ms))
+                if rc:
+                    raise RuntimeError(lib.kans_last_error().decode())
+                gbs = nbytes / ms.value / 1e6
                 if fmt not in stream_ceiling:
-                    # one read-only streaming kernel over the same number of bytes (kans_stream_ceiling)
-                    sb = DevBuf(lib, (nbytes + 15) // 16 * 16)
+                    # one read-only streaming kernel (kans_stream_ceiling) over ncopy times the block's bytes, so
+                    # that its repeated launches, like the rotating calls, read from HBM and not the MALL
+                    cb = ncopy * ((nbytes + 15) // 16 * 16)
+                    sb = DevBuf(lib, cb)
                     g = ctypes.c_double()
-                    assert lib.kans_stream_ceiling(sb.p, (nbytes + 15) // 16 * 16, ctypes.byref(g)) == 0, \
-                        lib.kans_last_error()
+                    assert lib.kans_stream_ceiling(sb.p, cb, ctypes.byref(g)) == 0, lib.kans_last_error()
                     sb.free()
                     stream_ceiling[fmt] = round(g.value, 1)
                 out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
                                                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                                                   "stream_ceiling_GB_per_s": stream_ceiling[fmt],
                                                   "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
-                                                  "bytes": int(nbytes), "batch": B}
+                                                  "bytes": int(nbytes), "batch": B,
+                                                  "timing": f"{ncopy} weight copies, calls rotating (from HBM)",
+                                                  "ms_mall_warm": round(warm, 5),
+                                                  "GB_per_s_mall_warm": round(nbytes / warm / 1e6, 1)}
             xd.free()
             yd.free()
-        lib.kans_gated_destroy(blk)
+        for b in blocks:
+            lib.kans_gated_destroy(b)
         for hnd in layers:
             lib.kans_qlayer_destroy(hnd)
     log(f"[bench] cfg5 ({time.perf_counter() - t0:.1f} s): {out}")

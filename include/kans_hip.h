@@ -313,6 +313,11 @@ int kans_gated_forward_noalloc(kans_gated* block, const void* X, int x_dtype, lo
 /* mean ms per block forward on device X / Y (use_graph: replay one captured HIP graph) */
 int kans_gated_time(kans_gated* block, const void* X, int x_dtype, void* Y, int y_dtype, int B, int warmup,
                     int iters, int use_graph, float* ms);
+/* mean ms per block forward, replaying one HIP graph per block and cycling through the n blocks (same
+ * shapes): with n copies of a block whose weights together exceed the 256 MB MALL, every call streams
+ * its weights from HBM (measurement only; no reference counterpart) */
+int kans_gated_time_rotate(kans_gated* const* blocks, int n, const void* X, int x_dtype, void* Y, int y_dtype,
+                           int B, int warmup, int iters, float* ms);
 /* algorithmic bytes of one block forward: packed weights + group parameters + x and y (fp16) */
 long long kans_gated_stream_bytes(const kans_gated* block, int B);
 /* The GatedKAN block computes SwiGLU(gate, up) and the down layer's basis in one step (on = 1, the

@@ -16,19 +16,23 @@ constexpr int kQSuper = 128;
 constexpr int kSmallB = 2;
 // Work items (waves) per CU the split-K aims for (measured on the config-5
 // block): small batches INT4 8 (resident: 12), ternary 12 (resident: 12, the
-// four-deep ring's occupancy); the workgroup kernel 10.
-inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_INT4 ? 8 : 12) : 10; }
+// four-deep ring's occupancy), INT8 as INT4; the workgroup kernel 10.
+inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_TERN ? 12 : 8) : 10; }
 
 // 16-row blocks per decode wave (64 output rows: each activation fragment
 // serves 4 weight tiles, and a wave reads 4 KB of INT4 codes per superchunk).
 constexpr int kQNW = 4;
 inline int qrow_blocks(int /*D_out*/) { return kQNW; }
 
+// Formats with a group affine (scale, bias) per 64 indices: INT4 and INT8 (the
+// kernels apply it to the fp32 accumulator with the group sums S of Phi).
+__host__ __device__ constexpr bool q_affine(int quant) { return quant != Q_TERN; }
+
 // Bytes of one 16-row x 128-index code tile, and of one record: the kQNW code
 // tiles a decode wave reads for one superchunk followed by their group
 // parameters (kQNW x 16 rows x float4), so the wave's whole input is one
 // contiguous stream.
-__host__ __device__ constexpr int qtile_bytes(int quant) { return quant == Q_INT4 ? 1024 : 512; }
+__host__ __device__ constexpr int qtile_bytes(int quant) { return quant == Q_INT4 ? 1024 : quant == Q_INT8 ? 2048 : 512; }
 __host__ __device__ constexpr int qrec_bytes(int quant) { return kQNW * (qtile_bytes(quant) + 16 * 16); }
 
 // Activation basis of one layer input (see k_prep).
@@ -40,7 +44,7 @@ struct QPrep {
   int D_in, K, has_base;
   int Cb, C_tot;   // superchunks of the basis segment and of basis + base
   _Float16* Phi;   // [MP][C_tot * 128]
-  float2* S;       // [C_tot][MP] (INT4 only; may be null for ternary)
+  float2* S;       // [C_tot][MP] (INT4 / INT8; may be null for ternary)
 };
 
 // What a small-batch decode GEMV does after its split-K partial sums are
@@ -97,6 +101,8 @@ struct QGemv {
 
 // Re-tile a packed matrix (C superchunks starting at superchunk c_off) into the records R.
 hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
+                      int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st);
+hipError_t qtile_int8(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
                       int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st);
 hipError_t qtile_tern(const unsigned* wp, const float* scales, int D_out, int wpr, long K_dim, int gpr, int nrb,
                       int C, int c_off, int C_tot, void* R, hipStream_t st);

@@ -1,9 +1,9 @@
 // Fused decode (small-batch) forward of Chebyshev KAN layers whose weights are
-// kept in the reference's packed INT4 or ternary formats, and of the GatedKAN
-// block built from three such layers.
+// kept in the reference's packed INT4, INT8 or ternary formats, and of the
+// GatedKAN block built from three such layers.
 //
 //   y[b,o] = bias[o] + sum_i SiLU(v[b,i]) Wb[o,i] + sum_{i,k} T_k(clamp v[b,i]) W[o,i*K+k]
-//   W  = q*s + b per group of 64 (INT4, quantization.py:13-99), or
+//   W  = q*s + b per group of 64 (INT4 / INT8, quantization.py:13-99), or
 //        t*s, t in {-1,0,+1} per group of 32 (ternary, quantization.py:191-246)
 //
 // Replaces metal_kan_forward_ternary_cheby (metal_kan_bridge.mm:4684-4733,
@@ -14,13 +14,15 @@
 // once at full bandwidth.  Design:
 //   * the packed weights are re-tiled once on upload into MFMA B-fragment order:
 //     one "superchunk" = 16 output rows x 128 reduction indices, one 16-byte
-//     (INT4) or 8-byte (ternary) load per lane, 1 KB / 512 B per wave, fully
-//     coalesced; the per-group affine parameters are re-tiled alongside;
+//     (INT4), two 16-byte (INT8) or one 8-byte (ternary) load per lane,
+//     1 KB / 2 KB / 512 B per wave, fully coalesced; the per-group affine
+//     parameters are re-tiled alongside;
 //   * INT4 nibbles become fp16 with the 0x6400|q trick (the fp16 value 1024+q,
-//     exact), two per v_and_or_b32; ternary codes become +-1/0 fp16 through a
-//     v_perm_b32 byte table.  The group scale is applied to the fp32 MFMA
-//     accumulator once per group: y += s * sum(phi*(1024+q)) + (b - 1024 s) *
-//     sum(phi) for INT4, y += s * sum(phi*t) for ternary;
+//     exact), two per v_and_or_b32; INT8 bytes become 1024+q with one
+//     v_perm_b32 per pair (high byte 0x64); ternary codes become +-1/0 fp16
+//     through a v_perm_b32 byte table.  The group scale is applied to the fp32
+//     MFMA accumulator once per group: y += s * sum(phi*(1024+q)) + (b - 1024 s)
+//     * sum(phi) for INT4 / INT8, y += s * sum(phi*t) for ternary;
 //   * the activation basis phi (T_k and SiLU of the layer input, fp16, permuted
 //     to match the unpack order) and its per-group sums are computed once per
 //     layer into a small buffer that stays in L2; the waves read their A
@@ -38,6 +40,7 @@
 #include "kans_common.h"
 #include "kans_api_internal.h"
 #include "kans_qgemv.h"
+#include "kans_tile.h"
 #include <algorithm>
 
 namespace kans {
@@ -98,10 +101,44 @@ __global__ void k_tile_int4(const unsigned char* __restrict__ qw, long rowbytes,
   }
 }
 
-// INT4 group parameters: SB[rb][c][r] = (s0, s0', s1, s1') for the groups
-// 2c, 2c+1 of row 16*rb + r, s' = b - 1024 s (zero past the row / matrix).
-__global__ void k_tile_int4_params(const float* __restrict__ scales, const float* __restrict__ biases, int gpr,
-                                   int D_out, int nrb, int C, int c_off, int C_tot, char* __restrict__ R) {
+// INT8 qweight: row n is `rowbytes` bytes, one code per byte.  Q[rb][c][lane],
+// lane = (q = l/16, r = l%16): dwords 2t, 2t+1 hold the 8 codes of row
+// 16*rb + r at reduction indices 128c + 32t + 8q .. +7 (bytes of the row in
+// order), i.e. 32 bytes per lane.
+__global__ void k_tile_int8(const unsigned char* __restrict__ qw, long rowbytes, int D_out, int nrb, int C,
+                            int c_off, int C_tot, char* __restrict__ R) {
+  const long total = (long)nrb * C * 64;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    const long r2 = idx >> 6;
+    const int c = (int)(r2 % C);
+    const int rb = (int)(r2 / C);
+    const int q = lane >> 4, r = lane & 15;
+    const int n = rb * 16 + r;
+    unsigned w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if (n < D_out) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const long off = 128L * c + 32 * t + 8 * q + 4 * hh;
+          if (off < rowbytes) {
+            const unsigned char* p = qw + (long)n * rowbytes + off;
+            w[2 * t + hh] = (unsigned)p[0] | ((unsigned)p[1] << 8) | ((unsigned)p[2] << 16) | ((unsigned)p[3] << 24);
+          }
+        }
+    }
+    uint4* dst = reinterpret_cast<uint4*>(R + qcode_offset<Q_INT8>(rb, c_off + c, C_tot, lane));
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
+// INT4 / INT8 group parameters: SB[rb][c][r] = (s0, s0', s1, s1') for the
+// groups 2c, 2c+1 of row 16*rb + r, s' = b - 1024 s (zero past the row / matrix).
+template <int QT>
+__global__ void k_tile_affine_params(const float* __restrict__ scales, const float* __restrict__ biases, int gpr,
+                                     int D_out, int nrb, int C, int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 16;
   for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
     const int r = (int)(idx & 15);
@@ -121,7 +158,7 @@ __global__ void k_tile_int4_params(const float* __restrict__ scales, const float
         }
       }
     }
-    *reinterpret_cast<float4*>(R + qparam_offset<Q_INT4>(rb, c_off + c, C_tot, r)) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(R + qparam_offset<QT>(rb, c_off + c, C_tot, r)) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -197,9 +234,10 @@ __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, in
 // feed): the basis segment
 // (p < Cb*128) holds T_k(clamp v[m][i]) at reduction index j = i*K + k, the base
 // segment SiLU(v[m][i]) at j = i; within each 8-block the order is the unpack
-// order pi of the weight format (INT4: 0,4,1,5,2,6,3,7; ternary: identity).
-// S[c][m] = (sum over group 2c, sum over group 2c+1) of the fp16-rounded values
-// (INT4 only).  Indices past the segment's length are 0.
+// order pi of the weight format (INT4: 0,4,1,5,2,6,3,7; INT8 and ternary:
+// identity).  S[c][m] = (sum over group 2c, sum over group 2c+1) of the
+// fp16-rounded values (INT4 / INT8 only).  Indices past the segment's length
+// are 0.
 // ---------------------------------------------------------------------------
 template <int QT>
 __device__ __forceinline__ int unpack_order(int e) {
@@ -304,7 +342,7 @@ __global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in
     sum += (float)hv[e];
   }
   if (live && m < MP) *reinterpret_cast<uint4*>(Phi + (long)m * C_tot * 128 + p0) = *reinterpret_cast<uint4*>(hv);
-  if constexpr (QT == Q_INT4) {
+  if constexpr (q_affine(QT)) {
     // group of 64 = 8 consecutive 8-blocks = 8 consecutive lanes
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2);
@@ -322,13 +360,14 @@ __global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in
 // literal and reads at most one SGPR); as opaque register values it selects
 // one v_and_or_b32.  The empty asm only hides the values from constant folding.
 struct UnpackConsts {
-  unsigned nib_mask, nib_magic, tsel_mask, tsel_zero;
+  unsigned nib_mask, nib_magic, tsel_mask, tsel_zero, byte_magic;
   __device__ __forceinline__ void init() {
     nib_mask = 0x000F000Fu;
     nib_magic = 0x64006400u;
     tsel_mask = 0x03000300u;
     tsel_zero = 0x000C000Cu;
-    asm volatile("" : "+v"(nib_mask), "+v"(nib_magic), "+v"(tsel_mask), "+v"(tsel_zero));
+    byte_magic = 0x64646464u;  // high byte of fp16 1024 + q, for the INT8 v_perm_b32
+    asm volatile("" : "+v"(nib_mask), "+v"(nib_magic), "+v"(tsel_mask), "+v"(tsel_zero), "+v"(byte_magic));
   }
 };
 
@@ -339,6 +378,18 @@ __device__ __forceinline__ half8v unpack_int4(unsigned w, const UnpackConsts& k)
   o[1] = ((w >> 4) & k.nib_mask) | k.nib_magic;
   o[2] = ((w >> 8) & k.nib_mask) | k.nib_magic;
   o[3] = ((w >> 12) & k.nib_mask) | k.nib_magic;
+  return *reinterpret_cast<half8v*>(o);
+}
+
+// INT8: 8 bytes (two dwords, codes in order) -> 8 fp16 values 1024+q.
+// v_perm_b32 selector bytes 0..3 pick bytes of the second operand (the codes),
+// 4..7 bytes of the first (0x64): (q_e, 0x64, q_e+1, 0x64).
+__device__ __forceinline__ half8v unpack_int8(unsigned w0, unsigned w1, const UnpackConsts& k) {
+  unsigned o[4];
+  o[0] = __builtin_amdgcn_perm(k.byte_magic, w0, 0x04010400u);
+  o[1] = __builtin_amdgcn_perm(k.byte_magic, w0, 0x04030402u);
+  o[2] = __builtin_amdgcn_perm(k.byte_magic, w1, 0x04010400u);
+  o[3] = __builtin_amdgcn_perm(k.byte_magic, w1, 0x04030402u);
   return *reinterpret_cast<half8v*>(o);
 }
 
@@ -357,6 +408,22 @@ __device__ __forceinline__ half8v unpack_tern(unsigned w, const UnpackConsts& k)
     o[p] = __builtin_amdgcn_perm(0u, kTable, sel);
   }
   return *reinterpret_cast<half8v*>(o);
+}
+
+// One lane's code word of a tile (qtile_bytes / 64 bytes) and the B fragment
+// of MFMA step t (reduction indices 32t .. 32t + 31 of the superchunk) in it.
+struct QW8 {
+  uint4 lo, hi;
+};
+template <int QT>
+using QWordOf = typename std::conditional<QT == Q_INT4, uint4,
+                                          typename std::conditional<QT == Q_INT8, QW8, uint2>::type>::type;
+template <int QT, int T, typename QW>
+__device__ __forceinline__ half8v unpack_step(const QW& qw, const UnpackConsts& k) {
+  const unsigned* dw = reinterpret_cast<const unsigned*>(&qw);
+  if constexpr (QT == Q_INT4) return unpack_int4(dw[T], k);
+  else if constexpr (QT == Q_INT8) return unpack_int8(dw[2 * T], dw[2 * T + 1], k);
+  else return unpack_tern<T & 1>(dw[T >> 1], k);
 }
 
 struct QMatDev {
@@ -437,7 +504,7 @@ __device__ __forceinline__ void epi_write_blocks(const _Float16* st, int n_st, l
     }
     const long p0 = p_lo + 8L * b;
     if (live) *reinterpret_cast<uint4*>(phi_row + p0) = *reinterpret_cast<uint4*>(hv);
-    if constexpr (QT == Q_INT4) {
+    if constexpr (q_affine(QT)) {
       sum += __shfl_xor(sum, 1);
       sum += __shfl_xor(sum, 2);
       sum += __shfl_xor(sum, 4);
@@ -526,7 +593,12 @@ __device__ __forceinline__ void epi_swiglu(const QEpi& E, const float* part, int
 // loads let a block whose weights fit the MALL hit it on the next call.
 template <bool NT, typename Q>
 __device__ __forceinline__ Q load_rec(const char* p) {
-  if constexpr (!NT) {
+  if constexpr (sizeof(Q) == 32) {
+    Q q;
+    q.lo = load_rec<NT, uint4>(p);
+    q.hi = load_rec<NT, uint4>(p + 16);
+    return q;
+  } else if constexpr (!NT) {
     return *reinterpret_cast<const Q*>(p);
   } else {
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -589,7 +661,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   const bool alive = arow < B;
   const _Float16* arow_p = Phi + (long)arow * ldphi + 8 * q;
 
-  typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
+  typedef QWordOf<QT> QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
 
   // operands of one superchunk: weights / group parameters (HBM stream) and
@@ -598,18 +670,17 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     QWord qw[NW];
     float4 sb;        // this lane's own row (row block q, row r)
     half8v a[4];
-    float2 sg[SR];    // INT4: group sums of batch rows 0 .. SR-1 (the same in every lane)
+    float2 sg[SR];    // INT4 / INT8: group sums of batch rows 0 .. SR-1 (the same in every lane)
   };
   auto compute = [&](const Ops& o) {
-    if constexpr (QT == Q_INT4) {
-#pragma unroll
-      for (int gs = 0; gs < 2; ++gs) {
+    if constexpr (q_affine(QT)) {
+      static_for<0, 2>([&](auto GS) __attribute__((always_inline)) {
+        constexpr int gs = decltype(GS)::value;
         floatx4 g[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const unsigned* dw = reinterpret_cast<const unsigned*>(&o.qw[w]);
-          const half8v b0 = unpack_int4(dw[2 * gs], uk);
-          const half8v b1 = unpack_int4(dw[2 * gs + 1], uk);
+          const half8v b0 = unpack_step<QT, 2 * gs>(o.qw[w], uk);
+          const half8v b1 = unpack_step<QT, 2 * gs + 1>(o.qw[w], uk);
           g[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
           g[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[2 * gs + 1], b1, g[w], 0, 0, 0);
         }
@@ -622,7 +693,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
             const float S_ = gs ? o.sg[i].y : o.sg[i].x;
             acc[w][i] = __builtin_fmaf(s, g[w][i], __builtin_fmaf(s2, S_, acc[w][i]));
           }
-      }
+      });
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -663,7 +734,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         if (alive) o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
-      if constexpr (QT == Q_INT4) {
+      if constexpr (q_affine(QT)) {
 #pragma unroll
         for (int i = 0; i < SR; ++i) o.sg[i] = S[(long)cc * MP + i];
       }
@@ -749,7 +820,9 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
                                                   float* __restrict__ part, int N_total) {
   constexpr int NW = kQNW;
   constexpr int FR = MT * 4;                    // activation fragments (1 KB each) per superchunk
-  constexpr int OPS = 2 * NW + FR / 4 + (QT == Q_INT4 ? 1 : 0);  // vector-memory instructions per wave and superchunk
+  // vector-memory instructions per wave and superchunk: code words (one or two
+  // 16-byte loads), group parameters, fragment copies, group sums
+  constexpr int OPS = NW * (qtile_bytes(QT) / 64 > 16 ? 2 : 1) + NW + FR / 4 + (q_affine(QT) ? 1 : 0);
   // three separate arrays per ring (not one indexed array): the compiler then
   // sees that reads of one stage do not depend on the copies into another,
   // and waits only for this stage's copies
@@ -772,7 +845,7 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   UnpackConsts uk;
   uk.init();
 
-  typedef typename std::conditional<QT == Q_INT4, uint4, uint2>::type QWord;
+  typedef QWordOf<QT> QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
   struct Wts {
     QWord qw[NW];
@@ -798,7 +871,7 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
       const _Float16* src = Phi + (long)row * ldphi + (long)c * 128 + 32 * (j & 3) + 8 * q;
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&sa[j * 64], 16, 0, 0);
     }
-    if constexpr (QT == Q_INT4) {
+    if constexpr (q_affine(QT)) {
       const float* ssrc = reinterpret_cast<const float*>(S + (long)c * MP) + min(lane, 2 * MP - 1);
       __builtin_amdgcn_global_load_lds(ssrc, (__attribute__((address_space(3))) void*)ss, 4, 0, 0);
     }
@@ -828,7 +901,7 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   // that DMA before these reads)
   struct Frags {
     half8v a[MT][4];
-    float2 sg[MT][4];  // INT4: group sums of rows 16 mt + 4 q + i
+    float2 sg[MT][4];  // INT4 / INT8: group sums of rows 16 mt + 4 q + i
   };
   auto read_frags = [&](const uint4* sa, const float2* ss, Frags& f) {
 #pragma unroll
@@ -838,7 +911,7 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
         const uint4 u = sa[(mt * 4 + t) * 64 + lane];
         f.a[mt][t] = *reinterpret_cast<const half8v*>(&u);
       }
-    if constexpr (QT == Q_INT4) {
+    if constexpr (q_affine(QT)) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -847,15 +920,14 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   };
   auto compute = [&](const Wts& ow, const Frags& f) {
     const auto& a = f.a;
-    if constexpr (QT == Q_INT4) {
-#pragma unroll
-      for (int gs = 0; gs < 2; ++gs) {
+    if constexpr (q_affine(QT)) {
+      static_for<0, 2>([&](auto GS) __attribute__((always_inline)) {
+        constexpr int gs = decltype(GS)::value;
         floatx4 g[MT][NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const unsigned* dw = reinterpret_cast<const unsigned*>(&ow.qw[w]);
-          const half8v b0 = unpack_int4(dw[2 * gs], uk);
-          const half8v b1 = unpack_int4(dw[2 * gs + 1], uk);
+          const half8v b0 = unpack_step<QT, 2 * gs>(ow.qw[w], uk);
+          const half8v b1 = unpack_step<QT, 2 * gs + 1>(ow.qw[w], uk);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             g[mt][w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][2 * gs], b0, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -874,7 +946,7 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
               acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
             }
           }
-      }
+      });
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -1048,8 +1120,17 @@ hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float*
                       int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st) {
   hipLaunchKernelGGL(k_tile_int4, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, qw, rowbytes, D_out, nrb, C,
                      c_off, C_tot, (char*)R);
-  hipLaunchKernelGGL(k_tile_int4_params, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales, biases, gpr,
-                     D_out, nrb, C, c_off, C_tot, (char*)R);
+  hipLaunchKernelGGL(k_tile_affine_params<Q_INT4>, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales,
+                     biases, gpr, D_out, nrb, C, c_off, C_tot, (char*)R);
+  return hipGetLastError();
+}
+
+hipError_t qtile_int8(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,
+                      int gpr, int nrb, int C, int c_off, int C_tot, void* R, hipStream_t st) {
+  hipLaunchKernelGGL(k_tile_int8, dim3(grid_for((long)nrb * C * 64)), dim3(256), 0, st, qw, rowbytes, D_out, nrb, C,
+                     c_off, C_tot, (char*)R);
+  hipLaunchKernelGGL(k_tile_affine_params<Q_INT8>, dim3(grid_for((long)nrb * C * 16)), dim3(256), 0, st, scales,
+                     biases, gpr, D_out, nrb, C, c_off, C_tot, (char*)R);
   return hipGetLastError();
 }
 
@@ -1069,6 +1150,9 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
   PrepIn in{P.X, P.x_dtype, P.ldx};
   if (qt == Q_INT4)
     hipLaunchKernelGGL((k_prep<Q_INT4>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
+                       P.C_tot, P.Phi, P.S);
+  else if (qt == Q_INT8)
+    hipLaunchKernelGGL((k_prep<Q_INT8>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
                        P.C_tot, P.Phi, P.S);
   else
     hipLaunchKernelGGL((k_prep<Q_TERN>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
@@ -1108,6 +1192,10 @@ static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
     if (small) KQ_SMALL(Q_INT4);
     else if (mt == 1) KQ_WG(Q_INT4, 1);
     else KQ_WG(Q_INT4, 2);
+  } else if (qt == Q_INT8) {
+    if (small) KQ_SMALL(Q_INT8);
+    else if (mt == 1) KQ_WG(Q_INT8, 1);
+    else KQ_WG(Q_INT8, 2);
   } else {
     if (small) KQ_SMALL(Q_TERN);
     else if (mt == 1) KQ_WG(Q_TERN, 1);
@@ -1131,11 +1219,13 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
 
 hipError_t qswiglu_basis(int qt, const QEpi& E, const float* part, int ksplit, int B, int MP, int h,
                          hipStream_t st) {
-  if (E.K2 < 1 || E.K2 > kMaxK || B < 1 || B > MP || !E.Phi2 || (qt == Q_INT4 && !E.S2)) return hipErrorInvalidValue;
+  if (E.K2 < 1 || E.K2 > kMaxK || B < 1 || B > MP || !E.Phi2 || (q_affine(qt) && !E.S2)) return hipErrorInvalidValue;
   const int n_groups = (h + 63) / 64;
   const dim3 grid((unsigned)n_groups, (unsigned)B);
   if (qt == Q_INT4)
     hipLaunchKernelGGL(k_swiglu_basis<Q_INT4>, grid, dim3(64), 0, st, E, part, ksplit, B, MP, h, n_groups);
+  else if (qt == Q_INT8)
+    hipLaunchKernelGGL(k_swiglu_basis<Q_INT8>, grid, dim3(64), 0, st, E, part, ksplit, B, MP, h, n_groups);
   else
     hipLaunchKernelGGL(k_swiglu_basis<Q_TERN>, grid, dim3(64), 0, st, E, part, ksplit, B, MP, h, n_groups);
   return hipGetLastError();

@@ -104,7 +104,7 @@ int choose_ksplit(int n_rg, int C_tot, int B, int quant) {
 
 int layer_geometry(kans_qlayer* L) {
   const long Jb = (long)L->D_in * L->K;
-  if (L->quant == Q_INT4) {
+  if (q_affine(L->quant)) {
     const long pb = (Jb + L->group - 1) / L->group * L->group;
     const long pw = ((long)L->D_in + L->group - 1) / L->group * L->group;
     L->Cb = (int)((pb + kQSuper - 1) / kQSuper);
@@ -590,8 +590,8 @@ int host_forward(DevBuf& hx, DevBuf& hy, const void* X, int x_dtype, int D_in, v
   return 0;
 }
 
-// INT4 / INT8 layer from the reference arrays: decode records (INT4 only) and
-// prefill tiles (K in {1, 2, 4}) built from one upload of each array.
+// INT4 / INT8 layer from the reference arrays: decode records and prefill
+// tiles (K in {1, 2, 4}) built from one upload of each array.
 int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
                   const void* qweight, const float* scales, const float* biases, const void* qweight_base,
                   const float* scales_base, const float* biases_base, const void* bias, int bias_dtype,
@@ -602,8 +602,6 @@ int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bi
     return kans_fail(KANS_ERR_ARG, "has_base set but base arrays are null");
   int rc = validate_q(D_in, D_out, K, has_base, has_bias, group_size, quant);
   if (rc) return rc;
-  if (quant == Q_INT8 && !qp_supported(quant, K))
-    return kans_fail(KANS_ERR_UNSUPPORTED, "fused INT8 path takes K in {1, 2, 4} (K = %d)", K);
   std::lock_guard<std::mutex> lk(kans_mutex());
   if ((rc = kans_ensure_init())) return rc;
   hipStream_t st = kans_default_stream();
@@ -617,7 +615,7 @@ int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bi
   L->group = group_size;
   layer_geometry(L);
   prefill_geometry(L);
-  L->decode = quant == Q_INT4;
+  L->decode = true;
   auto fail = [&](int code) { delete L; return code; };
   if (L->decode && (rc = alloc_tiles(L))) return fail(rc);
   // one matrix (basis: D_out x D_in*K; base: D_out x D_in), rows padded to the group:
@@ -633,9 +631,10 @@ int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bi
     if ((r = upload_tmp(ts, sc, (size_t)D_out * gpr * 4, st))) return r;
     if ((r = upload_tmp(tb, bi, (size_t)D_out * gpr * 4, st))) return r;
     if (L->decode) {
-      hipError_t e = qtile_int4((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, rowbytes,
-                                (int)gpr, L->nrb_pad, seg ? L->Cw : L->Cb, seg ? L->Cb : 0, L->C_tot, L->R.p, st);
-      if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "INT4 re-tiling failed: %s", hipGetErrorString(e));
+      auto tile = quant == Q_INT8 ? qtile_int8 : qtile_int4;
+      hipError_t e = tile((const unsigned char*)tq.p, (const float*)ts.p, (const float*)tb.p, D_out, rowbytes,
+                          (int)gpr, L->nrb_pad, seg ? L->Cw : L->Cb, seg ? L->Cb : 0, L->C_tot, L->R.p, st);
+      if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "INT%d re-tiling failed: %s", bits, hipGetErrorString(e));
     }
     if (L->prefill &&
         (r = build_ptiles(L, seg, tq.p, rowbytes, (const float*)ts.p, (const float*)tb.p, (int)gpr, st)))
@@ -649,6 +648,66 @@ int create_affine(int bits, int D_in, int D_out, int K, int has_base, int has_bi
   HIP_TRY(hipStreamSynchronize(st));
   *out = L;
   return 0;
+}
+
+// Mean ms per block forward, the calls cycling through the n blocks (n > 1: each
+// call's weights were last read n - 1 calls earlier, so blocks whose weights
+// together exceed the MALL are timed from HBM).  Lock held.
+int time_blocks_locked(kans_gated* const* Gs, int n, const void* X, int x_dtype, void* Y, int y_dtype, int B,
+                       int warmup, int iters, int use_graph, float* ms) {
+  hipStream_t st = kans_default_stream();
+  const int d = Gs[0]->gate->D_in;
+  for (int b = 1; b < n; ++b)
+    if (Gs[b]->gate->D_in != d || Gs[b]->down->D_out != Gs[0]->down->D_out)
+      return kans_fail(KANS_ERR_ARG, "blocks of different shapes");
+  std::vector<hipGraph_t> graphs(n, nullptr);
+  std::vector<hipGraphExec_t> execs(n, nullptr);
+  auto cleanup = [&]() {
+    for (auto e : execs)
+      if (e) (void)hipGraphExecDestroy(e);
+    for (auto g : graphs)
+      if (g) (void)hipGraphDestroy(g);
+  };
+  int rc = 0;
+  for (int b = 0; b < n && !rc; ++b) {
+    // one eager call sizes every workspace before any capture
+    if ((rc = gated_forward_locked(Gs[b], X, x_dtype, d, Y, y_dtype, d, B, 1, st))) break;
+    if (!use_graph) continue;
+    hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+      rc = kans_fail(KANS_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+      break;
+    }
+    rc = gated_forward_locked(Gs[b], X, x_dtype, d, Y, y_dtype, d, B, 1, st);
+    e = hipStreamEndCapture(st, &graphs[b]);
+    if (!rc && e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    if (!rc && (e = hipGraphInstantiate(&execs[b], graphs[b], nullptr, nullptr, 0)) != hipSuccess)
+      rc = kans_fail(KANS_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  }
+  auto run = [&](int i) -> int {
+    const int b = i % n;
+    if (use_graph) {
+      HIP_TRY(hipGraphLaunch(execs[b], st));
+      return 0;
+    }
+    return gated_forward_locked(Gs[b], X, x_dtype, d, Y, y_dtype, d, B, 1, st);
+  };
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float t = 0.f;
+  for (int i = 0; i < warmup && !rc; ++i) rc = run(i);
+  if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+    rc = kans_fail(KANS_ERR_HIP, "hipEventCreate failed");
+  if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipEventRecord failed");
+  for (int i = 0; i < iters && !rc; ++i) rc = run(i);
+  if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+              hipEventElapsedTime(&t, e0, e1) != hipSuccess))
+    rc = kans_fail(KANS_ERR_HIP, "event timing failed");
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (rc) (void)hipStreamSynchronize(st);
+  cleanup();
+  if (!rc) *ms = t / iters;
+  return rc;
 }
 
 }  // namespace
@@ -875,45 +934,18 @@ int kans_gated_time(kans_gated* G, const void* X, int x_dtype, void* Y, int y_dt
   std::lock_guard<std::mutex> lk(kans_mutex());
   int rc = kans_ensure_init();
   if (rc) return rc;
-  hipStream_t st = kans_default_stream();
-  const int d = G->gate->D_in;
-  // one eager call sizes every workspace before any capture
-  if ((rc = gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st))) return rc;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  if (use_graph) {
-    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    rc = gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st);
-    hipError_t e = hipStreamEndCapture(st, &graph);
-    if (rc) return rc;
-    HIP_TRY(e);
-    HIP_TRY(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-  }
-  auto run = [&]() -> int {
-    if (use_graph) {
-      HIP_TRY(hipGraphLaunch(exec, st));
-      return 0;
-    }
-    return gated_forward_locked(G, X, x_dtype, d, Y, y_dtype, d, B, 1, st);
-  };
-  for (int i = 0; i < warmup; ++i)
-    if ((rc = run())) return rc;
-  hipEvent_t e0, e1;
-  HIP_TRY(hipEventCreate(&e0));
-  HIP_TRY(hipEventCreate(&e1));
-  HIP_TRY(hipEventRecord(e0, st));
-  for (int i = 0; i < iters; ++i)
-    if ((rc = run())) return rc;
-  HIP_TRY(hipEventRecord(e1, st));
-  HIP_TRY(hipEventSynchronize(e1));
-  float t = 0.f;
-  HIP_TRY(hipEventElapsedTime(&t, e0, e1));
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (exec) (void)hipGraphExecDestroy(exec);
-  if (graph) (void)hipGraphDestroy(graph);
-  *ms = t / iters;
-  return 0;
+  return time_blocks_locked(&G, 1, X, x_dtype, Y, y_dtype, B, warmup, iters, use_graph, ms);
+}
+
+int kans_gated_time_rotate(kans_gated* const* blocks, int n, const void* X, int x_dtype, void* Y, int y_dtype, int B,
+                           int warmup, int iters, float* ms) {
+  if (!blocks || n <= 0 || !X || !Y || !ms || iters <= 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  for (int b = 0; b < n; ++b)
+    if (!blocks[b]) return kans_fail(KANS_ERR_ARG, "null block");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  return time_blocks_locked(blocks, n, X, x_dtype, Y, y_dtype, B, warmup, iters, 1, ms);
 }
 
 // Packed bytes the decode path streams per block forward (weights + group

@@ -6,9 +6,9 @@ A layer quantized with ``to_int8`` / ``to_int4`` (group 64) or ``to_ternary``
 formats (quantization.py:13-99, 191-246).  ``QLayerEngine`` uploads those packed
 arrays once and runs the fused kernels on them, which move the packed bytes
 instead of dequantized fp32 weights: the decode GEMVs for batches of at most
-``MAX_DECODE_B`` rows (INT4, ternary) and the fused prefill kernel for larger
-batches and for INT8 (Chebyshev degree K in ``PREFILL_K``).  The engine is
-rebuilt when the packed objects change (a new ``to_int4`` / ``to_ternary``).
+``MAX_DECODE_B`` rows and the fused prefill kernel for larger batches
+(Chebyshev degree K in ``PREFILL_K``).  The engine is rebuilt when the packed
+objects change (a new ``to_int8`` / ``to_int4`` / ``to_ternary``).
 """
 from __future__ import annotations
 
@@ -31,7 +31,7 @@ def fused_batch_ok(fmt: str, K: int, B: int) -> bool:
     fused quantized kernels (else the caller uses the dequantized weights)."""
     if B <= 0:
         return False
-    if B <= MAX_DECODE_B and fmt != "int8":
+    if B <= MAX_DECODE_B:
         return True
     return K in PREFILL_K
 
@@ -140,7 +140,7 @@ def layer_engine(layer) -> Optional["QLayerEngine"]:
             or layer._resolve_compute() != "float16":
         return None
     fmt = packed_format(layer)
-    if fmt is None or (fmt == "int8" and int(layer.degree) not in PREFILL_K):
+    if fmt is None:
         return None
     eng = layer.__dict__.get("_qlayer_engine")
     if eng is None or not eng.current(layer):

@@ -17,8 +17,8 @@ Quantized path: a float16 block quantized with ``to_int8()`` / ``to_int4()``
 (``_qengine.GatedEngine``): the packed weights are read from HBM once per
 forward instead of being dequantized, and gate/up, SwiGLU and down run back to
 back on the device (decode GEMVs up to 32 rows, the fused prefill kernels -- one
-launch for gate|up with the SwiGLU epilogue, one for down -- above, and for
-INT8).  Other cases use the three layers.
+launch for gate|up with the SwiGLU epilogue, one for down -- above).  Other
+cases use the three layers.
 """
 from __future__ import annotations
 
@@ -32,7 +32,7 @@ from ._engine import DT_F16, DT_F32, from_bf16_bits
 from ._layer import device_layer_handle
 from .cheby_kan import ChebyKAN
 from .quantization import to_int4, to_int8, to_ternary
-from ._qengine import PREFILL_K, GatedEngine, fused_batch_ok, packed_format
+from ._qengine import GatedEngine, fused_batch_ok, packed_format
 
 
 class GatedKAN:
@@ -67,8 +67,6 @@ class GatedKAN:
             return None
         fmt = packed_format(self.gate_kan)
         if fmt is None or packed_format(self.up_kan) != fmt or packed_format(self.down_kan) != fmt:
-            return None
-        if fmt == "int8" and self.degree not in PREFILL_K:
             return None
         eng = self.__dict__.get("_qblock")
         if eng is None or eng.fmt != fmt or not eng.current(self):

@@ -189,7 +189,7 @@ def _qlayer(lib, fmt, pk_w, pk_b, di, do):
 @pytest.mark.parametrize("fmt", ["int4", "ternary", "int8"])
 def test_cfg5_gatedkan_full_shape(gpu, cfg5_weights, fmt):
     """the fused quantized GatedKAN block at B = 1 and 32 (decode: one HIP graph of prep,
-    gate|up GEMV with the SwiGLU epilogue, down GEMV, reduce; INT8 runs the prefill kernel) and at B = 8192
+    gate|up GEMV with the SwiGLU epilogue at B = 1, down GEMV, reduce) and at B = 8192
     (prefill: gate|up in one launch with the SwiGLU epilogue, then down), against the float64 oracle block
     out = Down(SiLU(Gate(x)) * Up(x)) (gated_kan.py:86-138) on the dequantized weights.  At B = 8192 a seeded
     sample of 48 rows is checked (rows are independent), plus a bitwise rerun of the whole batch."""

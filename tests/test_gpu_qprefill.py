@@ -1,4 +1,4 @@
-"""GPU parity of the fused quantized prefill path (batches above 32 rows, and INT8 at every batch).
+"""GPU parity of the fused quantized prefill path (batches above 32 rows).
 
 The quantized forward of the reference is forward(x, dequant(quant(W))) in fp32
 (quantization.py:152-188); the fused kernel decodes the packed codes into fp16
@@ -145,25 +145,21 @@ def test_qlayer_prefill_io_dtypes(gpu, fmt):
         lib.kans_qlayer_destroy(h)
 
 
-def test_qlayer_prefill_rejects_unsupported_K(gpu):
-    """K outside {1, 2, 4}: INT8 layers cannot be built; INT4 / ternary layers decode small batches and report
-    KANS_ERR_UNSUPPORTED (-5) for batches the prefill kernel would take."""
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+def test_qlayer_prefill_rejects_unsupported_K(gpu, fmt):
+    """K outside {1, 2, 4}: the layer decodes small batches (any K) and reports KANS_ERR_UNSUPPORTED (-5) for
+    batches the prefill kernel would take."""
     lib = gpu
     rng = np.random.default_rng(0)
-    W = rng.normal(0, 0.1, (40, 24 * 3)).astype(np.float32)
-    (q, s, b), _ = quantize(lib, "int8", W)
-    h = ctypes.c_void_p()
-    assert lib.kans_qlayer_create_int8(24, 40, 3, 0, 0, 64, q.ctypes.data, s.ctypes.data, b.ctypes.data, None, None,
-                                       None, None, 0, ctypes.byref(h)) == -5
-    h4, L = make_qlayer(lib, "int4", 24, 40, 3, True, False, seed=1)
+    h, L = make_qlayer(lib, fmt, 24, 40, 3, True, False, seed=1)
     try:
         x = rng.uniform(-1, 1, (33, 24)).astype(np.float32)
         y = np.zeros((33, 40), np.float32)
-        assert lib.kans_qlayer_forward_host(h4, x.ctypes.data, 0, y.ctypes.data, 0, 33) == -5
-        y8 = run(lib, h4, x[:8], 40)          # decode path: any K
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 0, y.ctypes.data, 0, 33) == -5
+        y8 = run(lib, h, x[:8], 40)          # decode path: any K
         assert O.rel_err(y8, _oracle_rounded(L, x[:8])) <= 2e-3
     finally:
-        lib.kans_qlayer_destroy(h4)
+        lib.kans_qlayer_destroy(h)
 
 
 # ---------------------------------------------------------------- GatedKAN block
@@ -238,7 +234,7 @@ def test_gated_decode_and_prefill_agree(gpu, fmt):
 @pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
 def test_python_quantized_fp16_layer_uses_packed_weights(gpu, quant):
     """ChebyKAN(...).half().to_<quant>() keeps fp16 compute and runs on its packed weights at every batch
-    (decode GEMV up to 32 rows for INT4 / ternary, the prefill kernel above and for INT8)."""
+    (decode GEMV up to 32 rows, the prefill kernel above)."""
     import metal_kans as mk
     np.random.seed(7)
     L = mk.ChebyKAN(80, 50, degree=4)

@@ -27,7 +27,7 @@ def _dev(lib, a):
     return p
 
 
-@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 def test_noalloc_matches_allocating_entry_point(gpu, fmt):
     lib = gpu
     d, hdim = 256, 640
