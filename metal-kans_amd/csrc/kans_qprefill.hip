@@ -274,26 +274,33 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   // even K: per slot pair), so each load is one coalesced 64-lane access.
   constexpr int WB = QT == Q_TERN ? (KQ == 1 ? 2 : 4) : CB;   // bytes of one basis word group entry
   constexpr int NG = QT == Q_TERN ? (KQ == 1 ? 1 : KQ / 2) : KQ;  // basis word groups per block
+  // Every address is a wave-uniform base (feature block, column block, slot
+  // group) plus this lane's fixed byte offset, so the loads take the
+  // scalar-base + 32-bit vector-offset form and cost no per-block VALU.
+  // Group of a lane's chunk: g = (16 f + 8 hh) K / GS; with GS = 64 (INT4 /
+  // INT8, K <= 4) or GS = 32 and K <= 2 the hh term never crosses a group
+  // boundary, with GS = 32 and K = 4 it adds hh (base segment, K = 1: never).
+  const unsigned cb_off = (unsigned)lane * WB, cw_off = (unsigned)lane * CB;
+  const unsigned pb_off = (unsigned)(((QT == Q_TERN && KQ == 4 ? hh * M.ldp : 0) + o) * PF * 4);
+  const unsigned pw_off = (unsigned)(o * PF * 4);
   auto load_cb = [&](int fbq, int g, QRegs& r) __attribute__((always_inline)) {
     const int f = min(fbq, fb_end - 1);
-    const unsigned char* p = M.cb + ((((long)f * M.nob_pad + ob) * NG + g) * 64 + lane) * WB;
-    load_bytes<WB>(p, &r.cb[g * (WB >= 4 ? WB / 4 : 1)]);
+    const unsigned char* ub = M.cb + (((long)f * M.nob_pad + ob) * NG + g) * (64 * WB);
+    load_bytes<WB>(ub + cb_off, &r.cb[g * (WB >= 4 ? WB / 4 : 1)]);
   };
   auto load_cw = [&](int fbq, QRegs& r) __attribute__((always_inline)) {
     const int f = min(fbq, fb_end - 1);
-    load_bytes<CB>(M.cw + (((long)f * M.nob_pad + ob) * 64 + lane) * CB, r.cw);
+    load_bytes<CB>(M.cw + ((long)f * M.nob_pad + ob) * (64 * CB) + cw_off, r.cw);
   };
   auto load_params = [&](int fbq, QRegs& r) __attribute__((always_inline)) {
     const int f = min(fbq, fb_end - 1);
-    const int gb = ((16 * f + 8 * hh) * KQ) / GS;
-    const float* pb = M.pb + ((long)gb * M.ldp + o) * PF;
-    r.pb[0] = pb[0];
-    if constexpr (PF == 2) r.pb[1] = pb[1];
+    const char* pb = reinterpret_cast<const char*>(M.pb + (long)((16 * f * KQ) / GS) * M.ldp * PF) + pb_off;
+    r.pb[0] = reinterpret_cast<const float*>(pb)[0];
+    if constexpr (PF == 2) r.pb[1] = reinterpret_cast<const float*>(pb)[1];
     if constexpr (HB) {
-      const int gw = (16 * f + 8 * hh) / GS;
-      const float* pw = M.pw + ((long)gw * M.ldp + o) * PF;
-      r.pw[0] = pw[0];
-      if constexpr (PF == 2) r.pw[1] = pw[1];
+      const char* pw = reinterpret_cast<const char*>(M.pw + (long)((16 * f) / GS) * M.ldp * PF) + pw_off;
+      r.pw[0] = reinterpret_cast<const float*>(pw)[0];
+      if constexpr (PF == 2) r.pw[1] = reinterpret_cast<const float*>(pw)[1];
     }
   };
   auto load_all = [&](int fbq, QRegs& r) {
@@ -454,6 +461,10 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
       }
       pack(af[0], v);
     }
+    // slot 0's B-fragment reads stay ahead of the slots' scheduling regions:
+    // inside slot 0's the scheduler placed each just before its MFMA, which
+    // then waited for it
+    __builtin_amdgcn_sched_barrier(0);
     static_for<0, KP>([&](auto SCC) __attribute__((always_inline)) {
       constexpr int SC = decltype(SCC)::value;
       constexpr int P = SC & 1;
