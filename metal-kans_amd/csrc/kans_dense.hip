@@ -595,6 +595,9 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       gen.begin(xf, bp, bs_sel);
       __builtin_amdgcn_sched_barrier(0);
       bread(bfr[0], cur, 0);
+      // the reads issue here: in the region of slot 0 the scheduler placed
+      // each just before its MFMA, which then waited for it
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (BASIS == BASIS_BSPLINE_TAB) {
         float v[NV];
 #pragma unroll
