@@ -36,7 +36,7 @@ PEAK = {"f16": 2516.6, "bf16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s (MI3
 # from inside the timed process).
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_kan_fused_block_cfg3_fastkan_fp16.txt")
 SECONDARY = ("ns_cheby_fp16", "ns_bspline_fp16", "cfg4_bspline_bf16", "cfg4_bspline_fp32", "cfg1_cheby_fp32",
-             "cfg2", "cfg5")
+             "cfg2", "cfg5", "ref_published")
 HBM_PEAK_GBS = 8000.0
 METRIC = "fused KAN fwd TFLOP/s + % MFMA peak; quantized-weight HBM GB/s (1 MI355X)"
 
@@ -443,6 +443,38 @@ def run_cfg5(lib, warmup, iters):
     return out
 
 
+# The reference's own published points (README.md:147-162, scripts/render_figures.py:29-37): 64 -> 64 fp32
+# layers with the SiLU base branch, host wall clock per full call (Apple GPU, unified memory), ms per B.
+REF_PUBLISHED_MS = {
+    "cheby": {64: 0.279, 1024: 0.362, 4096: 0.812, 16384: 1.659, 65536: 8.995},
+    "rbf": {64: 0.268, 1024: 0.318, 4096: 0.710, 16384: 2.366, 65536: 14.815},
+    "bspline": {64: 0.258, 1024: 0.339, 4096: 0.782, 16384: 2.347, 65536: 14.857},
+}
+
+
+def run_ref_published(mk, iters):
+    """The reference's published benchmark shape: ChebyKAN(64, 64, degree=4), FastKAN(64, 64, 8 centres),
+    BSplineKAN(64, 64, grid 5), fp32, timed as the reference times it (layer.benchmark: mean host wall clock
+    per full synchronous call, here including the PCIe copies of x and y that unified memory does not need).
+    Context beside the published Apple-GPU numbers, not a roofline measurement."""
+    rng = np.random.default_rng(1100)
+    out = {}
+    for kind, K in (("cheby", 4), ("rbf", 8), ("bspline", 8)):
+        np.random.seed(1100)
+        L = {"cheby": lambda: mk.ChebyKAN(64, 64, degree=4), "rbf": lambda: mk.FastKAN(64, 64, num_centers=8),
+             "bspline": lambda: mk.BSplineKAN(64, 64, grid_size=5)}[kind]()
+        rows = []
+        for B, ref_ms in REF_PUBLISHED_MS[kind].items():
+            x = rng.uniform(-1, 1, (B, 64)).astype(np.float32)
+            ms = L.benchmark(x, warmup=5, iters=max(10, min(iters, 50)))
+            flops = 2.0 * B * 64 * 64 * (K + 1)
+            rows.append({"B": B, "ms_per_call": round(ms, 4), "gflops": round(flops / ms / 1e6, 1),
+                         "reference_published_ms": ref_ms, "reference_over_this": round(ref_ms / ms, 2)})
+        out[kind] = rows
+    log(f"[bench] ref_published: {out}")
+    return {"ref_published_64x64_fp32_host_call": out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -541,6 +573,8 @@ def main():
             workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters)
         if want("cfg5"):
             workloads.update(run_cfg5(lib, a.warmup, iters))
+        if want("ref_published"):
+            workloads.update(run_ref_published(mk, iters))
     result["workloads"] = workloads
     if not (a.quick or a.no_cpu):
         result["cpu_baseline"] = cpu_baseline_cfg3(st["x"], st["L"])

@@ -184,6 +184,33 @@ class KANLayerBase:
     def backward(self, *args, **kwargs):
         raise NotImplementedError("training (backward) is outside this build's forward-only scope")
 
+    # ---- benchmark (cheby_kan.py:233-257, fast_kan.py:223-247, bspline_kan.py:227-251) ----------
+    def _benchmark_args(self) -> tuple:
+        """(entry-point name, basis weight array, arrays passed between W_base and bias, integer / float
+        arguments between D_out and has_base) of the reference-named benchmark_metal_* call."""
+        raise NotImplementedError
+
+    def benchmark(self, x: np.ndarray, warmup: int = 10, iters: int = 50) -> float:
+        """Mean wall-clock ms per full host call of the fp32 reference-named forward on x (the reference's
+        benchmark: host arrays in, host array out, synchronous).  The weights are passed as float32 (a
+        16-bit layer's arrays are converted first; the reference would hand their raw bytes on)."""
+        x = np.asarray(x, dtype=np.float32)
+        x_flat = np.ascontiguousarray(x.reshape(-1, self.in_features))
+        B = x_flat.shape[0]
+        y = np.empty((B, self.out_features), dtype=np.float32)
+        name, W, mid, tail = self._benchmark_args()
+        f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+        W, Wb, bias = f32(W), f32(self.w_base), f32(self.bias)
+        mid = [f32(a) for a in mid]
+        ms = getattr(device.get_metal_bridge(), name)(x_flat.ctypes.data, W.ctypes.data, Wb.ctypes.data,
+                                                      *[a.ctypes.data for a in mid],
+                                                      bias.ctypes.data, y.ctypes.data, B, self.in_features,
+                                                      self.out_features, *tail, self.has_base, self.has_bias,
+                                                      int(warmup), int(iters))
+        if ms < 0:
+            raise RuntimeError(f"{name} failed: {device.last_error()}")
+        return float(ms)
+
 
 def device_layer_handle(layer: KANLayerBase, compute: str) -> int:
     """Make the layer's device weights current for compute dtype ``compute`` and return its ``kans_layer``

@@ -70,6 +70,9 @@ class BSplineKAN(KANLayerBase):
         self._compute = "float16"
         return self
 
+    def _benchmark_args(self) -> tuple:
+        return "benchmark_metal_bspline", self.w_spline, (self.grid,), (int(self.grid_size), int(self.spline_order))
+
     def float(self) -> "BSplineKAN":
         """Converts layer parameters to FP32 single precision."""
         self._cast_params(np.float32)

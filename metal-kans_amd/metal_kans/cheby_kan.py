@@ -60,6 +60,9 @@ class ChebyKAN(KANLayerBase):
         self._compute = "float16"
         return self
 
+    def _benchmark_args(self) -> tuple:
+        return "benchmark_metal_cheby", self.w_cheby, (), (int(self.degree),)
+
     def float(self) -> "ChebyKAN":
         """Converts layer parameters to FP32 single precision."""
         self._cast_params(np.float32)

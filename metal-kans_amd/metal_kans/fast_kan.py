@@ -63,6 +63,9 @@ class FastKAN(KANLayerBase):
         self._compute = "float16"
         return self
 
+    def _benchmark_args(self) -> tuple:
+        return "benchmark_metal_fastkan", self.w_rbf, (self.grid,), (int(self.num_centers), float(self.inv_denominator))
+
     def float(self) -> "FastKAN":
         """Converts layer parameters (and the grid) to FP32 single precision."""
         self._cast_params(np.float32)

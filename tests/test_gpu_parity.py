@@ -538,6 +538,22 @@ def test_reference_named_16bit_entry_points(gpu):
             assert O.rel_err(dec(y0), ref0) <= 2e-2, (kind, dt)
 
 
+def test_layer_benchmark_method(gpu):
+    """layer.benchmark(x, warmup, iters) (cheby_kan.py:233-257, fast_kan.py:223-247, bspline_kan.py:227-251):
+    mean ms per full host call of the fp32 reference-named forward, for fp32 and converted 16-bit layers;
+    the timed calls compute what the fp32 entry point computes."""
+    import metal_kans as mk
+    np.random.seed(11)
+    x = np.random.default_rng(11).uniform(-1, 1, (96, 40)).astype(np.float32)
+    for L in (mk.ChebyKAN(40, 24, degree=4), mk.FastKAN(40, 24, num_centers=8), mk.BSplineKAN(40, 24, grid_size=5)):
+        y_ref = L(x)
+        ms = L.benchmark(x, warmup=2, iters=5)
+        assert np.isfinite(ms) and ms > 0
+        assert np.array_equal(L(x), y_ref)
+        L.half()
+        assert L.benchmark(x, warmup=1, iters=2) > 0
+
+
 def test_reference_chain_entry_point(gpu):
     lib = gpu
     rng = np.random.default_rng(12)
