@@ -163,11 +163,24 @@ __global__ void k_tile_affine_params(const float* __restrict__ scales, const flo
 }
 
 // Ternary w_packed: row n is `wpr` uint32 words, code of index j at bits
-// 2*(j%16) of word j/16.  T[rb][c][lane] (uint2): word u in {0,1} covers steps
-// 2u ("A") and 2u+1 ("B"); the 8 codes of step t for lane (q, r) are those of
-// row 16*rb + r at indices j0 = 128c + 32t + 8q .. +7.  Code e of step A sits at
-// bit 2p (e = 2p) or 16 + 2p (e = 2p+1); of step B at bit 8 + 2p or 24 + 2p,
-// so that one shift aligns the two codes of an fp16 pair at bits 8 and 24.
+// 2*(j%16) of word j/16 (code 0 -> -1, 2 -> +1, 1 and 3 -> 0).
+// T[rb][c][lane] (uint2): word u in {0,1} covers steps 2u and 2u+1; the 8 codes
+// of step t for lane (q, r) are those of row 16*rb + r at indices
+// j0 = 128c + 32t + 8q .. +7.  Each weight is stored as two bits, "non-zero"
+// and "negative", placed so that the fp16 pair P = 4 (t & 1) + p (elements
+// e = 2p, 2p + 1 of the step) is (word << kTernShift[P]) & 0x88008800: the
+// non-zero bit lands on fp16 exponent bit 11, the sign on bit 15, so each
+// element reads +-2^-13 or 0 (unpack_tern).  The eight shifts map the pairs
+// onto disjoint bit sets that cover the word.
+constexpr int kTernShift[8] = {11, 10, 9, 8, 3, 2, 1, 0};
+constexpr unsigned kTernMask = 0x88008800u;
+
+__device__ __forceinline__ unsigned tern_bits(unsigned code, int k, int half) {
+  const unsigned nz = (code == 0u || code == 2u) ? 1u : 0u;
+  const unsigned neg = code == 0u ? 1u : 0u;
+  return (nz << (11 + 16 * half - k)) | (neg << (15 + 16 * half - k));
+}
+
 __global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim, int D_out, int nrb, int C,
                             int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 64;
@@ -192,12 +205,12 @@ __global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim
         } else {
           h = 0x5555u;
         }
-        const int base = (t & 1) ? 8 : 0;
         unsigned v = 0u;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-          v |= ((h >> (4 * p)) & 3u) << (base + 2 * p);           // e = 2p
-          v |= ((h >> (4 * p + 2)) & 3u) << (base + 16 + 2 * p);  // e = 2p + 1
+          const int k = kTernShift[4 * (t & 1) + p];
+          v |= tern_bits((h >> (4 * p)) & 3u, k, 0);      // e = 2p
+          v |= tern_bits((h >> (4 * p + 2)) & 3u, k, 1);  // e = 2p + 1
         }
         out[t >> 1] |= v;
       }
@@ -206,7 +219,10 @@ __global__ void k_tile_tern(const unsigned* __restrict__ wp, int wpr, long K_dim
   }
 }
 
-// Ternary scales: SB[rb][c][r] = scales of the four 32-groups of superchunk c.
+// Ternary scales: SB[rb][c][r] = scales of the four 32-groups of superchunk c,
+// times 2^13 (the unpacked weights are +-2^-13: every product phi * 2^-13 and
+// every fp32 partial sum of them is exact scaling of the +-1 case, so
+// (2^13 s) * g equals s * (2^13 g) bit for bit).
 __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, int D_out, int nrb, int C, int c_off,
                                    int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 16;
@@ -221,7 +237,7 @@ __global__ void k_tile_tern_params(const float* __restrict__ scales, int gpr, in
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int g = 4 * c + t;
-        if (g < gpr) v[t] = scales[(long)n * gpr + g];
+        if (g < gpr) v[t] = scales[(long)n * gpr + g] * 8192.0f;
       }
     }
     *reinterpret_cast<float4*>(R + qparam_offset<Q_TERN>(rb, c_off + c, C_tot, r)) = make_float4(v[0], v[1], v[2], v[3]);
@@ -360,14 +376,13 @@ __global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in
 // literal and reads at most one SGPR); as opaque register values it selects
 // one v_and_or_b32.  The empty asm only hides the values from constant folding.
 struct UnpackConsts {
-  unsigned nib_mask, nib_magic, tsel_mask, tsel_zero, byte_magic;
+  unsigned nib_mask, nib_magic, tern_mask, byte_magic;
   __device__ __forceinline__ void init() {
     nib_mask = 0x000F000Fu;
     nib_magic = 0x64006400u;
-    tsel_mask = 0x03000300u;
-    tsel_zero = 0x000C000Cu;
+    tern_mask = kTernMask;
     byte_magic = 0x64646464u;  // high byte of fp16 1024 + q, for the INT8 v_perm_b32
-    asm volatile("" : "+v"(nib_mask), "+v"(nib_magic), "+v"(tsel_mask), "+v"(tsel_zero), "+v"(byte_magic));
+    asm volatile("" : "+v"(nib_mask), "+v"(nib_magic), "+v"(tern_mask), "+v"(byte_magic));
   }
 };
 
@@ -393,19 +408,16 @@ __device__ __forceinline__ half8v unpack_int8(unsigned w0, unsigned w1, const Un
   return *reinterpret_cast<half8v*>(o);
 }
 
-// Ternary: the 8 codes of one step (layout of k_tile_tern) -> 8 fp16 in
-// {-1, 0, +1}.  v_perm_b32 picks each value's high byte from the table
-// {0xBC, 0x00, 0x3C, 0x00} (code 0 -> -1.0, 1 -> 0, 2 -> +1.0, 3 -> 0) with the
-// code as selector; selector 12 yields the zero low bytes.
+// Ternary: the 8 weights of step 2u + B_STEP in word u (layout of k_tile_tern)
+// -> 8 fp16 in {-2^-13, 0, +2^-13}: one shift and one AND per fp16 pair (the
+// last pair of a word none), 15 instructions per 16 weights.
 template <int B_STEP>
 __device__ __forceinline__ half8v unpack_tern(unsigned w, const UnpackConsts& k) {
-  constexpr unsigned kTable = 0x003C00BCu;
   unsigned o[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const unsigned v = B_STEP ? (w >> (2 * p)) : (w << (8 - 2 * p));
-    const unsigned sel = (v & k.tsel_mask) | k.tsel_zero;  // codes in bytes 1, 3; 12 (= 0x00) in bytes 0, 2
-    o[p] = __builtin_amdgcn_perm(0u, kTable, sel);
+    const int sh = kTernShift[4 * B_STEP + p];
+    o[p] = (sh ? (w << sh) : w) & k.tern_mask;
   }
   return *reinterpret_cast<half8v*>(o);
 }
@@ -889,6 +901,22 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // Passes a ring slot's registers through an empty asm after the wait that
+  // covers them, so their first use (the unpack) cannot be hoisted above it:
+  // hoisted, the code words are read while later loads are still in flight
+  // and the compiler's own wait for them becomes vmcnt(0), which drains the
+  // whole ring.
+  auto pin = [&](Wts& o) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      unsigned* d = reinterpret_cast<unsigned*>(&o.qw[w]);
+#pragma unroll
+      for (int i = 0; i < (int)(sizeof(QWord) / 4); ++i) asm volatile("" : "+v"(d[i]));
+      float* s = reinterpret_cast<float*>(&o.sb[w]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(s[i]));
+    }
+  };
 
   floatx4 acc[MT][NW];
 #pragma unroll
@@ -974,20 +1002,26 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   Wts w0, w1, w2;
   Frags f;
   issue(c_lo, sa0, ss0, w0);
+  // every load of superchunk c_lo before any of c_lo + 1: the waits count
+  // loads in issue order
+  __builtin_amdgcn_sched_barrier(0);
   issue(c_lo + 1, sa1, ss1, w1);
   // whole rounds of three superchunks: a branch-free body keeps the
   // compiler's own wait counts exact (a break inside it made them vmcnt(0))
   int c = c_lo;
   for (; c + 3 <= c_hi; c += 3) {
     sync_stage();
+    pin(w0);
     read_frags(sa0, ss0, f);
     issue(c + 2, sa2, ss2, w2);
     compute(w0, f);
     sync_stage();
+    pin(w1);
     read_frags(sa1, ss1, f);
     issue(c + 3, sa0, ss0, w0);
     compute(w1, f);
     sync_stage();
+    pin(w2);
     read_frags(sa2, ss2, f);
     issue(c + 4, sa1, ss1, w1);
     compute(w2, f);
