@@ -833,13 +833,20 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   constexpr int NW = kQNW;
   constexpr int FR = MT * 4;                    // activation fragments (1 KB each) per superchunk
   // vector-memory instructions per wave and superchunk: code words (one or two
-  // 16-byte loads), group parameters, fragment copies, group sums
-  constexpr int OPS = NW * (qtile_bytes(QT) / 64 > 16 ? 2 : 1) + NW + FR / 4 + (q_affine(QT) ? 1 : 0);
+  // 16-byte loads), fragment copies, group sums, the group-parameter copy
+  // PR: group parameters through LDS (below); INT4 keeps them in the register
+  // ring (through LDS its MT = 2 kernel took 256 registers, one wave per SIMD)
+  constexpr bool PR = QT != Q_INT4;
+  constexpr int OPS = NW * (qtile_bytes(QT) / 64 > 16 ? 2 : 1) + FR / 4 + (q_affine(QT) ? 1 : 0) + (PR ? 1 : NW);
   // three separate arrays per ring (not one indexed array): the compiler then
   // sees that reads of one stage do not depend on the copies into another,
   // and waits only for this stage's copies
   __shared__ uint4 sa0[FR * 64], sa1[FR * 64], sa2[FR * 64];
   __shared__ float2 ss0[32], ss1[32], ss2[32];
+  // PR: each wave's group parameters (its records' 1 KB parameter block) take
+  // the same route, so the register ring holds only code words (ternary MT = 2:
+  // 174 -> 150 registers, three waves per SIMD instead of two)
+  __shared__ float4 sp0[PR ? 4 * 64 : 1], sp1[PR ? 4 * 64 : 1], sp2[PR ? 4 * 64 : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ks = blockIdx.x % ksplit;
@@ -861,15 +868,22 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
   struct Wts {
     QWord qw[NW];
-    float4 sb[NW];
+    float4 sb[NW];  // !PR only
   };
   auto load_w = [&](int c, Wts& o) {
     const char* rec = rbase + (long)c * qrec_bytes(QT);
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
-      o.sb[w] = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
+      if constexpr (!PR) o.sb[w] = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + (w * 16 + r) * 16);
     }
+  };
+  // the record's parameter block (kQNW x 16 rows x float4, 1 KB) into this
+  // wave's slot of a stage: lane l copies bytes 16 l .. 16 l + 15
+  auto dma_params = [&](int c, float4* sp) {
+    const char* src = rbase + (long)c * qrec_bytes(QT) + NW * qtile_bytes(QT) + lane * 16;
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&sp[wave * 64], 16, 0,
+                                     NT ? 2 : 0);  // aux 2: non-temporal
   };
   // fragment j = 4 mt + t of superchunk c: lane l holds row 16 mt + l % 16,
   // reduction indices 128 c + 32 t + 8 (l / 16) .. + 7; wave w copies the
@@ -888,10 +902,11 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
       __builtin_amdgcn_global_load_lds(ssrc, (__attribute__((address_space(3))) void*)ss, 4, 0, 0);
     }
   };
-  auto issue = [&](int c, uint4* sa, float2* ss, Wts& o) {
+  auto issue = [&](int c, uint4* sa, float2* ss, float4* sp, Wts& o) {
     const int cc = min(c, c_hi - 1);
     load_w(cc, o);
     dma(cc, sa, ss);
+    if constexpr (PR) dma_params(cc, sp);
   };
   // waits for everything but the OPS loads of the superchunk after this one,
   // then the workgroup barrier; no fence (that would wait for all loads)
@@ -912,9 +927,11 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
       unsigned* d = reinterpret_cast<unsigned*>(&o.qw[w]);
 #pragma unroll
       for (int i = 0; i < (int)(sizeof(QWord) / 4); ++i) asm volatile("" : "+v"(d[i]));
-      float* s = reinterpret_cast<float*>(&o.sb[w]);
+      if constexpr (!PR) {
+        float* sv = reinterpret_cast<float*>(&o.sb[w]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(s[i]));
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(sv[i]));
+      }
     }
   };
 
@@ -930,8 +947,13 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   struct Frags {
     half8v a[MT][4];
     float2 sg[MT][4];  // INT4 / INT8: group sums of rows 16 mt + 4 q + i
+    float4 sb[NW];     // PR: group parameters of row r of tile w
   };
-  auto read_frags = [&](const uint4* sa, const float2* ss, Frags& f) {
+  auto read_frags = [&](const uint4* sa, const float2* ss, const float4* sp, Frags& f) {
+    if constexpr (PR) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) f.sb[w] = sp[wave * 64 + w * 16 + r];
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -969,8 +991,9 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
             const float S_ = gs ? f.sg[mt][i].y : f.sg[mt][i].x;
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
-              const float s = gs ? ow.sb[w].z : ow.sb[w].x;
-              const float s2 = gs ? ow.sb[w].w : ow.sb[w].y;
+              const float4& sbw = PR ? f.sb[w] : ow.sb[w];
+              const float s = gs ? sbw.z : sbw.x;
+              const float s2 = gs ? sbw.w : sbw.y;
               acc[mt][w][i] = __builtin_fmaf(s, g[mt][w][i], __builtin_fmaf(s2, S_, acc[mt][w][i]));
             }
           }
@@ -989,7 +1012,8 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
         }
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const float s = t == 0 ? ow.sb[w].x : t == 1 ? ow.sb[w].y : t == 2 ? ow.sb[w].z : ow.sb[w].w;
+          const float4& sbw = PR ? f.sb[w] : ow.sb[w];
+          const float s = t == 0 ? sbw.x : t == 1 ? sbw.y : t == 2 ? sbw.z : sbw.w;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1001,41 +1025,41 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
 
   Wts w0, w1, w2;
   Frags f;
-  issue(c_lo, sa0, ss0, w0);
+  issue(c_lo, sa0, ss0, sp0, w0);
   // every load of superchunk c_lo before any of c_lo + 1: the waits count
   // loads in issue order
   __builtin_amdgcn_sched_barrier(0);
-  issue(c_lo + 1, sa1, ss1, w1);
+  issue(c_lo + 1, sa1, ss1, sp1, w1);
   // whole rounds of three superchunks: a branch-free body keeps the
   // compiler's own wait counts exact (a break inside it made them vmcnt(0))
   int c = c_lo;
   for (; c + 3 <= c_hi; c += 3) {
     sync_stage();
     pin(w0);
-    read_frags(sa0, ss0, f);
-    issue(c + 2, sa2, ss2, w2);
+    read_frags(sa0, ss0, sp0, f);
+    issue(c + 2, sa2, ss2, sp2, w2);
     compute(w0, f);
     sync_stage();
     pin(w1);
-    read_frags(sa1, ss1, f);
-    issue(c + 3, sa0, ss0, w0);
+    read_frags(sa1, ss1, sp1, f);
+    issue(c + 3, sa0, ss0, sp0, w0);
     compute(w1, f);
     sync_stage();
     pin(w2);
-    read_frags(sa2, ss2, f);
-    issue(c + 4, sa1, ss1, w1);
+    read_frags(sa2, ss2, sp2, f);
+    issue(c + 4, sa1, ss1, sp1, w1);
     compute(w2, f);
   }
   // the last one or two superchunks (stages 0 and 1, issued above)
   if (c < c_hi) {
     sync_stage();
-    read_frags(sa0, ss0, f);
+    read_frags(sa0, ss0, sp0, f);
     compute(w0, f);
     if (c + 1 < c_hi) {
       __builtin_amdgcn_s_waitcnt(kWaitVmem);
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      read_frags(sa1, ss1, f);
+      read_frags(sa1, ss1, sp1, f);
       compute(w1, f);
     }
   }
