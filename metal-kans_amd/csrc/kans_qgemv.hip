@@ -640,9 +640,12 @@ __device__ __forceinline__ Q load_rec(const char* p) {
 // its own row (row block q, row r) and the epilogue applies them to every tile
 // (only tile q's result is kept and stored).  The parameters cost 4 registers
 // per superchunk in flight instead of 16, and one load instruction instead of
-// four.  Lanes whose MFMA row is not a batch row never load their activation
-// fragment (it stays 0); their results only reach accumulator rows that are
-// not stored.  NT: non-temporal weight loads (load_rec).
+// four.  Lanes whose MFMA row is not a batch row load batch row 0's fragment
+// (the same cache line as its own lanes): their results only reach
+// accumulator rows that are not stored, and an unconditional load keeps the
+// loop free of branches (with the load under a branch, the compiler's wait
+// counts merged across it and it drained the ring at every round; it also
+// held ~90 more registers).  NT: non-temporal weight loads (load_rec).
 template <int QT, int SR, int EPI, bool NT>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
@@ -671,7 +674,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 
   const int arow = r & 3;  // batch row of this lane's MFMA row (replicated every 4 rows)
   const bool alive = arow < B;
-  const _Float16* arow_p = Phi + (long)arow * ldphi + 8 * q;
+  const _Float16* arow_p = Phi + (long)(alive ? arow : 0) * ldphi + 8 * q;
 
   typedef QWordOf<QT> QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
@@ -732,20 +735,15 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     // half the size, keeps c+1 .. c+3 (measured on the config-5 block at
     // B = 1: ternary 72.7 -> 70.8 us with four stages, INT4 2 us slower).
     // Loads past the end of the range repeat the last superchunk (an L2 hit,
-    // no extra HBM traffic), so the loop body is branch-free between the exits
-    // and compute(c) waits for exactly the operands of c (vmcnt counts in issue
-    // order).  Cleared once: lanes that never load keep zeros.
+    // no extra HBM traffic), so the loop body is branch-free and compute(c)
+    // waits for exactly the operands of c (vmcnt counts in issue order).
     constexpr int RING = QT == Q_TERN ? 4 : 3;
     Ops o0, o1, o2, o3;
-    __builtin_memset(&o0, 0, sizeof(Ops));
-    __builtin_memset(&o1, 0, sizeof(Ops));
-    __builtin_memset(&o2, 0, sizeof(Ops));
-    if constexpr (RING == 4) __builtin_memset(&o3, 0, sizeof(Ops));
     auto issue = [&](int c, Ops& o) {
       const int cc = min(c, c_hi - 1);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        if (alive) o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
+        o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
       if constexpr (q_affine(QT)) {
 #pragma unroll
         for (int i = 0; i < SR; ++i) o.sg[i] = S[(long)cc * MP + i];
@@ -756,33 +754,59 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
       o.sb = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + lane * 16);
     };
+    // The loop body is whole rounds of RING superchunks with no exit inside,
+    // and the prologue issues its slots in order: with an exit per
+    // superchunk the compiler's wait counts merged across the exits and it
+    // drained the ring (vmcnt(0)) at the top of every round.
+    // Scheduling fences before each issue: one superchunk's loads are issued
+    // together, after the previous superchunk's multiplies, which keeps the
+    // register use of the old loop (three waves per SIMD).
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
     issue(c_lo, o0);
+    fence();
     issue(c_lo + 1, o1);
+    int c = c_lo;
     if constexpr (RING == 3) {
-      for (int c = c_lo; c < c_hi; c += 3) {
+      for (; c + 3 <= c_hi; c += 3) {
+        fence();
         issue(c + 2, o2);
         compute(o0);
-        if (c + 1 >= c_hi) break;
+        fence();
         issue(c + 3, o0);
         compute(o1);
-        if (c + 2 >= c_hi) break;
+        fence();
         issue(c + 4, o1);
         compute(o2);
       }
+      // o0, o1 hold superchunks c, c + 1
+      if (c < c_hi) {
+        compute(o0);
+        if (c + 1 < c_hi) compute(o1);
+      }
     } else {
+      fence();
       issue(c_lo + 2, o2);
-      for (int c = c_lo; c < c_hi; c += 4) {
+      for (; c + 4 <= c_hi; c += 4) {
+        fence();
         issue(c + 3, o3);
         compute(o0);
-        if (c + 1 >= c_hi) break;
+        fence();
         issue(c + 4, o0);
         compute(o1);
-        if (c + 2 >= c_hi) break;
+        fence();
         issue(c + 5, o1);
         compute(o2);
-        if (c + 3 >= c_hi) break;
+        fence();
         issue(c + 6, o2);
         compute(o3);
+      }
+      // o0, o1, o2 hold superchunks c, c + 1, c + 2
+      if (c < c_hi) {
+        compute(o0);
+        if (c + 1 < c_hi) {
+          compute(o1);
+          if (c + 2 < c_hi) compute(o2);
+        }
       }
     }
   }
