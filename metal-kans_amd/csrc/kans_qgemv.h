@@ -14,10 +14,10 @@ constexpr int kQSuper = 128;
 // replicated across the MFMA rows, three- or four-deep register ring); larger ones up to
 // 32 the workgroup GEMV k_qgemv_wg (activations shared through LDS).
 constexpr int kSmallB = 2;
-// Work items (waves) per CU the split-K aims for (measured on the config-5
-// block): small batches INT4 8 (resident: 12), ternary 12 (resident: 12, the
-// four-deep ring's occupancy), INT8 as INT4; the workgroup kernel 10.
-inline int items_per_cu(int quant, int B) { return B <= kSmallB ? (quant == Q_TERN ? 12 : 8) : 10; }
+// Work items (waves) per CU the split-K aims for (swept on the config-5
+// block): small batches 8 for every format (resident: 12; 6, 7, 12 and 16
+// were slower), the workgroup kernel 10 (4 to 18 measured within 1 %).
+inline int items_per_cu(int /*quant*/, int B) { return B <= kSmallB ? 8 : 10; }
 
 // 16-row blocks per decode wave (64 output rows: each activation fragment
 // serves 4 weight tiles, and a wave reads 4 KB of INT4 codes per superchunk).

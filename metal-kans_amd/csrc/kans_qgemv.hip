@@ -729,16 +729,14 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   };
 
   if (c_lo < c_hi) {
-    // Register ring: INT4 keeps superchunks c+1 and c+2 in flight while c is
-    // consumed (~10 KB per wave: the stream needs that much in flight to
-    // cover the HBM latency at full bandwidth); ternary, whose records are
-    // half the size, keeps c+1 .. c+3 (measured on the config-5 block at
-    // B = 1: ternary 72.7 -> 70.8 us with four stages, INT4 2 us slower).
-    // Loads past the end of the range repeat the last superchunk (an L2 hit,
-    // no extra HBM traffic), so the loop body is branch-free and compute(c)
-    // waits for exactly the operands of c (vmcnt counts in issue order).
-    constexpr int RING = QT == Q_TERN ? 4 : 3;
-    Ops o0, o1, o2, o3;
+    // Register ring: superchunks c+1 and c+2 are in flight while c is
+    // consumed (INT4 ~10 KB per wave).  Loads past the end of the range
+    // repeat the last superchunk (an L2 hit, no extra HBM traffic), so the
+    // loop body is branch-free and compute(c) waits for exactly the operands
+    // of c (vmcnt counts in issue order).  A four-deep ring for ternary, whose
+    // records are half the size, measured slower with this loop (cfg5 block
+    // at B = 1: 73.2 against 69.2 us).
+    Ops o0, o1, o2;
     auto issue = [&](int c, Ops& o) {
       const int cc = min(c, c_hi - 1);
 #pragma unroll
@@ -754,60 +752,31 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
       o.sb = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + lane * 16);
     };
-    // The loop body is whole rounds of RING superchunks with no exit inside,
-    // and the prologue issues its slots in order: with an exit per
-    // superchunk the compiler's wait counts merged across the exits and it
-    // drained the ring (vmcnt(0)) at the top of every round.
-    // Scheduling fences before each issue: one superchunk's loads are issued
-    // together, after the previous superchunk's multiplies, which keeps the
-    // register use of the old loop (three waves per SIMD).
+    // The loop body is whole rounds of three superchunks with no exit
+    // inside: with an exit per superchunk the compiler's wait counts merged
+    // across the exits and it drained the ring (vmcnt(0)) at the top of every
+    // round.  Scheduling fences before each issue keep one superchunk's loads
+    // together and the slots in ring order.
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
     issue(c_lo, o0);
     fence();
     issue(c_lo + 1, o1);
     int c = c_lo;
-    if constexpr (RING == 3) {
-      for (; c + 3 <= c_hi; c += 3) {
-        fence();
-        issue(c + 2, o2);
-        compute(o0);
-        fence();
-        issue(c + 3, o0);
-        compute(o1);
-        fence();
-        issue(c + 4, o1);
-        compute(o2);
-      }
-      // o0, o1 hold superchunks c, c + 1
-      if (c < c_hi) {
-        compute(o0);
-        if (c + 1 < c_hi) compute(o1);
-      }
-    } else {
+    for (; c + 3 <= c_hi; c += 3) {
       fence();
-      issue(c_lo + 2, o2);
-      for (; c + 4 <= c_hi; c += 4) {
-        fence();
-        issue(c + 3, o3);
-        compute(o0);
-        fence();
-        issue(c + 4, o0);
-        compute(o1);
-        fence();
-        issue(c + 5, o1);
-        compute(o2);
-        fence();
-        issue(c + 6, o2);
-        compute(o3);
-      }
-      // o0, o1, o2 hold superchunks c, c + 1, c + 2
-      if (c < c_hi) {
-        compute(o0);
-        if (c + 1 < c_hi) {
-          compute(o1);
-          if (c + 2 < c_hi) compute(o2);
-        }
-      }
+      issue(c + 2, o2);
+      compute(o0);
+      fence();
+      issue(c + 3, o0);
+      compute(o1);
+      fence();
+      issue(c + 4, o1);
+      compute(o2);
+    }
+    // o0, o1 hold superchunks c, c + 1
+    if (c < c_hi) {
+      compute(o0);
+      if (c + 1 < c_hi) compute(o1);
     }
   }
 
