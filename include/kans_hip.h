@@ -326,6 +326,11 @@ long long kans_gated_stream_bytes(const kans_gated* block, int B);
  * identical results.  Returns the previous setting (no reference counterpart: a tuning and test
  * switch). */
 int kans_gated_set_fused_swiglu(int on);
+/* At B <= 2 with the fused SwiGLU epilogue, the gate|up GEMV computes the basis of x itself, each
+ * wave for its own range of the reduction axis in LDS (on = 1, the default: 3 launches per block);
+ * on = 0 runs the separate basis kernel first.  Both give identical results.  Returns the previous
+ * setting (no reference counterpart: a tuning and test switch). */
+int kans_decode_set_pre_basis(int on);
 /* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
  * non-temporal.  Automatic uses non-temporal loads when a call's packed weights exceed the 256 MB
  * MALL (they cannot stay cached between calls), plain loads otherwise (a smaller block hits the

@@ -97,7 +97,17 @@ struct QGemv {
   int N_total;
   int nt = 0;      // non-temporal weight-record loads (see load_rec)
   QEpi epi;        // k_qgemv (B <= kSmallB) only
+  // In-kernel activation basis (k_qgemv only, qgemv_pre_fits): with X set,
+  // every wave computes Phi / S of its own superchunk range from the layer
+  // input X into LDS, as k_prep would, and Phi / S are not read.
+  const void* X = nullptr;
+  int x_dtype = 0;
+  long ldx = 0;
+  int D_in = 0, K = 0, has_base = 0, Cb = 0;
 };
+
+// Whether the in-kernel basis fits LDS for this launch shape.
+bool qgemv_pre_fits(int qt, int B, int C_tot, int ksplit, int epi_kind);
 
 // Re-tile a packed matrix (C superchunks starting at superchunk c_off) into the records R.
 hipError_t qtile_int4(const unsigned char* qw, const float* scales, const float* biases, int D_out, long rowbytes,

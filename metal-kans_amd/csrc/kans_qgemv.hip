@@ -628,6 +628,58 @@ __device__ __forceinline__ Q load_rec(const char* p) {
   }
 }
 
+// In-kernel activation basis of k_qgemv (PRE): the layer input and the basis
+// geometry, and each wave's LDS slice: Phi rows [SR][span * 128] (fp16, in the
+// weight format's unpack order) then the group sums [span][SR] (INT4 / INT8).
+struct QPreDev {
+  const void* X;
+  int x_dtype;
+  long ldx;
+  int D_in, K, has_base, Cb;
+  int span;   // superchunks per slice, >= every wave's range
+  int slice;  // bytes of LDS per wave (also holds the SwiGLU epilogue's stage)
+};
+constexpr int kPreBatch = 16;           // input loads in flight per lane
+constexpr int kPreVec = 8;              // 16-byte input loads in flight per lane (base segment)
+constexpr int kPreLdsMax = 80 * 1024;   // dynamic LDS per workgroup (two per CU)
+
+// One batch of layer inputs, x[m][min(fb + lane + 64 it, f1 - 1)] for
+// it < kPreBatch, as raw bits (4- or 2-byte loads under one uniform branch):
+// no value is used before the batch's last load is issued, so the loads stay
+// in flight together (converted in the branch, each load was waited for in
+// turn).  x_of_raw converts as load_any does (all three conversions exact).
+__device__ __forceinline__ void load_x_raw(unsigned (&xr)[kPreBatch], const QPreDev& P, int m, int fb, int f1,
+                                           int lane) {
+  // a uniform row pointer and 32-bit lane offsets: one VGPR per address
+  const int es = P.x_dtype == DT_F32 ? 4 : 2;
+  const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
+  if (es == 4) {
+#pragma unroll
+    for (int it = 0; it < kPreBatch; ++it)
+      xr[it] = *reinterpret_cast<const unsigned*>(row + 4u * (unsigned)min(fb + lane + 64 * it, f1 - 1));
+  } else {
+#pragma unroll
+    for (int it = 0; it < kPreBatch; ++it)
+      xr[it] = *reinterpret_cast<const unsigned short*>(row + 2u * (unsigned)min(fb + lane + 64 * it, f1 - 1));
+  }
+}
+__device__ __forceinline__ float x_of_raw(unsigned r, int dt) {
+  if (dt == DT_F32) return __uint_as_float(r);
+  if (dt == DT_F16) return (float)__builtin_bit_cast(_Float16, (unsigned short)r);
+  return __uint_as_float(r << 16);  // bf16
+}
+
+// LDS / Phi position of reduction index rp within its 8-block: the inverse of
+// unpack_order.
+template <int QT>
+__device__ __forceinline__ int unpack_pos(int rp) {
+  if constexpr (QT == Q_INT4) {
+    const int u = rp & 7;
+    return (rp & ~7) | (u < 4 ? 2 * u : 2 * (u - 4) + 1);
+  }
+  return rp;
+}
+
 // Small-batch decode GEMV (B = SR <= kSmallB).  One wave = kQNW row blocks
 // (64 output rows) x one contiguous superchunk range (split-K over waves for
 // memory-level parallelism); 4 independent waves per workgroup.
@@ -646,11 +698,18 @@ __device__ __forceinline__ Q load_rec(const char* p) {
 // loop free of branches (with the load under a branch, the compiler's wait
 // counts merged across it and it drained the ring at every round; it also
 // held ~90 more registers).  NT: non-temporal weight loads (load_rec).
-template <int QT, int SR, int EPI, bool NT>
+//
+// PRE: the wave computes Phi / S of its own superchunk range from the layer
+// input into its LDS slice first (QPreDev), with the values, rounding and sum
+// order of k_prep, so the results equal the k_prep path bit for bit.  The
+// input loads of the first batch are issued before the ring's first weight
+// loads, so they return first; the weights stream while the basis is
+// computed, and the k_prep launch and its wait disappear.
+template <int QT, int SR, int EPI, bool NT, bool PRE>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
                                                const float2* __restrict__ S, int B, int MP,
-                                               float* __restrict__ part, int N_total, QEpi E) {
+                                               float* __restrict__ part, int N_total, QEpi E, QPreDev P) {
   static_assert(SR >= 1 && SR <= kSmallB, "small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
@@ -675,6 +734,13 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   const int arow = r & 3;  // batch row of this lane's MFMA row (replicated every 4 rows)
   const bool alive = arow < B;
   const _Float16* arow_p = Phi + (long)(alive ? arow : 0) * ldphi + 8 * q;
+  // PRE: this wave's LDS slice
+  extern __shared__ __attribute__((aligned(16))) char qg_dyn[];
+  char* const myl = qg_dyn + (threadIdx.x >> 6) * P.slice;
+  _Float16* const phl = reinterpret_cast<_Float16*>(myl);
+  float2* const sl = reinterpret_cast<float2*>(myl + P.span * SR * 256);
+  const int lrow = P.span * 128;
+  const _Float16* const arow_l = phl + (alive ? arow : 0) * lrow + 8 * q;
 
   typedef QWordOf<QT> QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
@@ -737,20 +803,39 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     // records are half the size, measured slower with this loop (cfg5 block
     // at B = 1: 73.2 against 69.2 us).
     Ops o0, o1, o2;
-    auto issue = [&](int c, Ops& o) {
+    // activation fragments and group sums of superchunk c: from Phi / S, or
+    // (PRE) from the wave's LDS slice
+    auto issue_a = [&](int c, Ops& o) {
       const int cc = min(c, c_hi - 1);
+      if constexpr (PRE) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
-      if constexpr (q_affine(QT)) {
+        for (int t = 0; t < 4; ++t)
+          o.a[t] = *reinterpret_cast<const half8v*>(arow_l + (cc - c_lo) * 128 + 32 * t);
+        if constexpr (q_affine(QT)) {
 #pragma unroll
-        for (int i = 0; i < SR; ++i) o.sg[i] = S[(long)cc * MP + i];
+          for (int i = 0; i < SR; ++i) o.sg[i] = sl[(cc - c_lo) * SR + i];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          o.a[t] = *reinterpret_cast<const half8v*>(arow_p + (long)cc * 128 + 32 * t);
+        if constexpr (q_affine(QT)) {
+#pragma unroll
+          for (int i = 0; i < SR; ++i) o.sg[i] = S[(long)cc * MP + i];
+        }
       }
+    };
+    auto issue_w = [&](int c, Ops& o) {
+      const int cc = min(c, c_hi - 1);
       const char* rec = rbase + (long)cc * qrec_bytes(QT);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
         o.qw[w] = load_rec<NT, QWord>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QWord));
       o.sb = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + lane * 16);
+    };
+    auto issue = [&](int c, Ops& o) {
+      issue_a(c, o);
+      issue_w(c, o);
     };
     // The loop body is whole rounds of three superchunks with no exit
     // inside: with an exit per superchunk the compiler's wait counts merged
@@ -758,9 +843,164 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     // round.  Scheduling fences before each issue keep one superchunk's loads
     // together and the slots in ring order.
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
-    issue(c_lo, o0);
-    fence();
-    issue(c_lo + 1, o1);
+    if constexpr (PRE) {
+      bool started = false;
+      // the ring's first weight loads, issued once, right after the first
+      // batch of input loads
+      auto kick = [&] {
+        if (started) return;
+        started = true;
+        fence();
+        issue_w(c_lo, o0);
+        fence();
+        issue_w(c_lo + 1, o1);
+        fence();
+      };
+      const long P_lo = (long)c_lo * 128, P_hi = (long)c_hi * 128;
+      const int nblk = (c_hi - c_lo) * 16;
+      // zero the slice: indices past the segments' values read 0
+#pragma unroll
+      for (int m = 0; m < SR; ++m)
+        for (int i = lane; i < nblk; i += 64)
+          reinterpret_cast<uint4*>(phl + m * lrow)[i] = make_uint4(0u, 0u, 0u, 0u);
+      // basis segment: T_k(clamp(x_i)) at index i K + k (k_prep / cheb_k)
+      const long Pb_end = min(P_hi, min((long)P.Cb * 128, (long)P.D_in * P.K));
+      if (P_lo < Pb_end) {
+        const int f0 = (int)(P_lo / P.K), f1 = (int)((Pb_end - 1) / P.K) + 1;
+        for (int m = 0; m < SR; ++m)
+          for (int fb = f0; fb < f1; fb += 64 * kPreBatch) {
+            unsigned xr[kPreBatch];
+            load_x_raw(xr, P, m, fb, f1, lane);
+            kick();
+#pragma unroll
+            for (int it = 0; it < kPreBatch; ++it) {
+              const int f = fb + lane + 64 * it;
+              if (f < f1) {
+                const float t = fminf(fmaxf(x_of_raw(xr[it], P.x_dtype), -1.0f), 1.0f);
+                float a = 1.0f, b = t;
+                for (int k = 0; k < P.K; ++k) {
+                  float v = k == 0 ? a : b;
+                  if (k >= 2) {
+                    const float cn = __builtin_fmaf(2.0f * t, b, -a);
+                    a = b;
+                    b = cn;
+                    v = cn;
+                  }
+                  const long j = (long)f * P.K + k;
+                  if (j >= P_lo && j < Pb_end) phl[m * lrow + unpack_pos<QT>((int)(j - P_lo))] = half_of(v);
+                }
+              }
+            }
+          }
+      }
+      // base segment: SiLU(x_i) at index Cb * 128 + i
+      if (P.has_base) {
+        const long w0 = (long)P.Cb * 128;
+        const long Pw0 = max(P_lo, w0), Pw1 = min(P_hi, w0 + P.D_in);
+        const int es = P.x_dtype == DT_F32 ? 4 : 2;
+        // 16-byte loads of 8 consecutive inputs when the rows allow them:
+        // one 8-block per load, so a whole base range is one batch
+        const bool vec = (P.D_in & 7) == 0 &&
+                         ((reinterpret_cast<unsigned long>(P.X) | (unsigned long)(P.ldx * es)) & 15) == 0;
+        if (Pw0 < Pw1 && vec) {
+          const int ch0 = (int)(Pw0 - w0) / 8, ch1 = (int)(Pw1 - w0) / 8;  // 8-input chunks
+          for (int m = 0; m < SR; ++m) {
+            const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
+            for (int cb = ch0; cb < ch1; cb += 64 * kPreVec) {
+              uint4 xr[kPreVec];  // es = 2: one chunk each; es = 4: half a chunk each
+              if (es == 2) {
+#pragma unroll
+                for (int it = 0; it < kPreVec; ++it)
+                  xr[it] = *reinterpret_cast<const uint4*>(row + 16u * (unsigned)min(cb + lane + 64 * it, ch1 - 1));
+              } else {
+#pragma unroll
+                for (int it = 0; it < kPreVec; ++it)
+                  xr[it] = *reinterpret_cast<const uint4*>(
+                      row + 32u * (unsigned)min(cb + lane + 64 * (it >> 1), ch1 - 1) + 16u * (unsigned)(it & 1));
+              }
+              kick();
+              // chunk `it` of this lane: SiLU of its 8 inputs into one 8-block
+              auto put = [&](int it, const float (&v)[8]) {
+                const int ch = cb + lane + 64 * it;
+                if (ch < ch1) {
+                  _Float16 hv[8];
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) hv[e] = half_of(silu_f32(v[unpack_order<QT>(e)]));
+                  *reinterpret_cast<uint4*>(phl + m * lrow + (w0 + 8L * ch - P_lo)) = *reinterpret_cast<uint4*>(hv);
+                }
+              };
+              if (es == 2) {
+#pragma unroll
+                for (int it = 0; it < kPreVec; ++it) {
+                  const unsigned* w = reinterpret_cast<const unsigned*>(&xr[it]);
+                  float v[8];
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) v[e] = x_of_raw((w[e >> 1] >> (16 * (e & 1))) & 0xffffu, P.x_dtype);
+                  put(it, v);
+                }
+              } else {
+#pragma unroll
+                for (int it = 0; it < kPreVec / 2; ++it) {
+                  const unsigned* w0p = reinterpret_cast<const unsigned*>(&xr[2 * it]);
+                  const unsigned* w1p = reinterpret_cast<const unsigned*>(&xr[2 * it + 1]);
+                  float v[8];
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    v[e] = __uint_as_float(w0p[e]);
+                    v[4 + e] = __uint_as_float(w1p[e]);
+                  }
+                  put(it, v);
+                }
+              }
+            }
+          }
+        } else if (Pw0 < Pw1) {
+          const int f0 = (int)(Pw0 - w0), f1 = (int)(Pw1 - w0);
+          for (int m = 0; m < SR; ++m)
+            for (int fb = f0; fb < f1; fb += 64 * kPreBatch) {
+              unsigned xr[kPreBatch];
+              load_x_raw(xr, P, m, fb, f1, lane);
+              kick();
+#pragma unroll
+              for (int it = 0; it < kPreBatch; ++it) {
+                const int f = fb + lane + 64 * it;
+                if (f < f1)
+                  phl[m * lrow + unpack_pos<QT>((int)(w0 + f - P_lo))] = half_of(silu_f32(x_of_raw(xr[it], P.x_dtype)));
+              }
+            }
+        }
+      }
+      kick();
+      asm volatile("" ::: "memory");  // LDS writes before the reads below (one wave, in order)
+      // group sums as k_prep: each 8-block's fp16 values in order, then the
+      // 8-block sums of a 64-group by xor steps 1, 2, 4 over its 8 lanes
+      if constexpr (q_affine(QT)) {
+#pragma unroll
+        for (int m = 0; m < SR; ++m)
+          for (int b0 = 0; b0 < nblk; b0 += 64) {
+            const int blk = b0 + lane;
+            const bool live = blk < nblk;
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (live) u = reinterpret_cast<const uint4*>(phl + m * lrow)[blk];
+            const _Float16* hv = reinterpret_cast<const _Float16*>(&u);
+            float sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += (float)hv[e];
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            sum += __shfl_xor(sum, 4);
+            const float other = __shfl_xor(sum, 8);
+            if (live && (lane & 15) == 0) sl[(blk >> 4) * SR + m] = make_float2(sum, other);
+          }
+        asm volatile("" ::: "memory");
+      }
+      issue_a(c_lo, o0);
+      issue_a(c_lo + 1, o1);
+    } else {
+      issue(c_lo, o0);
+      fence();
+      issue(c_lo + 1, o1);
+    }
     int c = c_lo;
     for (; c + 3 <= c_hi; c += 3) {
       fence();
@@ -795,9 +1035,15 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     }
   }
   if constexpr (EPI == QEPI_SWIGLU) {
-    __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
+    _Float16* stg;
+    if constexpr (PRE) {
+      stg = phl;  // the slice is free again
+    } else {
+      __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
+      stg = stage[threadIdx.x >> 6];
+    }
     if (!last_arrival(E.counters + rg_loc * kCntStride, 2 * ksplit, lane)) return;
-    epi_swiglu<QT, true>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stage[threadIdx.x >> 6], lane, 0, B);
+    epi_swiglu<QT, true>(E, part, ksplit, B, MP, m0.D_out, rg_loc, rg_split, stg, lane, 0, B);
   }
 }
 
@@ -1211,6 +1457,27 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Bytes of one wave's LDS slice for the in-kernel basis (QPreDev).
+static int pre_slice_bytes(int qt, int B, int span, int epi_kind) {
+  int b = span * B * 256 + (q_affine(qt) ? span * B * 8 : 0);
+  if (epi_kind == QEPI_SWIGLU) b = std::max(b, 64 * (kMaxK + 1) * 2);
+  return (b + 15) & ~15;
+}
+
+bool qgemv_pre_fits(int qt, int B, int C_tot, int ksplit, int epi_kind) {
+  static int lds_max = -1;  // per-workgroup LDS limit of the device
+  if (lds_max < 0) {
+    int dev = 0, v = 0;
+    lds_max = hipGetDevice(&dev) == hipSuccess &&
+                      hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess
+                  ? v
+                  : 0;
+  }
+  if (B < 1 || B > kSmallB || ksplit < 1) return false;
+  const int span = (C_tot + ksplit - 1) / ksplit;
+  return 4 * pre_slice_bytes(qt, B, span, epi_kind) <= std::min(kPreLdsMax, lds_max);
+}
+
 // Launch of the decode GEMV kernel for G (arguments checked by qgemv).
 template <bool NT>
 static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
@@ -1218,9 +1485,22 @@ static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
   QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
   dim3 grid((unsigned)((items + 3) / 4));
-#define KQ_GEMV(QTV, SR, EP)                                                                                 \
-  hipLaunchKernelGGL((k_qgemv<QTV, SR, EP, NT>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg, G.ksplit,    \
-                     G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi)
+  QPreDev P{G.X, G.x_dtype, G.ldx, G.D_in, G.K, G.has_base, G.Cb, 0, 0};
+  const bool pre = G.X != nullptr;
+  if (pre) {
+    P.span = (G.C_tot + G.ksplit - 1) / G.ksplit;
+    P.slice = pre_slice_bytes(qt, G.B, P.span, G.epi.kind);
+  }
+  const size_t dyn = pre ? (size_t)4 * P.slice : 0;
+#define KQ_GEMV(QTV, SR, EP)                                                                                      \
+  do {                                                                                                           \
+    if (pre)                                                                                                     \
+      hipLaunchKernelGGL((k_qgemv<QTV, SR, EP, NT, true>), grid, dim3(256), dyn, st, a, b, G.rg_split, G.n_rg,    \
+                         G.ksplit, G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi, P);                 \
+    else                                                                                                         \
+      hipLaunchKernelGGL((k_qgemv<QTV, SR, EP, NT, false>), grid, dim3(256), 0, st, a, b, G.rg_split, G.n_rg,     \
+                         G.ksplit, G.C_tot, G.Phi, G.S, G.B, G.MP, G.part, G.N_total, G.epi, P);                 \
+  } while (0)
   const int mt = G.MP / 16;
   const bool small = G.B <= kSmallB;
   const int ep = G.epi.kind;
@@ -1261,6 +1541,8 @@ hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   const bool small = G.B <= kSmallB;
   const int ep = G.epi.kind;
   if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
+    return hipErrorInvalidValue;
+  if (G.X && (!qgemv_pre_fits(qt, G.B, G.C_tot, G.ksplit, ep) || G.K < 1 || G.D_in < 1 || G.ldx < G.D_in))
     return hipErrorInvalidValue;
   if (!small && G.MP > 32) return hipErrorInvalidValue;
   if (G.nt) qgemv_launch<true>(qt, G, st);

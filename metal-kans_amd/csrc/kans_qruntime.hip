@@ -58,6 +58,8 @@ constexpr int kMaxDecodeB = 32;
 // GEMV's epilogue (QEPI_SWIGLU) at B <= 2, k_swiglu_basis above -- instead of
 // k_qswiglu + k_prep.
 bool g_fused_swiglu = true;
+// In-kernel basis of x in the B <= 2 gate|up GEMV (kans_decode_set_pre_basis).
+bool g_pre_basis = true;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
 
@@ -255,8 +257,18 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, _Fl
 // GEMV of layer a (and b, sharing a's activations phi / S): split-K partial sums
 // in part ([ksplit][B][a.D_out + b.D_out]), then the epilogue `epi`.
 int gemv_locked(kans_qlayer* a, kans_qlayer* b, int B, int ksplit, const QEpi& epi, int nt, const _Float16* phi,
-                const float2* S, float* part, hipStream_t st) {
+                const float2* S, float* part, hipStream_t st, const void* X = nullptr, int x_dtype = 0,
+                long ldx = 0) {
   QGemv G;
+  if (X) {  // in-kernel basis of a's input (qgemv_pre_fits checked by the caller)
+    G.X = X;
+    G.x_dtype = x_dtype;
+    G.ldx = ldx;
+    G.D_in = a->D_in;
+    G.K = a->K;
+    G.has_base = a->has_base;
+    G.Cb = a->Cb;
+  }
   G.rec0 = a->R.p;
   G.D_out0 = a->D_out;
   G.rec1 = b ? b->R.p : nullptr;
@@ -460,8 +472,29 @@ int gated_decode(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, i
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
   const int h = g->D_out;
   int rc;
-  if ((rc = prep_locked(g, X, x_dtype, ldx, B, ws.phi, ws.s, st))) return rc;
   const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d));
+  // B <= 2 with the fused epilogue: the gate|up GEMV computes the basis of x
+  // itself (no k_prep launch) when its LDS slices fit
+  if (g_fused_swiglu && g_pre_basis && B <= kSmallB && ks1 <= kMaxEpiSplit &&
+      qgemv_pre_fits(g->quant, B, g->C_tot, ks1, QEPI_SWIGLU)) {
+    QEpi e1;
+    e1.kind = QEPI_SWIGLU;
+    e1.counters = ws.cnt;
+    e1.bias = g->has_bias ? g->bias.p : nullptr;
+    e1.bias_dtype = g->bias_dtype;
+    e1.bias_u = u->has_bias ? u->bias.p : nullptr;
+    e1.bias_u_dtype = u->bias_dtype;
+    e1.round16 = round16;
+    e1.K2 = d->K;
+    e1.has_base2 = d->has_base;
+    e1.Cb2 = d->Cb;
+    e1.C_tot2 = d->C_tot;
+    e1.Phi2 = ws.phi2;
+    e1.S2 = ws.s2;
+    if ((rc = gemv_locked(g, u, B, ks1, e1, nt, nullptr, nullptr, ws.part, st, X, x_dtype, ldx))) return rc;
+    return gemv_reduce_locked(d, B, ks2, Y, y_dtype, ldy, nt, ws.phi2, ws.s2, ws.part2, st);
+  }
+  if ((rc = prep_locked(g, X, x_dtype, ldx, B, ws.phi, ws.s, st))) return rc;
   if (g_fused_swiglu) {
     // SwiGLU(gate, up) straight into the down layer's basis: in the gate|up
     // GEMV's epilogue at B <= 2, by k_swiglu_basis after it otherwise
@@ -790,6 +823,13 @@ int kans_gated_set_fused_swiglu(int on) {
   std::lock_guard<std::mutex> lk(kans_mutex());
   const int prev = g_fused_swiglu ? 1 : 0;
   g_fused_swiglu = on != 0;
+  return prev;
+}
+
+int kans_decode_set_pre_basis(int on) {
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  const int prev = g_pre_basis ? 1 : 0;
+  g_pre_basis = on != 0;
   return prev;
 }
 

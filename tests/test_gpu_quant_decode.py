@@ -313,6 +313,50 @@ def test_gated_fused_epilogue_matches_unfused(gpu, fmt, cfg):
             lib.kans_qlayer_destroy(h)
 
 
+PRE_CFGS = [  # d, h, K and base branch of gate / up
+    (96, 200, 1, True), (100, 70, 5, False), (130, 64, 32, True), (2048, 256, 4, True), (33, 17, 3, True)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("cfg", PRE_CFGS, ids=lambda c: "d{}h{}K{}b{}".format(*c[:3], int(c[3])))
+def test_gated_pre_basis_matches_kprep(gpu, fmt, cfg):
+    """At B <= 2 the gate|up GEMV computes the basis of x itself, each wave for its own superchunk
+    range in LDS (kans_decode_set_pre_basis(1), the default).  It must equal the separate basis
+    kernel (k_prep) bit for bit, for every input dtype, with and without the base branch, K = 1 to
+    32 (a feature's basis values split across two waves' ranges), and on a repeated call."""
+    lib = gpu
+    d, hdim, K, base = cfg
+    layers = []
+    for i, (di, do, k, b) in enumerate(((d, hdim, K, base), (d, hdim, K, base), (hdim, d, 4, True))):
+        layers.append(make_qlayer(lib, fmt, di, do, k, b, True, seed=400 + i)[0])
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_create(*layers, ctypes.byref(blk)) == 0, lib.kans_last_error()
+    try:
+        for B in (1, 2):
+            x32 = np.random.default_rng(B + d + K).normal(0, 1, (B, d)).astype(np.float32)
+            x32[0, :3] = (1.5, -1.5, 0.0)  # clamped and zero inputs
+            xs = {DT_F32: x32, DT_F16: x32.astype(np.float16),
+                  DT_BF16: (x32.view(np.uint32) >> 16).astype(np.uint16)}
+            for xdt, x in xs.items():
+                outs = []
+                for pre in (1, 0, 1):
+                    prev = lib.kans_decode_set_pre_basis(pre)
+                    try:
+                        y = np.full((B, d), np.nan, np.float32)
+                        assert lib.kans_gated_forward_host(blk, x.ctypes.data, xdt, y.ctypes.data, DT_F32, B, 0) == 0, \
+                            lib.kans_last_error()
+                    finally:
+                        lib.kans_decode_set_pre_basis(prev)
+                    outs.append(y)
+                assert np.isfinite(outs[0]).all()
+                assert np.array_equal(outs[0], outs[1]), (B, xdt, float(np.max(np.abs(outs[0] - outs[1]))))
+                assert np.array_equal(outs[0], outs[2])
+    finally:
+        lib.kans_gated_destroy(blk)
+        for h in layers:
+            lib.kans_qlayer_destroy(h)
+
+
 @pytest.mark.parametrize("quant", FMTS)
 def test_gatedkan_python_decode(gpu, quant):
     """GatedKAN(dtype=float16).to_int8() / .to_int4() / .to_ternary() takes the fused block for B <= 32."""
