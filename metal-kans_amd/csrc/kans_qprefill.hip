@@ -486,12 +486,15 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
         }
       }
       nxt[(SC * kQNB + wave) * 64 + lane] = d;
-      // issue order: per column block one MFMA, a share of the VALU work, the
-      // next slot's B-fragment read; the decoded chunk's LDS write last
+      // issue order: per column block one MFMA, a share of the VALU work (up to
+      // 8 instructions: a slot has ~60, so all of them sit between MFMAs; 4 left
+      // some after the last MFMA, 0.8 % slower for INT4 / INT8, 6 was slower,
+      // 10 no faster), the next slot's B-fragment read; the decoded chunk's LDS
+      // write last
 #pragma unroll
       for (int nb = 0; nb < kQNB; ++nb) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
         if constexpr (SC + 1 < KP) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
