@@ -353,6 +353,29 @@ def _create_qlayer(lib, fmt, shape, K, arrs):
     return h
 
 
+def _dense_dequant_block(lib, packed, shapes, K):
+    """Dense fp16 GatedKAN block (kan_fused_block) on INT4 weights dequantized by the library's own
+    metal_kan_dequantize_int4 (fp32, then rounded to fp16 on upload): the same weight values the fused INT4
+    prefill feeds its MFMAs, moved as 2 bytes per weight."""
+    layers = []
+    for (d_out, d_in), arrs in zip(shapes, packed):
+        q, s_, b_, qb, sb, bb = arrs
+        W = np.empty((d_out, d_in * K), np.float32)
+        Wb = np.empty((d_out, d_in), np.float32)
+        assert lib.metal_kan_dequantize_int4(q.ctypes.data, s_.ctypes.data, b_.ctypes.data, W.ctypes.data,
+                                             s_.size, 64) == 0, lib.kans_last_error()
+        assert lib.metal_kan_dequantize_int4(qb.ctypes.data, sb.ctypes.data, bb.ctypes.data, Wb.ctypes.data,
+                                             sb.size, 64) == 0, lib.kans_last_error()
+        h = ctypes.c_void_p()
+        assert lib.kans_layer_create(0, 1, d_in, d_out, K, 1, 0, ctypes.byref(h)) == 0, lib.kans_last_error()
+        assert lib.kans_layer_load_weights_f32(h, W.ctypes.data, Wb.ctypes.data, None) == 0, lib.kans_last_error()
+        layers.append(h)
+        del W, Wb
+    blk = ctypes.c_void_p()
+    assert lib.kans_gated_dense_create(*layers, ctypes.byref(blk)) == 0, lib.kans_last_error()
+    return blk, layers
+
+
 # Weight copies the decode lines rotate over: each call's weights were last read COPIES - 1 calls earlier,
 # so even the ternary block (254 MB, within the 256 MB MALL) streams from HBM, as in a model whose layers
 # together exceed the MALL.
@@ -439,6 +462,24 @@ def run_cfg5(lib, warmup, iters):
             lib.kans_gated_destroy(b)
         for hnd in layers:
             lib.kans_qlayer_destroy(hnd)
+        if fmt == "int4":
+            # reference point measured in the same run: the dense fp16 kernel on the dequantized weights
+            dblk, dlayers = _dense_dequant_block(lib, packed, [Wb.shape for (W, Wb) in mats], K)
+            x, B = xs[8192], 8192
+            y = np.empty_like(x)
+            assert lib.kans_gated_dense_forward_host(dblk, x.ctypes.data, 1, y.ctypes.data, B) == 0
+            ms = ctypes.c_float()
+            it = max(5, iters // 10)
+            assert lib.kans_gated_dense_time(dblk, B, min(warmup, it), it, 0, ctypes.byref(ms)) == 0, \
+                lib.kans_last_error()
+            out["cfg5_int4_dequant_fp16_prefill_b8192"] = {
+                "ms": round(ms.value, 4), "tflops": round(prefill_flops / ms.value / 1e9, 2),
+                "frac_mfma_peak": round(prefill_flops / ms.value / 1e9 / PEAK["f16"], 4), "batch": B,
+                "path": "reference point: dense fp16 GatedKAN (kan_fused_block) on the INT4 weights dequantized "
+                        "by metal_kan_dequantize_int4 and rounded to fp16 (2 bytes per weight), same run"}
+            lib.kans_gated_dense_destroy(dblk)
+            for hnd in dlayers:
+                lib.kans_layer_destroy(hnd)
     log(f"[bench] cfg5 ({time.perf_counter() - t0:.1f} s): {out}")
     return out
 
