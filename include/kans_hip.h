@@ -181,6 +181,11 @@ int kans_layer_set_rbf(kans_layer* layer, const float* centers, float inv_denomi
 int kans_layer_set_bspline(kans_layer* layer, int grid_size, float grid_min, float inv_h);
 /* tiling override for tuning: (wm, nb) in {(64,4),(32,8),(32,4),(32,1)} or (0,0) = automatic; splits >= 0 */
 int kans_layer_set_tiling(kans_layer* layer, int wm, int nb, int splits);
+/* wave groups per workgroup of the 4-wave fp16/bf16 Chebyshev block kernel, for tuning: 0 = automatic
+   (small layers that leave at most one workgroup per CU), 1, 2 or 4 (2 on tiles (32,1) and (32,4), 4 on
+   (32,1); elsewhere 1).  The groups split a tile's feature blocks and add their partial sums in a fixed
+   order through LDS.  No reference counterpart (the reference has no tiling). */
+int kans_layer_set_wave_groups(kans_layer* layer, int groups);
 int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
 /* name of the fused kernel (and its tile) that a forward of batch B runs, NUL-terminated in name[len] */
 int kans_layer_kernel(const kans_layer* layer, int B, char* name, int len);

@@ -19,6 +19,7 @@ struct DenseLaunch {
   int B, D_in, D_out, nfb;
   BasisParams bp;
   int wm, nb, splits;   // tile config
+  int ks = 1;           // wave groups per workgroup (4-wave block kernel, block_wave_groups_ok)
 };
 
 }  // namespace kans

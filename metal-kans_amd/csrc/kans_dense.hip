@@ -21,7 +21,9 @@
 //   * fp16 / bf16 use v_mfma_f32_32x32x16_{f16,bf16}; fp32 uses
 //     v_mfma_f32_32x32x2_f32 eight times per step.  Accumulation is fp32.
 //   * an optional split over feature blocks writes fp32 partials that a finalize
-//     kernel reduces (used when the output tile count alone cannot fill the GPU).
+//     kernel reduces (used when the output tile count alone cannot fill the GPU);
+//     the 4-wave block kernel can also split a tile's feature blocks over KS
+//     wave groups of one workgroup, reduced through LDS (no finalize kernel).
 //
 // Two kernels share this decomposition:
 //   kan_fused_block  fp16/bf16: Chebyshev with K+base <= 10 (4 waves), RBF and
@@ -319,6 +321,16 @@ kan_fused_dense(const TX* __restrict__ X, long ldx,
 // 160 KB LDS (9 slots for the RBF and B-spline table kernels, whose lookup
 // tables also live in LDS).
 //
+// KS > 1 (4-wave Chebyshev tiles, small problems): the workgroup holds KS wave
+// groups of WAVES waves on the same output tile.  Group g takes its own
+// contiguous run of the split's feature blocks with its own two LDS stages;
+// all groups run the same number of rounds (a group past its run only joins
+// the barrier), so the block barrier stays workgroup-wide.  At the end groups
+// 1 .. KS-1 write their accumulators into the then idle stages and group 0
+// adds them in group order and writes the tile.  With one workgroup per CU
+// this gives 4·KS waves per CU instead of 4 and a KS times shorter chain of
+// feature blocks per wave, for layers too small to fill the GPU.
+//
 // Requires KP = K + has_base <= block_slots(WAVES, BASIS) (the launcher checks).
 // ---------------------------------------------------------------------------
 // emit<KN> of a table generator (BsplineTab) into the A-fragments a
@@ -348,8 +360,13 @@ constexpr int kValuPerMfma =
          NV + NV / 2 +
      MFMAS - 1) / MFMAS;
 
-template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64, WAVES == 4 ? 2 : 1)
+// Workgroups per CU the block kernel is compiled for (register budget).
+__host__ __device__ constexpr int block_min_wgs(int waves, int nb, int ks) {
+  return waves == 4 && (ks == 1 || (ks == 2 && nb == 1)) ? 2 : 1;
+}
+
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES, int KS = 1>
+__global__ void __launch_bounds__(WAVES * 64 * KS, block_min_wgs(WAVES, NB, KS))
 kan_fused_block(const TX* __restrict__ X, long ldx,
                 const uint4* __restrict__ Wt, int nob_pad,
                 const T* __restrict__ bias,
@@ -364,15 +381,19 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   typedef typename Mfma<T>::frag frag;
 
   constexpr int SLOTS = block_slots(WAVES, BASIS);
-  __shared__ uint4 stage0[SLOTS * SLOT];
-  __shared__ uint4 stage1[SLOTS * SLOT];
+  static_assert(KS == 1 || (WAVES == 4 && (BASIS == BASIS_CHEBY || BASIS == BASIS_CHEBY_POST)),
+                "wave groups: 4-wave Chebyshev tiles only");
+  __shared__ uint4 stage0[KS * SLOTS * SLOT];
+  __shared__ uint4 stage1[KS * SLOTS * SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // wave index as a scalar: the compiler cannot see that tid >> 6 is uniform
   // per wave, and would otherwise keep wave-derived loop counters and
   // addresses in vector registers
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = KS > 1 ? wave_wg / WAVES : 0;  // wave group
+  const int wave = KS > 1 ? wave_wg - grp * WAVES : wave_wg;
   int m_tile, n_tile;
   tile_of(xcd_remap(blockIdx.x, m_tiles * n_tiles), m_tiles, n_tiles, m_tile, n_tile);
   const int split = blockIdx.y;
@@ -383,6 +404,12 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   const int fb_end = min(nfb_total, fb_begin + fb_per_split);
   const int KP = bp.K + has_base;
   if (fb_end <= fb_begin) return;  // uniform per workgroup (empty split)
+  // this wave group's feature blocks [gb, ge), `rounds` block rounds for every group
+  const int rounds = KS > 1 ? (fb_end - fb_begin + KS - 1) / KS : fb_end - fb_begin;
+  const int gb = KS > 1 ? min(fb_end, fb_begin + grp * rounds) : fb_begin;
+  const int ge = KS > 1 ? min(fb_end, gb + rounds) : fb_end;
+  uint4* const st0 = stage0 + (KS > 1 ? grp * SLOTS * SLOT : 0);
+  uint4* const st1 = stage1 + (KS > 1 ? grp * SLOTS * SLOT : 0);
 
   // ---- weights: global -> LDS DMA ------------------------------------------
   // Slot s, column block nb of block fb is W'[fb][s][ob0 + nb][lane]: 64 lanes x
@@ -467,7 +494,7 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[rb][nb][r] = 0.0f;
 
-  // ---- prologue: block fb_begin in stage0 and registers ----------------------
+  // ---- prologue: the group's first block in its stage 0 and registers -------
   // B-spline table kernels: HB = has_base at compile time
   constexpr bool kTab = BASIS == BASIS_BSPLINE_TAB || BASIS == BASIS_BSPLINE_TAB0;
   typedef typename std::conditional<kTab, BsplineTab<T, NV>, BasisGen<BASIS, NV>>::type Gen;
@@ -485,8 +512,10 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
     if (tid <= bp.K) rbf_tab[tid] = tid < bp.K ? bp.rbf_sc[tid] : 0.0f;
     gen.tab = rbf_tab;
   }
-  dma(fb_begin, stage0);
-  xload(fb_begin);
+  if (KS == 1 || gb < ge) {
+    dma(gb, st0);
+    xload(gb);
+  }
   __syncthreads();
   // kHoist (RBF): the B fragments in one register set per slot parity and the
   // read addresses of a slot pair hoisted (see the slot loop).  Measured on
@@ -508,7 +537,7 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   // at the block start (measured: the spread gains 2 % on the fully unrolled
   // table kernels and loses 1-3 % in the slot loop of the others).
   const uint4* dsrc = wtile;
-  uint4* ddst = stage1;
+  uint4* ddst = st1;
   auto dma_one = [&](int si) __attribute__((always_inline)) {
     static_assert(!kTab || (NB == WAVES), "one DMA instruction per wave and slot");
     const int j = wave + si * WAVES;
@@ -580,13 +609,13 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   auto block = [&](int fb, const uint4* cur, uint4* nxt) {
     float xf[NV];
     xunpack(fb, xf);
-    if (fb + 1 < fb_end) xload(fb + 1);
+    if (fb + 1 < ge) xload(fb + 1);
     if constexpr (kTab) {
       // the last block reloads its own weights into the idle stage (in bounds,
       // branch-free; waited for by the closing barrier like the others)
-      dsrc = wtile + (long)min(fb + 1, fb_end - 1) * KP * nob_pad * 64;
+      dsrc = wtile + (long)min(fb + 1, ge - 1) * KP * nob_pad * 64;
       ddst = nxt;
-    } else if (fb + 1 < fb_end) {
+    } else if (fb + 1 < ge) {
       dma(fb + 1, nxt);
     }
     if constexpr (kTab) {
@@ -641,11 +670,61 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       }
       if (s < KP) slot(cur, s, std::integral_constant<int, 0>{});
     }
-    __syncthreads();
   };
-  for (int fb = fb_begin; fb < fb_end; fb += 2) {
-    block(fb, stage0, stage1);
-    if (fb + 1 < fb_end) block(fb + 1, stage1, stage0);
+  // each block ends with the barrier that waits for its successor's DMA and
+  // input loads and frees its stage
+  if constexpr (KS == 1) {
+    for (int fb = fb_begin; fb < fb_end; fb += 2) {
+      block(fb, st0, st1);
+      __syncthreads();
+      if (fb + 1 < fb_end) {
+        block(fb + 1, st1, st0);
+        __syncthreads();
+      }
+    }
+  } else {
+    // every group runs `rounds` rounds; a group past its run only joins the barrier
+    for (int it = 0; it < rounds; it += 2) {
+      if (gb + it < ge) block(gb + it, st0, st1);
+      __syncthreads();
+      if (it + 1 < rounds) {
+        if (gb + it + 1 < ge) block(gb + it + 1, st1, st0);
+        __syncthreads();
+      }
+    }
+    // groups 1 .. KS-1 hand their accumulators to group 0 through the idle
+    // stages (lane-contiguous, conflict-free); group 0 adds them in group order
+    constexpr int NACC = RB * NB * 16;
+    constexpr int GRP_FLOATS = WAVES * NACC * 64;
+    constexpr int PER_STAGE = KS * SLOTS * SLOT * 4 / GRP_FLOATS;  // groups per stage array
+    static_assert(2 * PER_STAGE >= KS - 1, "wave-group reduction does not fit the stages");
+    auto red_of = [&](int g) -> float* {  // g = 1 .. KS-1
+      const int i = g - 1;
+      float* base = reinterpret_cast<float*>(i < PER_STAGE ? stage0 : stage1);
+      const int j = i < PER_STAGE ? i : i - PER_STAGE;
+      return base + (j * WAVES + wave) * NACC * 64 + lane;
+    };
+    if (grp > 0) {
+      float* r = red_of(grp);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) r[((rb * NB + nb) * 16 + q) * 64] = acc[rb][nb][q];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) {
+      const float* r = red_of(g);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[rb][nb][q] += r[((rb * NB + nb) * 16 + q) * 64];
+    }
   }
 
   // ---- epilogue -------------------------------------------------------------
@@ -772,9 +851,23 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   if (waves == 4) {
     if constexpr (kBlock4) {
       constexpr int BB = BASIS == BASIS_CHEBY ? BASIS_CHEBY_POST : BASIS;
-      hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 4>), grid, dim3(256), 0, st, (const TX*)L.X,
-                         L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
-                         L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+      auto go = [&](auto KSC) {
+        constexpr int KS = decltype(KSC)::value;
+        hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 4, KS>), grid, dim3(256 * KS), 0, st,
+                           (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy,
+                           part, L.B, L.D_in, L.D_out, m_tiles, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+      };
+      // wave groups (block_wave_groups_ok): 2 on (32,1) and (32,4), 4 on (32,1)
+      if constexpr (WM == 32 && NB == 1) {
+        if (L.ks == 4) go(std::integral_constant<int, 4>{});
+        else if (L.ks == 2) go(std::integral_constant<int, 2>{});
+        else go(std::integral_constant<int, 1>{});
+      } else if constexpr (WM == 32 && NB == 4) {
+        if (L.ks == 2) go(std::integral_constant<int, 2>{});
+        else go(std::integral_constant<int, 1>{});
+      } else {
+        go(std::integral_constant<int, 1>{});
+      }
     }
   } else if (waves == 8) {
     if constexpr (kBlock8) {
@@ -836,6 +929,12 @@ static hipError_t launch_dense_cfg(const DenseLaunch& L, hipStream_t st) {
   if (L.wm == 32 && L.nb == 4) return launch_dense_t<T, TX, TY, BASIS, 32, 4>(L, st);
   if (L.wm == 32 && L.nb == 1) return launch_dense_t<T, TX, TY, BASIS, 32, 1>(L, st);
   return hipErrorInvalidValue;
+}
+
+// Wave groups per workgroup the 4-wave block kernel is instantiated with for a
+// tile (KS = 1 always).  Keep in sync with launch_dense_t.
+bool block_wave_groups_ok(int wm, int nb, int ks) {
+  return ks == 1 || (wm == 32 && ((nb == 1 && (ks == 2 || ks == 4)) || (nb == 4 && ks == 2)));
 }
 
 bool dense_config_supported(int wm, int nb) {

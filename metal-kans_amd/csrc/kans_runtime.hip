@@ -38,6 +38,7 @@ using namespace kans;
 namespace kans {
 hipError_t launch_dense(const DenseLaunch& L, hipStream_t st);
 bool dense_config_supported(int wm, int nb);
+bool block_wave_groups_ok(int wm, int nb, int ks);
 int block_waves(bool half, int basis, int wm, int nb, int KP);
 hipError_t launch_repack(int src_dtype, int dtype, const void* W, const void* Wb, void* Wt, int D_in, int D_out,
                          int K, int has_base, int nfb, int nob_pad, hipStream_t st);
@@ -122,6 +123,7 @@ struct kans_layer {
   DevBuf Wt, bias_d, part, x_d, y_d, raw_w, raw_wb;
   bool have_weights = false;
   int forced_wm = 0, forced_nb = 0, forced_splits = 0;  // tuning overrides (0 = heuristic)
+  int forced_ks = 0;  // wave groups per workgroup override (0 = heuristic)
   unsigned gen = 0;  // bumped whenever a buffer captured by a graph may have moved
 };
 
@@ -238,6 +240,15 @@ int kans_layer_set_tiling(kans_layer* L, int wm, int nb, int splits) {
   L->forced_wm = wm;
   L->forced_nb = nb;
   L->forced_splits = splits;
+  ++L->gen;
+  return 0;
+}
+
+int kans_layer_set_wave_groups(kans_layer* L, int groups) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  if (groups != 0 && groups != 1 && groups != 2 && groups != 4)
+    return kans_fail(KANS_ERR_ARG, "wave groups must be 0 (automatic), 1, 2 or 4");
+  L->forced_ks = groups;
   ++L->gen;
   return 0;
 }
@@ -380,6 +391,25 @@ static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* spl
   *splits = s;
 }
 
+// Wave groups per workgroup (KS) of the 4-wave block kernel for a forward of
+// batch B on tile (wm, nb) x splits.  A layer that leaves at most one such
+// workgroup per CU gets 4 groups on (32,1) or 2 on (32,4), when each group
+// still has at least 4 feature blocks: one workgroup per CU then holds 4·KS
+// waves instead of 4, each with a KS times shorter chain of blocks.  A forced
+// tile keeps one group unless the groups are forced too; a forced count that
+// the tile is not instantiated with falls back to 1.
+static int choose_wave_groups(const kans_layer* L, int B, int wm, int nb, int splits) {
+  if (block_waves(L->dtype != DT_F32, L->basis, wm, nb, L->K + L->has_base) != 4) return 1;
+  if (L->forced_ks) return block_wave_groups_ok(wm, nb, L->forced_ks) ? L->forced_ks : 1;
+  if (L->forced_wm) return 1;
+  const long wgs = (long)((B + 4 * wm - 1) / (4 * wm)) * (((L->D_out + 31) / 32 + nb - 1) / nb) * splits;
+  const int fbps = (L->nfb + splits - 1) / splits;
+  if (wgs > 256) return 1;
+  if (block_wave_groups_ok(wm, nb, 4) && fbps >= 16) return 4;
+  if (block_wave_groups_ok(wm, nb, 2) && fbps >= 8) return 2;
+  return 1;
+}
+
 // Reserve the split workspace a forward of batch B needs (no launch).
 static int layer_reserve_locked(kans_layer* L, int B) {
   int wm, nb, splits;
@@ -430,6 +460,7 @@ static int layer_launch_locked(kans_layer* L, const void* X, long ldx, void* Y, 
   D.nfb = L->nfb;
   D.bp = L->bp;
   choose_tiling(L, B, &D.wm, &D.nb, &D.splits);
+  D.ks = choose_wave_groups(L, B, D.wm, D.nb, D.splits);
   if (D.splits > 1) {
     if (L->part.cap < (size_t)D.splits * B * L->D_out * sizeof(float))
       return kans_fail(KANS_ERR_STATE, "split workspace not reserved");
@@ -549,14 +580,17 @@ int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
   static const char* dt[] = {"float", "_Float16", "__bf16"};
   static const char* bs[] = {"BASIS_CHEBY", "BASIS_RBF", "BASIS_BSPLINE"};
   const int waves = block_waves(L->dtype != DT_F32, L->basis, wm, nb, L->K + L->has_base);
+  const int ks = choose_wave_groups(L, B, wm, nb, splits);
+  char groups[32] = "";
+  if (ks > 1) snprintf(groups, sizeof groups, " x %d groups", ks);
   int n;
   if (waves)
-    n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves>", dt[L->dtype],
+    n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves%s>", dt[L->dtype],
                  L->basis == BASIS_RBF       ? (L->bp.rbf_rec ? "BASIS_RBF_REC" : "BASIS_RBF_TABLE")
                  : L->basis == BASIS_BSPLINE && waves == 8 && L->bp.grid_size == kBsplineTabG
                      ? (L->has_base ? "BASIS_BSPLINE_TAB" : "BASIS_BSPLINE_TAB0")
                      : bs[L->basis],
-                 wm, nb, waves);
+                 wm, nb, waves, groups);
   else
     n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", dt[L->dtype], bs[L->basis], wm, nb);
   if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);

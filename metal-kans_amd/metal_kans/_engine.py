@@ -110,6 +110,7 @@ class LayerEngine:
         self.snaps: Optional[Sequence[_Snapshot]] = None
         self.dev_key: Optional[tuple] = None
         self.tiling = (0, 0, 0)
+        self.wave_groups = 0
 
     def __del__(self):
         try:
@@ -139,13 +140,17 @@ class LayerEngine:
         self.dev_key = None
         if self.tiling != (0, 0, 0):
             device.check(lib.kans_layer_set_tiling(self.handle, *self.tiling), "kans_layer_set_tiling")
+        if self.wave_groups:
+            device.check(lib.kans_layer_set_wave_groups(self.handle, self.wave_groups), "kans_layer_set_wave_groups")
         return lib
 
-    def set_tiling(self, wm: int, nb: int, splits: int = 0) -> None:
+    def set_tiling(self, wm: int, nb: int, splits: int = 0, wave_groups: int = 0) -> None:
         self.tiling = (int(wm), int(nb), int(splits))
+        self.wave_groups = int(wave_groups)
         if self.handle:
-            device.check(device.get_metal_bridge().kans_layer_set_tiling(self.handle, *self.tiling),
-                         "kans_layer_set_tiling")
+            lib = device.get_metal_bridge()
+            device.check(lib.kans_layer_set_tiling(self.handle, *self.tiling), "kans_layer_set_tiling")
+            device.check(lib.kans_layer_set_wave_groups(self.handle, self.wave_groups), "kans_layer_set_wave_groups")
 
     def prepare_f32(self, dt: int, W: np.ndarray, W_base: Optional[np.ndarray], bias: Optional[np.ndarray],
                     params: tuple, verify: bool = True) -> None:

@@ -88,9 +88,11 @@ class KANLayerBase:
         self._frozen = bool(frozen)
         return self
 
-    def set_tiling(self, wm: int, nb: int, splits: int = 0) -> None:
-        """Force the fused kernel's tile shape (tuning/testing); (0, 0) restores the heuristic."""
-        self._engine().set_tiling(wm, nb, splits)
+    def set_tiling(self, wm: int, nb: int, splits: int = 0, wave_groups: int = 0) -> None:
+        """Force the fused kernel's tile shape (tuning/testing); (0, 0) restores the heuristic.
+        ``wave_groups`` (1, 2, 4; 0 = automatic) splits a 16-bit Chebyshev tile's feature blocks over
+        wave groups of one workgroup where the tile is instantiated with them."""
+        self._engine().set_tiling(wm, nb, splits, wave_groups)
 
     def _engine(self) -> LayerEngine:
         if self._engine_obj is None:

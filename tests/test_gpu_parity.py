@@ -141,6 +141,31 @@ def test_block_kernel_small_tile_stages(gpu, dtype, K, base, bias, d_in):
         assert name.value.startswith(b"kans::kan_fused_block<") and b"32, 1, 4 waves>" in name.value, name.value
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("wm,nb,groups", [(32, 1, 2), (32, 1, 4), (32, 4, 2)])
+@pytest.mark.parametrize("K,base,bias", [(9, True, True), (4, False, True), (1, True, False)])
+@pytest.mark.parametrize("d_in", [200, 64, 16])
+def test_block_kernel_wave_groups(gpu, dtype, wm, nb, groups, K, base, bias, d_in):
+    """The 4-wave Chebyshev block kernel with 2 or 4 wave groups per workgroup splitting a tile's
+    feature blocks (13, 4 and 1 blocks: uneven runs and groups with no block), alone and under a
+    3-way feature split, ragged rows and columns; the groups' sums are added in a fixed order, so
+    a rerun is bit-identical."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", d_in, 70, K, bias=bias, base=base, seed=31)
+    x = np.random.default_rng(9).uniform(-1.2, 1.2, (150, d_in)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    for splits in (1, 3):
+        L.set_tiling(wm, nb, splits, groups)
+        y = L(x)
+        assert O.rel_err(y, y_ref) <= TOL[dtype], splits
+        assert np.array_equal(L(x).view(np.uint16), y.view(np.uint16))
+        name = ctypes.create_string_buffer(160)
+        assert gpu.kans_layer_kernel(L._engine().handle, 150, name, 160) == 0
+        tag = f"{wm}, {nb}, 4 waves x {groups} groups>".encode()
+        assert name.value.startswith(b"kans::kan_fused_block<") and tag in name.value, name.value
+
+
 def test_rbf_arbitrary_centres(gpu):
     import metal_kans as mk
     L = make_layer(mk, "rbf", 48, 40, 5, seed=4)
