@@ -784,6 +784,46 @@ __global__ void kan_split_finalize(const float* __restrict__ part, int splits, c
   }
 }
 
+// The same reduction for 4 consecutive columns per thread (D_out and ldy
+// multiples of 4, Y aligned to 4 elements): 16-byte partial loads and one
+// vector store, the same sum order per element.
+template <typename T, typename TY>
+__global__ void kan_split_finalize4(const float4* __restrict__ part, int splits, const T* __restrict__ bias,
+                                    TY* __restrict__ Y, long ldy, int B, int D_out) {
+  const long n4 = (long)B * D_out / 4;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
+    const long idx = 4 * i;
+    const int row = (int)(idx / D_out), col = (int)(idx - (long)row * D_out);
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = bias ? to_f32(bias[col + j]) : 0.0f;
+    for (int k0 = 0; k0 < splits; k0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = k0 + u < splits ? part[(long)(k0 + u) * n4 + i] : make_float4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < splits) {
+          s[0] += v[u].x;
+          s[1] += v[u].y;
+          s[2] += v[u].z;
+          s[3] += v[u].w;
+        }
+    }
+    TY* out = Y + (long)row * ldy + col;
+    if constexpr (sizeof(TY) == 4) {
+      *reinterpret_cast<float4*>(out) = make_float4(s[0], s[1], s[2], s[3]);
+    } else {
+      TY h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = from_f32<TY>(s[j]);
+      uint2 u;
+      __builtin_memcpy(&u, h, 8);
+      *reinterpret_cast<uint2*>(out) = u;
+    }
+  }
+}
+
 // Repack raw weights W[D_out][D_in*K] (k fastest) and W_base[D_out][D_in], of
 // element type S, into the tiled layout W'[fb][s][ob][chunk][lane][e] of type T
 // (see kans_common.h), converting S -> T with round-to-nearest-even; zero
@@ -899,10 +939,16 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (splits > 1) {
-    long n = (long)L.B * L.D_out;
-    int blocks = (int)std::min<long>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL((kan_split_finalize<T, TY>), dim3(blocks), dim3(256), 0, st, part, splits,
-                       (const T*)L.bias, (TY*)L.Y, L.ldy, L.B, L.D_out);
+    const long n = (long)L.B * L.D_out;
+    if (L.D_out % 4 == 0 && L.ldy % 4 == 0 && ((uintptr_t)L.Y % (4 * sizeof(TY))) == 0) {
+      const int blocks = (int)std::min<long>((n / 4 + 255) / 256, 4096);
+      hipLaunchKernelGGL((kan_split_finalize4<T, TY>), dim3(blocks), dim3(256), 0, st, (const float4*)part, splits,
+                         (const T*)L.bias, (TY*)L.Y, L.ldy, L.B, L.D_out);
+    } else {
+      const int blocks = (int)std::min<long>((n + 255) / 256, 4096);
+      hipLaunchKernelGGL((kan_split_finalize<T, TY>), dim3(blocks), dim3(256), 0, st, part, splits,
+                         (const T*)L.bias, (TY*)L.Y, L.ldy, L.B, L.D_out);
+    }
     e = hipGetLastError();
   }
   return e;

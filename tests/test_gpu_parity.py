@@ -100,6 +100,22 @@ def test_tilings_and_splits(gpu, wm, nb, splits, dtype, kind, K):
     assert O.rel_err(cast(L, dtype)(x), y_ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("wm,nb", [(32, 4), (32, 8), (32, 1)])
+@pytest.mark.parametrize("d_out", [200, 64])
+def test_split_reduce_vector_path(gpu, dtype, wm, nb, d_out):
+    """Feature splits on layers whose output width is a multiple of 4 take the 4-column split reduce
+    (16-byte partial loads, one vector store); splits of 2, 3 and 5, ragged rows."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", 120, d_out, 6, seed=17)
+    x = np.random.default_rng(12).uniform(-1, 1, (201, 120)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    for splits in (2, 3, 5):
+        L.set_tiling(wm, nb, splits)
+        assert O.rel_err(L(x), y_ref) <= TOL[dtype], splits
+
+
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("kind,K", [("rbf", 8), ("bspline", 8), ("rbf", 5), ("bspline", 6), ("cheby", 9),
                                     ("cheby", 4)])
