@@ -1347,14 +1347,15 @@ __global__ void __launch_bounds__(256) k_qreduce(const float* __restrict__ part,
   const long total = (long)B * N;
   float sum = 0.0f;
   if (n < N) {
-    // splits g, g+4, ... in order, loaded 8 at a time (one memory round trip each)
+    // splits g, g+4, ... in order, loaded 16 at a time (one memory round trip
+    // each; the B = 32 down GEMV has ~40 splits, 10 per thread)
     const float* p = part + (long)m * N + n;
-    for (int k0 = g; k0 < ksplit; k0 += 32) {
-      float v[8];
+    for (int k0 = g; k0 < ksplit; k0 += 64) {
+      float v[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = k0 + 4 * u < ksplit ? p[(long)(k0 + 4 * u) * total] : 0.f;
+      for (int u = 0; u < 16; ++u) v[u] = k0 + 4 * u < ksplit ? p[(long)(k0 + 4 * u) * total] : 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 16; ++u)
         if (k0 + 4 * u < ksplit) sum += v[u];
     }
   }
