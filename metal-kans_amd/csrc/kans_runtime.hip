@@ -341,7 +341,8 @@ int kans_layer_load_weights_device(kans_layer* L, const void* W, const void* W_b
 //    measured on the config-2 chain's layers (4096 x 784 -> 256 best at
 //    (32,4) x 4 splits, 4096 x 256 -> 256 at (32,1) unsplit).
 // 3. Else the shape with the most tiles, split towards 512 workgroups, at most
-//    nfb / 2 ways (4096 x 256 -> 10: (32,1) x 8).
+//    nfb / 2 ways on the block kernel (4096 x 256 -> 10: (32,1) x 8) and nfb
+//    ways on the per-slot kernel.
 static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* splits) {
   static const int pref_n8[4][2] = {{32, 8}, {64, 4}, {32, 4}, {32, 1}};
   static const int pref_n4[4][2] = {{32, 4}, {64, 4}, {32, 8}, {32, 1}};
@@ -382,7 +383,11 @@ static void choose_tiling(const kans_layer* L, int B, int* wm, int* nb, int* spl
       if (mostly_padding(c[1])) continue;
       if (wgs(c[0], c[1]) > bt) { bw = c[0]; bn = c[1]; bt = wgs(c[0], c[1]); }
     }
-    s = std::max(1, std::min((512 + bt - 1) / bt, std::max(1, L->nfb / 2)));
+    // at most one feature block per split on the per-slot kernel (one barrier per
+    // slot: a shorter chain pays; 256 x 64 -> 64 fp32: 4 splits 9.0 us, 2 splits
+    // 12.8 us), two on the block kernel
+    const bool per_slot = block_waves(!f32, L->basis, bw, bn, KP) == 0;
+    s = std::max(1, std::min((512 + bt - 1) / bt, std::max(1, per_slot ? L->nfb : L->nfb / 2)));
   }
   if (L->forced_wm && L->forced_nb) { bw = L->forced_wm; bn = L->forced_nb; }
   if (L->forced_splits) s = L->forced_splits;
