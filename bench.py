@@ -558,8 +558,8 @@ def main():
                                   ln_normal, np.sqrt(1.0 / (1024 * 8)), a.warmup, iters, grid_range=(-2.0, 2.0))
     F = st["flops"]
     wall_ms = head["ms_wall"]
-    name = ctypes.create_string_buffer(160)
-    assert lib.kans_layer_kernel(st["eng"].handle, 16384, name, 160) == 0
+    name = ctypes.create_string_buffer(200)
+    assert lib.kans_layer_kernel_ex(st["eng"].handle, 16384, 1, 1, name, 200) == 0   # fp16 x and y, as timed
     head_kernel = name.value.decode()
     value = F / wall_ms / 1e9
     kernel_ms = head["ms"]

@@ -189,6 +189,10 @@ int kans_layer_set_wave_groups(kans_layer* layer, int groups);
 int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
 /* name of the fused kernel (and its tile) that a forward of batch B runs, NUL-terminated in name[len] */
 int kans_layer_kernel(const kans_layer* layer, int B, char* name, int len);
+/* as kans_layer_kernel for a forward with X / Y element types x_dtype / y_dtype (each the layer dtype or
+ * KANS_DT_F32), naming the template's layer, X and Y types in template order, e.g.
+ * "kans::kan_fused_block<_Float16, _Float16, _Float16, BASIS_RBF_REC, 32, 8, 8 waves>" */
+int kans_layer_kernel_ex(const kans_layer* layer, int B, int x_dtype, int y_dtype, char* name, int len);
 /* weights in the layer dtype: W [D_out][D_in*K] (k fastest), W_base [D_out][D_in], bias [D_out] */
 int kans_layer_load_weights(kans_layer* layer, const void* W, const void* W_base, const void* bias);
 int kans_layer_load_weights_device(kans_layer* layer, const void* W, const void* W_base, const void* bias);

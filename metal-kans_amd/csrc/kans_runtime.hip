@@ -578,8 +578,11 @@ int kans_layer_describe(const kans_layer* L, int B, int* wm, int* nb, int* split
   return 0;
 }
 
-int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
-  if (!L || !name || len <= 0) return kans_fail(KANS_ERR_ARG, "null argument");
+// Name of the fused kernel a forward of batch B runs.  io = false: the layer dtype and basis variant
+// ("kans::kan_fused_block<_Float16, BASIS_RBF_REC, 32, 8, 8 waves>"); io = true: the template's element
+// types of X and Y as well, in template order ("kans::kan_fused_block<_Float16, _Float16, _Float16,
+// BASIS_RBF_REC, 32, 8, 8 waves>"), as launch_dense routes x_dtype / y_dtype.
+static int layer_kernel_name(const kans_layer* L, int B, bool io, int x_dtype, int y_dtype, char* name, int len) {
   int wm, nb, splits;
   choose_tiling(L, B, &wm, &nb, &splits);
   static const char* dt[] = {"float", "_Float16", "__bf16"};
@@ -588,18 +591,36 @@ int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
   const int ks = choose_wave_groups(L, B, wm, nb, splits);
   char groups[32] = "";
   if (ks > 1) snprintf(groups, sizeof groups, " x %d groups", ks);
+  char types[64];
+  if (io)
+    snprintf(types, sizeof types, "%s, %s, %s", dt[L->dtype], dt[x_dtype == DT_F32 ? DT_F32 : L->dtype],
+             dt[y_dtype == DT_F32 ? DT_F32 : L->dtype]);
+  else
+    snprintf(types, sizeof types, "%s", dt[L->dtype]);
   int n;
   if (waves)
-    n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves%s>", dt[L->dtype],
+    n = snprintf(name, len, "kans::kan_fused_block<%s, %s, %d, %d, %d waves%s>", types,
                  L->basis == BASIS_RBF       ? (L->bp.rbf_rec ? "BASIS_RBF_REC" : "BASIS_RBF_TABLE")
                  : L->basis == BASIS_BSPLINE && waves == 8 && L->bp.grid_size == kBsplineTabG
                      ? (L->has_base ? "BASIS_BSPLINE_TAB" : "BASIS_BSPLINE_TAB0")
                      : bs[L->basis],
                  wm, nb, waves, groups);
   else
-    n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", dt[L->dtype], bs[L->basis], wm, nb);
+    n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", types, bs[L->basis], wm, nb);
   if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);
   return 0;
+}
+
+int kans_layer_kernel(const kans_layer* L, int B, char* name, int len) {
+  if (!L || !name || len <= 0) return kans_fail(KANS_ERR_ARG, "null argument");
+  return layer_kernel_name(L, B, false, L->dtype, L->dtype, name, len);
+}
+
+int kans_layer_kernel_ex(const kans_layer* L, int B, int x_dtype, int y_dtype, char* name, int len) {
+  if (!L || !name || len <= 0) return kans_fail(KANS_ERR_ARG, "null argument");
+  if ((x_dtype != L->dtype && x_dtype != DT_F32) || (y_dtype != L->dtype && y_dtype != DT_F32))
+    return kans_fail(KANS_ERR_ARG, "input/output dtype must be the layer dtype or fp32");
+  return layer_kernel_name(L, B, true, x_dtype, y_dtype, name, len);
 }
 
 // ---------------------------------------------------------------------------
@@ -956,6 +977,9 @@ static unsigned chain_gen(const kans_chain* C) {
 
 static int chain_reserve(kans_chain* C, int B) {
   int rc;
+  for (auto* L : C->layers)
+    if (L->dtype != C->dtype)
+      return kans_fail(KANS_ERR_STATE, "a chain layer's dtype changed since kans_chain_create");
   if (B > C->cap_B) {
     const size_t es = dtype_size(C->dtype);
     void* olds[4] = {C->x_d.p, C->ping.p, C->pong.p, C->y_d.p};
@@ -1300,6 +1324,9 @@ static unsigned dgated_gen(const kans_gated_dense* D) {
 
 static int dgated_reserve(kans_gated_dense* D, int B) {
   int rc;
+  for (const kans_layer* L : {D->gate, D->up, D->down})
+    if (L->dtype != D->dtype)
+      return kans_fail(KANS_ERR_STATE, "a block layer's dtype changed since kans_gated_dense_create");
   if (B > D->cap_B) {
     const size_t es = dtype_size(D->dtype);
     void* olds[5] = {D->x_d.p, D->g_d.p, D->u_d.p, D->h_d.p, D->y_d.p};

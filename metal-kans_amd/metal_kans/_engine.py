@@ -22,6 +22,7 @@ hash would cost ~5 ms per 37 MB of weights).
 from __future__ import annotations
 
 import ctypes
+import itertools
 from typing import Optional, Sequence
 
 import numpy as np
@@ -31,6 +32,10 @@ from . import device
 BASIS = {"cheby": 0, "rbf": 1, "bspline": 2}
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 VERIFY_BYTES = 4 << 20
+# Serial number of every kans_layer handle this process creates.  Objects that borrow layer handles (the
+# multi-layer chain, the dense GatedKAN block) are keyed on serials, never on handle addresses: a handle
+# destroyed and re-created (a dtype change) can come back at the same address.
+_HANDLE_SERIAL = itertools.count(1)
 
 
 def dtype_code(kind: str) -> int:
@@ -105,6 +110,7 @@ class LayerEngine:
         self.has_base = int(has_base)
         self.has_bias = int(has_bias)
         self.handle = ctypes.c_void_p()
+        self.serial = 0          # _HANDLE_SERIAL of the current handle (0: none)
         self.dt = None
         self.params = None
         self.snaps: Optional[Sequence[_Snapshot]] = None
@@ -134,6 +140,7 @@ class LayerEngine:
         device.check(lib.kans_layer_create(BASIS[self.basis], dt, self.d_in, self.d_out, self.K, self.has_base,
                                            self.has_bias, ctypes.byref(h)), "kans_layer_create")
         self.handle = h
+        self.serial = next(_HANDLE_SERIAL)
         self.dt = dt
         self.params = None
         self.snaps = None

@@ -216,7 +216,8 @@ class KANLayerBase:
 
 def device_layer_handle(layer: KANLayerBase, compute: str) -> int:
     """Make the layer's device weights current for compute dtype ``compute`` and return its ``kans_layer``
-    handle (used by the multi-layer chain and the GatedKAN block, which launch the layers themselves)."""
+    handle (used by the multi-layer chain and the GatedKAN block, which launch the layers themselves).
+    Key anything that keeps the handle on ``layer._engine().serial`` with it (see ``_engine``)."""
     dt = {"float32": DT_F32, "float16": DT_F16, "bfloat16": DT_BF16}[compute]
     eng = layer._engine()
     W = getattr(layer, layer._weight_attr)

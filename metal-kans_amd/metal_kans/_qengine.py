@@ -48,7 +48,7 @@ def packed_format(layer) -> Optional[str]:
 
         def live(obj):
             snap = getattr(obj, "_deq_snapshot", None)
-            return snap is not None and snap.same(cur)
+            return snap is not None and snap.same(cur, verify=not getattr(layer, "_frozen", False))
         q = getattr(layer, f"_{attr}_quantized", None)
         if isinstance(q, QuantizedWeight) and q.group_size == 64 and live(q):
             return "int4" if q.bits == 4 else "int8"

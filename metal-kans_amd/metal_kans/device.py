@@ -73,6 +73,7 @@ SIGNATURES = {
     "kans_layer_set_wave_groups": (c_int, [P, c_int]),
     "kans_layer_describe": (c_int, [P, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
     "kans_layer_kernel": (c_int, [P, c_int, ctypes.c_char_p, c_int]),
+    "kans_layer_kernel_ex": (c_int, [P, c_int, c_int, c_int, ctypes.c_char_p, c_int]),
     "kans_cheby_backward": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "metal_kan_cheby_backward_fused": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int]),
     "metal_kan_cheby_backward": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int]),

@@ -88,14 +88,18 @@ class GatedKAN:
         x2 = np.ascontiguousarray(x_2d, dtype=x_in)
         if x2.shape[1] != self.d_model:
             raise ValueError(f"Expected d_model={self.d_model}, got {x2.shape[1]}")
-        handles = tuple(device_layer_handle(k, compute) for k in (self.gate_kan, self.up_kan, self.down_kan))
+        layers = (self.gate_kan, self.up_kan, self.down_kan)
+        handles = tuple(device_layer_handle(k, compute) for k in layers)
         lib = device.get_metal_bridge()
-        if self.__dict__.get("_dense_key") != handles:
+        # keyed on the handles' serial numbers and the compute dtype: a layer whose dtype changed got a new
+        # handle, possibly at the old address, and the block must not keep the destroyed one
+        key = (tuple(k._engine().serial for k in layers), compute)
+        if self.__dict__.get("_dense_key") != key:
             self._drop_dense()
             h = ctypes.c_void_p()
             device.check(lib.kans_gated_dense_create(*handles, ctypes.byref(h)), "kans_gated_dense_create")
             self._dense_block = h
-            self._dense_key = handles
+            self._dense_key = key
         B = x2.shape[0]
         x_dt = DT_F16 if x2.dtype == np.float16 else DT_F32
         if compute == "bfloat16":
@@ -124,6 +128,11 @@ class GatedKAN:
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.d_model) if len(orig_shape) > 2 else x
         self._saved_x = x_2d
+        # the block runs gate, up and down on the device without the layers' own forward: clear what an
+        # earlier direct call to a layer saved, so that a layer backward raises instead of differentiating
+        # a stale input (the reference's forward saves them, gated_kan.py:97-132)
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            kan._saved_x = None
         if x_2d.shape[0] > 0:
             eng = self._decode_engine()
             if eng is not None and fused_batch_ok(eng.fmt, self.degree, x_2d.shape[0]):
@@ -142,6 +151,14 @@ class GatedKAN:
         return out
 
     __call__ = forward
+
+    def freeze_weights(self, frozen: bool = True) -> "GatedKAN":
+        """Declare that gate, up and down's weight arrays will not be edited in place (inference loops): the
+        forward then checks arrays above 4 MB by identity instead of hashing their bytes on every call (see
+        ``KANLayerBase.freeze_weights``)."""
+        for kan in (self.gate_kan, self.up_kan, self.down_kan):
+            kan.freeze_weights(frozen)
+        return self
 
     def to_int8(self, group_size: int = 64) -> "GatedKAN":
         for kan in (self.gate_kan, self.up_kan, self.down_kan):

@@ -142,7 +142,8 @@ class MetalKAN:
         B = x2.shape[0]
         handles = [device_layer_handle(layer, compute) for layer in self.layers]
         lib = device.get_metal_bridge()
-        key = tuple(handles)
+        # handle serial numbers, not addresses: a re-created handle can reuse a destroyed one's address
+        key = (tuple(layer._engine().serial for layer in self.layers), compute)
         if self._chain_key != key:
             self._drop_chain()
             arr = (ctypes.c_void_p * len(handles))(*handles)

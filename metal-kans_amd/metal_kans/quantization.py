@@ -15,9 +15,12 @@ bit-identical to the reference's.  There is no NumPy fallback.
 Each packed object remembers (``_deq_snapshot``) the dequantized array it put
 in place, so a fused kernel that reads the packed weights directly can check
 that they still are the layer's weights (``_qengine.packed_format``).  The
-dequantized arrays are handed out read-only: an in-place edit raises instead of
-silently diverging from the packed weights the fused kernels read; assigning a
-new array changes the weights (the layer then runs on that array).
+dequantized arrays stay writeable, as in the reference (its optimizers update
+them in place, optim.py; torch_module.py:101 assigns into them): an in-place
+edit or a new array retires the packed path for that layer, which then runs on
+the edited fp32 weights.  The check compares contents (a copy up to 4 MB, a
+hash above), so ``layer.freeze_weights()`` (``GatedKAN.freeze_weights()``)
+skips it for large arrays in inference loops.
 
 One addition: a layer that computed in fp16/bf16 before quantization keeps
 that compute dtype (``_quantized_from``), so a quantized ``GatedKAN(dtype=
@@ -109,15 +112,6 @@ class TernaryQuantizedWeight:
         return out
 
 
-def _read_only(a: np.ndarray) -> np.ndarray:
-    """The dequantized weights, read-only together with every array they view (see the module docstring)."""
-    b = a
-    while isinstance(b, np.ndarray):
-        b.flags.writeable = False
-        b = b.base
-    return a
-
-
 def _remember_compute(model: Any) -> None:
     cd = getattr(model, "_compute", None)
     if cd in ("float16", "bfloat16") and not hasattr(model, "_quantized_from"):
@@ -137,7 +131,7 @@ def quantize(model: Any, bits: int = 8, group_size: int = 64) -> Any:
             if w is not None and isinstance(w, np.ndarray) and w.ndim == 2:
                 qw = QuantizedWeight(w, bits=bits, group_size=group_size)
                 setattr(model, f"_{attr}_quantized", qw)
-                setattr(model, attr, _read_only(qw.dequantize()))
+                setattr(model, attr, qw.dequantize())
                 qw._deq_snapshot = _Snapshot(getattr(model, attr))
     if hasattr(model, "sub_layer"):
         quantize(model.sub_layer, bits=bits, group_size=group_size)
@@ -169,7 +163,7 @@ def to_ternary(model: Any, group_size: int = 32) -> Any:
             if w is not None and isinstance(w, np.ndarray) and w.ndim == 2:
                 qw = TernaryQuantizedWeight(w, group_size=group_size)
                 setattr(model, f"_{attr}_ternary", qw)
-                setattr(model, attr, _read_only(qw.dequantize()))
+                setattr(model, attr, qw.dequantize())
                 qw._deq_snapshot = _Snapshot(getattr(model, attr))
     if hasattr(model, "sub_layer"):
         to_ternary(model.sub_layer, group_size=group_size)

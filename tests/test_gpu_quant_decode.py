@@ -384,10 +384,17 @@ def test_gatedkan_python_decode(gpu, quant):
     ref2 = O.gated_forward(x.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
                                                     for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
     assert O.rel_err(out2.astype(np.float32), ref2) <= 2e-2
-    # the dequantized weights are read-only: an in-place edit raises instead of diverging from the
-    # packed weights; a new array retires the packed path for that layer
-    with pytest.raises(ValueError):
-        blk.down_kan.w_cheby[0, 0] += 1.0
+    # the dequantized weights stay writeable, as in the reference: an in-place edit (an optimizer's
+    # param -= lr * update) retires the packed path for that layer, which then runs on the edited weights
+    blk.down_kan.w_cheby[0, :] += np.float32(0.5)
+    assert blk._decode_engine() is None
+    refe = O.gated_forward(x.astype(np.float32), *[{"W": k.w_cheby, "W_base": k.w_base, "K": 4}
+                                                    for k in (blk.gate_kan, blk.up_kan, blk.down_kan)])
+    assert O.rel_err(blk(x).astype(np.float32), refe) <= 2e-2
+    assert O.rel_err(refe, ref2) > 1e-2      # the edit changed the result
+    # so does a new array
+    getattr(blk, f"to_{quant}")()
+    assert blk._decode_engine() is not None
     w = blk.down_kan.w_cheby.copy()
     w[0, 0] += 1.0
     blk.down_kan.w_cheby = w
