@@ -35,8 +35,8 @@ PEAK = {"f16": 2516.6, "bf16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s (MI3
 # calibration: the source of roofline.traffic (PMC counters cannot be read
 # from inside the timed process).
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_kan_fused_block_cfg3_fastkan_fp16.txt")
-SECONDARY = ("ns_cheby_fp16", "ns_bspline_fp16", "cfg4_bspline_bf16", "cfg4_bspline_fp32", "cfg1_cheby_fp32",
-             "cfg2", "cfg5", "ref_published")
+SECONDARY = ("python_api", "ns_cheby_fp16", "ns_bspline_fp16", "cfg4_bspline_bf16", "cfg4_bspline_fp32",
+             "cfg1_cheby_fp32", "cfg2", "cfg5", "ref_published")
 HBM_PEAK_GBS = 8000.0
 METRIC = "fused KAN fwd TFLOP/s + % MFMA peak; quantized-weight HBM GB/s (1 MI355X)"
 
@@ -232,40 +232,17 @@ def measured_traffic(kernel):
         return None
 
 
-def cpu_baseline_cfg3(x, L, budget_s=12.0):
-    """Oracle fp32 four-stage forward (reference stage order) on a row sample of cfg 3."""
-    from oracle import kan_oracle as O
+def cpu_env():
+    """(cores, description) of the host the CPU baselines run on: BLAS threads = the process's CPU share
+    (capped by OMP_NUM_THREADS), CPU model and BLAS library."""
     try:
-        from threadpoolctl import threadpool_limits, threadpool_info
+        from threadpoolctl import threadpool_info
     except Exception:  # pragma: no cover
-        threadpool_limits = None
         threadpool_info = lambda: []  # noqa: E731
     cores = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         cores = min(cores, int(env))
-    rows = 2048
-    xs = np.asarray(x[:rows], dtype=np.float32)
-    W = np.asarray(L.w_rbf, dtype=np.float32)
-    Wb = np.asarray(L.w_base, dtype=np.float32)
-    bias = np.asarray(L.bias, dtype=np.float32)
-    params = {"grid": np.asarray(L.grid, np.float32), "inv_den": L.inv_denominator}
-    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
-    times = []
-    try:
-        O.kan_forward("rbf", xs[:256], W, Wb, bias, params, acc=np.float32)  # warm-up
-        t_start = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-            t0 = time.perf_counter()
-            O.kan_forward("rbf", xs, W, Wb, bias, params, acc=np.float32)
-            times.append(time.perf_counter() - t0)
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
-    t = float(np.median(times))
-    d_out, d_in = Wb.shape
-    K = W.shape[1] // d_in
-    flops = 2.0 * rows * d_out * d_in * (K + 1)
     blas = ""
     try:
         info = threadpool_info()
@@ -280,13 +257,106 @@ def cpu_baseline_cfg3(x, L, budget_s=12.0):
                 break
     except Exception:
         pass
-    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"cfg3 rows 0..{rows - 1} of 16384 (1/8 of the batch), fp32 NumPy four-stage forward "
-                      f"(SiLU+bias, silu(x)W_base^T, Phi, Phi W^T), median of {len(times)} runs "
-                      f"({t * 1e3:.1f} ms each); CPU {cpu_model}; BLAS {blas}"}
+    return cores, f"CPU {cpu_model}; BLAS {blas}"
 
 
-def run_chain_cfg2(lib, mk, warmup, iters):
+def cpu_time(fn, min_runs=3, budget_s=8.0, max_runs=20, warm=None):
+    """Median wall seconds of fn() over at least min_runs calls (more while within budget_s), after one
+    warm-up call (``warm``, default fn itself), with BLAS threads = cpu_env()'s cores."""
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    cores, _ = cpu_env()
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    times = []
+    try:
+        (warm or fn)()
+        t_start = time.perf_counter()
+        while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    return float(np.median(times)), len(times)
+
+
+def _layer_params(L, kind):
+    if kind == "cheby":
+        return {"K": L.degree}
+    if kind == "rbf":
+        return {"grid": np.asarray(L.grid, np.float32), "inv_den": L.inv_denominator}
+    return {"G": L.grid_size, "grid_min": float(L.grid_params[0]), "inv_h": float(L.grid_params[1])}
+
+
+def cpu_layer_baseline(name, kind, x, L, dtype, rows, budget_s=8.0):
+    """The oracle's fp32 four-stage NumPy forward (SiLU+bias, silu(x)W_base^T, Phi, Phi W^T: the reference's
+    stage order, metal_kan_bridge.mm:472-523) on rows 0..rows-1 of the workload's input as the GPU received
+    it (16-bit inputs and weights upcast to fp32: NumPy has no fast fp16 GEMM)."""
+    from oracle import kan_oracle as O
+    B = x.shape[0]
+    rows = min(rows, B)
+    xs = np.asarray(x[:rows], np.float32)
+    if dtype == "f16":
+        xs = xs.astype(np.float16).astype(np.float32)
+    elif dtype == "bf16":
+        xs = O.bf16_to_f32(O.bf16_round(xs)).reshape(xs.shape)
+    W = np.asarray(getattr(L, L._weight_attr), dtype=np.float32)
+    Wb = np.asarray(L.w_base, dtype=np.float32)
+    bias = np.asarray(L.bias, dtype=np.float32)
+    params = _layer_params(L, kind)
+    fwd = lambda: O.kan_forward(kind, xs, W, Wb, bias, params, acc=np.float32)  # noqa: E731
+    t, n = cpu_time(fwd, budget_s=budget_s, warm=lambda: O.kan_forward(kind, xs[:min(rows, 64)], W, Wb, bias, params,
+                                                                       acc=np.float32))
+    d_out, d_in = Wb.shape
+    K = W.shape[1] // d_in
+    flops = 2.0 * rows * d_out * d_in * (K + 1)
+    cores, env = cpu_env()
+    frac = "the whole batch" if rows == B else f"1/{B // rows} of the batch"
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "ms": round(t * 1e3, 3),
+            "tokens_per_s": round(rows / t, 1), "cores": cores, "kind": "port",
+            "sample": f"{name} rows 0..{rows - 1} of {B} ({frac}), fp32 NumPy four-stage forward "
+                      f"(SiLU+bias, silu(x)W_base^T, Phi, Phi W^T), median of {n} runs ({t * 1e3:.1f} ms each); "
+                      f"{env}"}
+
+
+def run_python_api(L, x, flops, kernel_ms, iters=20):
+    """The drop-in API end to end at cfg3: ``layer(x)`` on host fp16 arrays, as a user of the reference calls
+    it (cheby_kan.py:92-141; the reference times whole host calls the same way, metal_kan_bridge.mm:1250-1371).
+    Each call checks the weights for in-place edits (content hash of the weight arrays above 4 MB), stages x
+    through pinned memory, copies it to the device, runs the fused kernel and copies y back; ``frozen``
+    repeats it after ``layer.freeze_weights()``, which skips the hash."""
+    x16 = np.ascontiguousarray(x, dtype=np.float16)
+
+    def med(n):
+        L(x16)
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            L(x16)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e3
+    ms = med(iters)
+    L.freeze_weights(True)
+    try:
+        ms_frozen = med(iters)
+    finally:
+        L.freeze_weights(False)
+    wbytes = int(np.asarray(L.w_rbf).nbytes + np.asarray(L.w_base).nbytes)
+    out = {"ms_per_call": round(ms, 3), "ms_per_call_frozen": round(ms_frozen, 3), "kernel_ms": round(kernel_ms, 5),
+           "tflops_per_call": round(flops / ms / 1e9, 2), "tflops_per_call_frozen": round(flops / ms_frozen / 1e9, 2),
+           "tokens_per_s": round(x16.shape[0] / ms * 1e3, 1), "weight_bytes_checked": wbytes,
+           "io_bytes": int(2 * x16.nbytes), "calls": iters,
+           "what": "FastKAN.__call__ on a host fp16 x (16384 x 1024) returning a host fp16 y: weight check "
+                   "(xxh3 hash of w_rbf and w_base; skipped when frozen), pinned staging, H2D, kernel, D2H, median "
+                   "wall clock per call"}
+    log(f"[bench] cfg3_python_api_host_call: {out}")
+    return out
+
+
+def run_chain_cfg2(lib, mk, warmup, iters, cpu=True):
     """ChebyKAN MLP 784 -> 256 -> 256 -> 10, K = 9, fp16, B = 4096, one HIP graph."""
     rng = np.random.default_rng(1002)
     B = 4096
@@ -308,6 +378,18 @@ def run_chain_cfg2(lib, mk, warmup, iters):
            "frac_mfma_peak": round(flops / ms_dev.value / 1e9 / PEAK["f16"], 4),
            "tokens_per_s": round(B / ms_dev.value * 1e3, 1), "shape": "4096x[784,256,256,10]", "K": 9,
            "dtype": "f16"}
+    if cpu:
+        from oracle import kan_oracle as O
+        specs = [{"kind": "cheby", "W": np.asarray(l.w_cheby, np.float32), "W_base": np.asarray(l.w_base, np.float32),
+                  "bias": np.asarray(l.bias, np.float32), "params": {"K": 9}} for l in net.layers]
+        xs = np.asarray(x, np.float32)
+        t, n = cpu_time(lambda: O.chain_forward(specs, xs, acc=np.float32),
+                        warm=lambda: O.chain_forward(specs, xs[:64], acc=np.float32))
+        cores, env = cpu_env()
+        out["cpu_baseline"] = {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "ms": round(t * 1e3, 3),
+                               "tokens_per_s": round(B / t, 1), "cores": cores, "kind": "port",
+                               "sample": f"cfg2 whole batch (4096 rows), fp32 NumPy forward of the three layers "
+                                         f"(four stages each), median of {n} runs; {env}"}
     log(f"[bench] cfg2_chain: {out}")
     return out
 
@@ -376,13 +458,66 @@ def _dense_dequant_block(lib, packed, shapes, K):
     return blk, layers
 
 
+def _dequantized(lib, fmt, arrs, shape, K):
+    """fp32 (W, W_base) of one layer from its reference-format packed arrays (library dequantizers,
+    bit-identical to quantization.py:136-148 / :275-286)."""
+    d_out, d_in = shape
+    res = []
+    for j, kd in enumerate((d_in * K, d_in)):
+        out = np.empty((d_out, kd), np.float32)
+        if fmt == "ternary":
+            p_, s_ = arrs[2 * j], arrs[2 * j + 1]
+            assert lib.metal_kan_dequantize_ternary(p_.ctypes.data, s_.ctypes.data, out.ctypes.data, d_out, kd,
+                                                    32) == 0, lib.kans_last_error()
+        else:
+            q, s_, b_ = arrs[3 * j:3 * j + 3]
+            fn = lib.metal_kan_dequantize_int4 if fmt == "int4" else lib.metal_kan_dequantize_int8
+            assert fn(q.ctypes.data, s_.ctypes.data, b_.ctypes.data, out.ctypes.data, s_.size, 64) == 0, \
+                lib.kans_last_error()
+        res.append(out)
+    return res
+
+
+def cpu_cfg5(lib, fmt, packed, shapes, K, xs, out, batches):
+    """CPU baseline of the cfg5 lines in the reference's quantized semantics (quantization.py:152-178,
+    gated_kan.py:86-138): the weights dequantized to fp32 once (not timed), then the fp32 NumPy GatedKAN
+    forward (four stages per layer, SwiGLU with the +-20 clip) on the line's own x, timed per batch."""
+    from oracle import kan_oracle as O
+    specs = []
+    for arrs, shape in zip(packed, shapes):
+        W, Wb = _dequantized(lib, fmt, arrs, shape, K)
+        specs.append({"W": W, "W_base": Wb, "K": K})
+    cores, env = cpu_env()
+    for B in batches:
+        x = np.asarray(xs[B], np.float32)
+        fwd = lambda: O.gated_forward(x, *specs, acc=np.float32)  # noqa: E731
+        if B >= 8192:   # one run (about 10-20 s), after a one-row warm-up
+            t, n = cpu_time(fwd, min_runs=1, budget_s=0.0, warm=lambda: O.gated_forward(x[:1], *specs, acc=np.float32))
+        else:
+            t, n = cpu_time(fwd, min_runs=3, budget_s=3.0)
+        key = f"cfg5_{fmt}_prefill_b8192" if B >= 8192 else f"cfg5_{fmt}_decode_b{B}"
+        line = {"ms": round(t * 1e3, 3), "tokens_per_s": round(B / t, 2), "cores": cores, "kind": "port",
+                "sample": f"cfg5 {fmt} GatedKAN at B={B} (the line's own x), weights dequantized to fp32 once "
+                          f"(reference semantics), fp32 NumPy forward, median of {n} runs; {env}"}
+        if B >= 8192:
+            line["value"] = round(2.0 * B * sum(sp["W_base"].size for sp in specs) * (K + 1) / t / 1e12, 4)
+            line["unit"] = "TFLOP/s"
+        else:
+            wb = 4 * sum(sp["W"].size + sp["W_base"].size for sp in specs)
+            line["value"] = round(wb / t / 1e9, 1)
+            line["unit"] = "GB/s of fp32 weights read"
+        out[key]["cpu_baseline"] = line
+        log(f"[bench] {key} cpu_baseline: {line}")
+    del specs
+
+
 # Weight copies the decode lines rotate over: each call's weights were last read COPIES - 1 calls earlier,
 # so even the ternary block (254 MB, within the 256 MB MALL) streams from HBM, as in a model whose layers
 # together exceed the MALL.
 COPIES = 3
 
 
-def run_cfg5(lib, warmup, iters):
+def run_cfg5(lib, warmup, iters, cpu=True):
     """GatedKAN d=4096, h=11008, K=4 (base on, no bias), all six weight matrices
     ~N(0, 0.02) then INT4 (group 64) or ternary (group 32), plus the north star's INT8 (group 64); x ~ N(0,1)
     fp16.  Every line is one whole block forward (gate, up, SwiGLU, down) replayed as one HIP graph on
@@ -427,6 +562,7 @@ def run_cfg5(lib, warmup, iters):
             if B == 8192:
                 out[f"cfg5_{fmt}_prefill_b8192"] = {
                     "ms": round(ms.value, 4), "tflops": round(prefill_flops / ms.value / 1e9, 2),
+                    "tokens_per_s": round(B / ms.value * 1e3, 1),
                     "frac_mfma_peak": round(prefill_flops / ms.value / 1e9 / PEAK["f16"], 4),
                     "packed_weight_bytes": int(nbytes - 2 * 2 * B * d), "batch": B,
                     "path": "fused prefill: packed weights decoded into fp16 MFMA tiles; gate|up one launch "
@@ -449,6 +585,7 @@ def run_cfg5(lib, warmup, iters):
                     sb.free()
                     stream_ceiling[fmt] = round(g.value, 1)
                 out[f"cfg5_{fmt}_decode_b{B}"] = {"ms": round(ms.value, 5), "GB_per_s": round(gbs, 1),
+                                                  "tokens_per_s": round(B / ms.value * 1e3, 1),
                                                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                                                   "stream_ceiling_GB_per_s": stream_ceiling[fmt],
                                                   "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
@@ -462,6 +599,9 @@ def run_cfg5(lib, warmup, iters):
             lib.kans_gated_destroy(b)
         for hnd in layers:
             lib.kans_qlayer_destroy(hnd)
+        if cpu and fmt in ("int4", "ternary"):
+            cpu_cfg5(lib, fmt, packed, [Wb.shape for (W, Wb) in mats], K, xs, out,
+                     batches=(1, 32, 8192) if fmt == "int4" else (1, 32))
         if fmt == "int4":
             # reference point measured in the same run: the dense fp16 kernel on the dequantized weights
             dblk, dlayers = _dense_dequant_block(lib, packed, [Wb.shape for (W, Wb) in mats], K)
@@ -594,6 +734,14 @@ def main():
                                           "frac": round(achieved / head["mfma_ceiling_same_data_tflops"], 4)}},
     }
     workloads = {"cfg3_fastkan_fp16": head}
+    cpu = not (a.quick or a.no_cpu)
+    cpu_rows = {"cfg3_fastkan_fp16": 2048, "ns_cheby_fp16": 2048, "ns_bspline_fp16": 2048, "cfg4_bspline_bf16": 1024,
+                "cfg4_bspline_fp32": 1024, "cfg1_cheby_fp32": 256}
+    if cpu:
+        head["cpu_baseline"] = cpu_layer_baseline("cfg3", "rbf", st["x"], st["L"], "f16", cpu_rows["cfg3_fastkan_fp16"])
+        log(f"[bench] cfg3 cpu_baseline: {head['cpu_baseline']}")
+    if not a.quick and want("python_api"):
+        workloads["cfg3_python_api_host_call"] = run_python_api(st["L"], st["x"], F, kernel_ms)
     if not a.quick:
         unif = lambda lo, hi: (lambda rng, B, d: rng.uniform(lo, hi, (B, d)).astype(np.float32))  # noqa: E731
         for name, kind, B, di, do, K, dt, seed, xf, ws in [
@@ -606,21 +754,21 @@ def main():
             if not want(name):
                 continue
             out, s2 = run_layer_workload(lib, mk, name, kind, B, di, do, K, dt, seed, xf, ws, a.warmup, iters)
+            if cpu:
+                out["cpu_baseline"] = cpu_layer_baseline(name, kind, s2["x"], s2["L"], dt, cpu_rows[name])
+                log(f"[bench] {name} cpu_baseline: {out['cpu_baseline']}")
             workloads[name] = out
             s2["xd"].free()
             s2["yd"].free()
             del s2
         if want("cfg2"):
-            workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters)
+            workloads["cfg2_chain_fp16_graph"] = run_chain_cfg2(lib, mk, a.warmup, iters, cpu=cpu)
         if want("cfg5"):
-            workloads.update(run_cfg5(lib, a.warmup, iters))
+            workloads.update(run_cfg5(lib, a.warmup, iters, cpu=cpu))
         if want("ref_published"):
             workloads.update(run_ref_published(mk, iters))
     result["workloads"] = workloads
-    if not (a.quick or a.no_cpu):
-        result["cpu_baseline"] = cpu_baseline_cfg3(st["x"], st["L"])
-    else:
-        result["cpu_baseline"] = None
+    result["cpu_baseline"] = head.get("cpu_baseline")
     print(json.dumps(result), flush=True)
 
 

@@ -341,11 +341,10 @@ int kans_gated_set_fused_swiglu(int on);
  * setting (no reference counterpart: a tuning and test switch). */
 int kans_decode_set_pre_basis(int on);
 /* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
- * non-temporal.  Automatic uses non-temporal loads when a call's packed weights exceed the 256 MB
- * MALL (they cannot stay cached between calls), plain loads otherwise (a smaller block hits the
- * MALL on the next call).  Results do not depend on it.  Returns the previous mode, or a
- * negative error code for a mode outside 0..2 (no reference counterpart: a tuning and test
- * switch). */
+ * non-temporal.  Automatic loads INT4 and ternary records non-temporally and INT8 records with plain
+ * loads, the faster form for each when a model's weights stream from HBM on every decode step.
+ * Results do not depend on it.  Returns the previous mode, or a negative error code for a mode
+ * outside 0..2 (no reference counterpart: a tuning and test switch). */
 int kans_decode_set_weight_loads(int mode);
 
 /* Measured ceilings for the roofline report (no reference counterpart; measurement only).

@@ -29,6 +29,10 @@ int kans_fail(int code, const char* fmt, ...);
 // called by the library's initialisation with `device` current.
 int kans_noalloc_setup(int device);
 hipStream_t kans_default_stream();
+// fp32 Chebyshev forward (no base branch) of host X on device-resident fp32 weights (kans_runtime.hip);
+// call with the library lock held.
+int kans_ref_cheby_forward_devw_locked(const float* X, const float* W_dev, const float* bias_dev, float* Y, int B,
+                                       int D_in, int D_out, int K, int has_bias);
 
 // Library lock (serialises every entry point that touches device state), lazy
 // device initialisation (call with the lock held) and the grow-only pinned

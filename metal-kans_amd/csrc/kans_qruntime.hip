@@ -68,23 +68,26 @@ size_t dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
 // Weight-record loads of the decode GEMVs: 0 automatic (use_nt), 1 plain,
 // 2 non-temporal.
 int g_weight_loads = 0;
-// MI355X's last-level cache (MALL, "Infinity Cache").
-constexpr size_t kMallBytes = size_t(256) << 20;
 
 // Packed bytes of a layer's re-tiled records (codes + group parameters).
 size_t rec_bytes(const kans_qlayer* L) {
   return (size_t)(L->nrb_pad / L->nw) * L->C_tot * qrec_bytes(L->quant);
 }
 
-// Non-temporal weight loads exactly when the call's weights cannot stay in the
-// MALL between calls anyway.  Measured on the config-5 blocks: INT4 (423 MB)
-// is faster non-temporal at every batch (B = 1 92.5 -> 85.7 us, B = 8
-// 105 -> 94.5, B = 32 129.6 -> 125.4); ternary (254 MB) is faster with plain
-// loads, which hit the MALL on the next call (B = 1 69.4 vs 75.2 us, B = 8
-// 79.3 vs 85.4, B = 32 110.4 vs 114.3).
-int use_nt(size_t weight_bytes) {
+// Cache policy of the weight-record loads, by format.  A decode step of a
+// model streams every layer's weights once, and a model whose quantized layers
+// together exceed the 256 MB MALL finds none of them cached on its next step,
+// so the choice is made for weights read from HBM: measured on the config-5
+// blocks with three weight copies used in turn (one box, same run):
+//   INT4    B = 1: 83.0 us non-temporal, 91.4 plain; B = 32: 130.7 / 132.9
+//   ternary B = 1: 63.0 non-temporal, 66.3 plain;   B = 32: 104.2 / 105.4
+//   INT8    B = 1: 150.0 non-temporal, 141.7 plain; B = 32: 205.8 / 188.3
+// so INT4 and ternary load non-temporally and INT8 with plain loads.  (A
+// ternary block replayed alone stays in the MALL and is faster with plain
+// loads, 60 against 63 us, but that is not how a model's layers are read.)
+int use_nt(int quant) {
   if (g_weight_loads != 0) return g_weight_loads == 2 ? 1 : 0;
-  return weight_bytes > kMallBytes ? 1 : 0;
+  return quant == Q_INT8 ? 0 : 1;
 }
 
 // Superchunk ranges per row group: about items_per_cu work items (waves) per
@@ -373,7 +376,7 @@ int qlayer_forward_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, 
   _Float16* phi = (_Float16*)L->Phi.p;
   float2* S = (float2*)L->S.p;
   if ((rc = prep_locked(L, X, x_dtype, ldx, B, phi, S, st))) return rc;
-  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(rec_bytes(L)), phi, S, (float*)L->part.p, st);
+  return gemv_reduce_locked(L, B, ks, Y, y_dtype, ldy, use_nt(L->quant), phi, S, (float*)L->part.p, st);
 }
 
 // GatedKAN prefill: one launch for gate | up with the SwiGLU epilogue into the
@@ -472,7 +475,7 @@ int gated_decode(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, i
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
   const int h = g->D_out;
   int rc;
-  const int nt = use_nt(rec_bytes(g) + rec_bytes(u) + rec_bytes(d));
+  const int nt = use_nt(g->quant);
   // B <= 2 with the fused epilogue: the gate|up GEMV computes the basis of x
   // itself (no k_prep launch) when its LDS slices fit
   if (g_fused_swiglu && g_pre_basis && B <= kSmallB && ks1 <= kMaxEpiSplit &&
@@ -1013,33 +1016,32 @@ long long kans_gated_stream_bytes(const kans_gated* G, int B) {
 // Reference fused ternary forward (metal_kan_bridge.mm:4684-4733): fp32 X, no
 // base branch, ternary W (D_out x D_in*degree), optional fp32 bias.  Computed
 // in fp32 on the exact dequantized weights (the same arithmetic contract as
-// the reference kernel), so results match the fp32 oracle to 1e-4.
+// the reference kernel), so results match the fp32 oracle to 1e-4.  The codes
+// are dequantized into a device buffer that the fused fp32 kernel's weight
+// re-tiling reads directly: the fp32 weights never leave the device.
 int metal_kan_forward_ternary_cheby(const float* X, const uint32_t* W_packed, const float* scales, const float* bias,
                                     float* Y, int B, int D_in, int D_out, int degree, int group_size, int has_bias) {
   if (!X || !W_packed || !scales || !Y || B <= 0 || D_in <= 0 || D_out <= 0 || degree <= 0 || group_size <= 0)
     return kans_fail(KANS_ERR_ARG, "bad argument");
   if (degree > kMaxK) return kans_fail(KANS_ERR_ARG, "degree %d > %d", degree, kMaxK);
-  std::vector<float> W((size_t)D_out * D_in * degree);
-  {
-    std::lock_guard<std::mutex> lk(kans_mutex());
-    int rc = kans_ensure_init();
-    if (rc) return -1;
-    hipStream_t st = kans_default_stream();
-    const long kd = (long)D_in * degree;
-    const size_t pbytes = (size_t)D_out * ((kd + 15) / 16) * 4, sbytes = (size_t)D_out * ((kd + group_size - 1) / group_size) * 4;
-    DevBuf dp, ds, dw;
-    if ((rc = upload_tmp(dp, W_packed, pbytes, st)) || (rc = upload_tmp(ds, scales, sbytes, st)) ||
-        (rc = dw.reserve(W.size() * 4)))
-      return rc;
-    if ((rc = dequant_ternary_device((const uint32_t*)dp.p, (const float*)ds.p, (float*)dw.p, D_out, (int)kd,
-                                     group_size, st)))
-      return rc;
-    HIP_TRY(hipMemcpyAsync(W.data(), dw.p, W.size() * 4, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
-  }
-  std::vector<float> zero_b(has_bias ? 0 : 1, 0.0f);
-  return metal_kan_cheby_forward(X, W.data(), X /*unused: no base*/, has_bias ? bias : zero_b.data(), Y, B, D_in, D_out,
-                                 degree, 0, has_bias ? 1 : 0);
+  if (has_bias && !bias) return kans_fail(KANS_ERR_ARG, "has_bias=1 but bias is null");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  hipStream_t st = kans_default_stream();
+  const long kd = (long)D_in * degree;
+  const size_t pbytes = (size_t)D_out * ((kd + 15) / 16) * 4, sbytes = (size_t)D_out * ((kd + group_size - 1) / group_size) * 4;
+  DevBuf dp, ds, dw, db;
+  if ((rc = upload_tmp(dp, W_packed, pbytes, st)) || (rc = upload_tmp(ds, scales, sbytes, st)) ||
+      (rc = dw.reserve((size_t)D_out * kd * 4)))
+    return rc;
+  if (has_bias && (rc = upload_tmp(db, bias, (size_t)D_out * 4, st))) return rc;
+  if ((rc = dequant_ternary_device((const uint32_t*)dp.p, (const float*)ds.p, (float*)dw.p, D_out, (int)kd,
+                                   group_size, st)))
+    return rc;
+  // the weight upload synchronises the stream after re-tiling, before these buffers are released
+  return kans_ref_cheby_forward_devw_locked(X, (const float*)dw.p, has_bias ? (const float*)db.p : nullptr, Y, B,
+                                            D_in, D_out, degree, has_bias ? 1 : 0);
 }
 
 }  // extern "C"

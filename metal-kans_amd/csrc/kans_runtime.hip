@@ -820,6 +820,22 @@ static int ref_forward(int basis, int dtype, const void* X, const void* W, const
   return layer_forward_host_locked(L, X, Y, B);
 }
 
+// fp32 Chebyshev forward without a base branch of host X on device-resident fp32 weights W_dev
+// [D_out][D_in*K] and bias_dev (device; null when !has_bias), through the same per-signature layer as
+// the reference-named calls.  Lock held.  For weights produced on the device
+// (metal_kan_forward_ternary_cheby): they are re-tiled from device memory, with no host copy.
+int kans_ref_cheby_forward_devw_locked(const float* X, const float* W_dev, const float* bias_dev, float* Y, int B,
+                                       int D_in, int D_out, int K, int has_bias) {
+  if (!X || !W_dev || !Y || (has_bias && !bias_dev)) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (B < 0) return kans_fail(KANS_ERR_ARG, "B=%d < 0", B);
+  int rc = validate_dims(BASIS_CHEBY, DT_F32, D_in, D_out, K, 0, has_bias);
+  if (rc) return rc;
+  kans_layer* L;
+  if ((rc = sig_layer(BASIS_CHEBY, DT_F32, D_in, D_out, K, 0, has_bias, {}, &L))) return rc;
+  if ((rc = layer_upload_locked(L, W_dev, nullptr, bias_dev, true, DT_F32))) return rc;
+  return layer_forward_host_locked(L, X, Y, B);
+}
+
 static void half_to_floats(const uint16_t* h, float* f, int n) {
   for (int i = 0; i < n; ++i) {
     _Float16 v;
