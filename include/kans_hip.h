@@ -262,16 +262,16 @@ int kans_dequantize_ternary_device(const uint32_t* packed, const float* scales, 
                                    int group_size, void* stream);
 
 /* ----------------------------------------------------------------------- *
- * Quantized Chebyshev layers and the GatedKAN block, fused over the packed   *
+ * Quantized KAN layers and the GatedKAN block, fused over the packed        *
  * weights.  Built from the reference's packed formats (quantization.py:13-99 *
  * INT8 / INT4, :191-246 ternary); no reference counterpart for the fused     *
  * forward with the base branch (the reference dequantizes to fp32,           *
  * quantization.py:152-178, gated_kan.py:86-138).  Batches of at most 32 rows *
- * (INT4, ternary) run the decode GEMVs; larger batches, and every INT8       *
- * batch, the fused prefill kernel, which decodes the packed weights into     *
- * fp16 MFMA tiles and supports K in {1, 2, 4} (other K: KANS_ERR_UNSUPPORTED *
- * for those batches).  Activations are evaluated in fp32 and fed to the      *
- * MFMAs in fp16; results are accumulated in fp32.                            *
+ * (every format) run the decode GEMVs; larger batches the fused prefill     *
+ * kernel, which decodes the packed weights into fp16 MFMA tiles (K and       *
+ * basis limits: kans_qlayer_fused; other layers: KANS_ERR_UNSUPPORTED for    *
+ * those batches).  Activations are evaluated in fp32 and fed to the MFMAs in *
+ * fp16; results are accumulated in fp32.                                     *
  * ----------------------------------------------------------------------- */
 typedef struct kans_qlayer kans_qlayer;
 /* INT4, group_size 64: qweight [D_out * pad/64][32] uint8, scales / biases [D_out * pad/64] fp32,
@@ -280,8 +280,7 @@ int kans_qlayer_create_int4(int D_in, int D_out, int K, int has_base, int has_bi
                             const void* qweight, const float* scales, const float* biases,
                             const void* qweight_base, const float* scales_base, const float* biases_base,
                             const void* bias, int bias_dtype, kans_qlayer** out);
-/* INT8, group_size 64: as INT4 with qweight [D_out * pad/64][64] uint8 (quantization.py:88-97);
- * K in {1, 2, 4} (prefill kernel at every batch) */
+/* INT8, group_size 64: as INT4 with qweight [D_out * pad/64][64] uint8 (quantization.py:88-97) */
 int kans_qlayer_create_int8(int D_in, int D_out, int K, int has_base, int has_bias, int group_size,
                             const void* qweight, const float* scales, const float* biases,
                             const void* qweight_base, const float* scales_base, const float* biases_base,
@@ -292,6 +291,18 @@ int kans_qlayer_create_ternary(int D_in, int D_out, int K, int has_base, int has
                                const uint32_t* w_packed, const float* scales, const uint32_t* w_packed_base,
                                const float* scales_base, const void* bias, int bias_dtype, kans_qlayer** out);
 int kans_qlayer_destroy(kans_qlayer* layer);
+/* The basis expansion of a quantized layer (Chebyshev unless set): the Gaussian RBF with K centres and
+ * inv_denominator = 1/(2h^2) (fast_kan.py:40-42; as kans_layer_set_rbf), or the clamped cubic B-spline with
+ * G = K - 3 intervals from grid_min, inv_h = G / (max - min) (bspline_kan.py:40-54; as
+ * kans_layer_set_bspline).  No reference counterpart: the reference quantizes every layer family's weight
+ * matrices (quantization.py:152-178) and runs their fp32 forward on the dequantized weights. */
+int kans_qlayer_set_rbf(kans_qlayer* layer, const float* centers, float inv_denominator);
+int kans_qlayer_set_bspline(kans_qlayer* layer, int grid_size, float grid_min, float inv_h);
+/* 1 when a forward of B rows runs on the fused packed-weight kernels: B <= 32 always (decode GEMVs, every
+ * basis and K); larger B when the prefill kernel is built for the layer's K and basis (Chebyshev K in
+ * {1, 2, 4, 8}; RBF on uniform centres and B-spline K in {4, 8}); 0 when such a forward returns
+ * KANS_ERR_UNSUPPORTED. */
+int kans_qlayer_fused(const kans_qlayer* layer, int B);
 /* device pointers; x_dtype / y_dtype any of KANS_DT_* (the prefill path reads fp16 / fp32 X, 16-byte aligned,
  * ldx % 8 == 0 and ldx >= round_up(D_in, 8)) */
 int kans_qlayer_forward(kans_qlayer* layer, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy,
@@ -300,10 +311,11 @@ int kans_qlayer_forward_host(kans_qlayer* layer, const void* X, int x_dtype, voi
 
 /* GatedKAN block out = down(SiLU(gate(x)) * up(x)) (gated_kan.py:86-138); the layers are borrowed and
  * must outlive the block.  round16: 1 (fp16) / 2 (bf16) rounds the gate, up and hidden activations as a
- * 16-bit model does, 0 keeps them fp32.  Decode (B <= 32, INT4 / ternary): one prep, the gate|up GEMV with
- * SwiGLU into the down layer's basis, the down GEMV and its reduce.  Prefill (larger B, INT8 always): one
- * fused launch for gate|up with the SwiGLU epilogue (gate and up columns paired in one tile) writing the
- * hidden activations, one for down. */
+ * 16-bit model does, 0 keeps them fp32.  Chebyshev layers only (the reference's GatedKAN is built of
+ * ChebyKAN layers).  Decode (B <= 32, every format): the gate|up GEMV with SwiGLU into the down layer's
+ * basis (computing the basis of x itself at B <= 2, after one prep kernel above), the down GEMV and its
+ * reduce.  Prefill (larger B, K in {1, 2, 4, 8}): one fused launch for gate|up with the SwiGLU epilogue
+ * (gate and up columns paired in one tile) writing the hidden activations, one for down. */
 typedef struct kans_gated kans_gated;
 int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out);
 int kans_gated_destroy(kans_gated* block);

@@ -22,6 +22,11 @@ struct DenseLaunch {
   int ks = 1;           // wave groups per workgroup (4-wave block kernel, block_wave_groups_ok)
 };
 
+// RBF parameters (centres, scaled centres, recurrence eligibility) of bp (bp.K set) from K centres and
+// inv_denominator = 1/(2h^2); false (bp unchanged) when inv_den is negative or not finite
+// (kans_runtime.hip).
+bool kans_set_rbf_params(BasisParams& bp, const float* centers, float inv_den);
+
 }  // namespace kans
 
 int kans_fail(int code, const char* fmt, ...);

@@ -2,6 +2,7 @@
 // the runtime.
 #pragma once
 #include <hip/hip_runtime.h>
+#include "kans_common.h"
 
 namespace kans {
 
@@ -45,6 +46,8 @@ struct QPrep {
   int Cb, C_tot;   // superchunks of the basis segment and of basis + base
   _Float16* Phi;   // [MP][C_tot * 128]
   float2* S;       // [C_tot][MP] (INT4 / INT8; may be null for ternary)
+  int basis = BASIS_CHEBY;  // BASIS_CHEBY / BASIS_RBF / BASIS_BSPLINE
+  BasisParams bp{};         // RBF centres and neg_l, B-spline grid (bp.K = K)
 };
 
 // What a small-batch decode GEMV does after its split-K partial sums are

@@ -308,12 +308,40 @@ __device__ __forceinline__ float load_any(const void* p, long i, int dt) {
   return to_f32(reinterpret_cast<const __bf16*>(p)[i]);
 }
 
-// Layer input v[m][i] of k_prep.
+// Layer input v[m][i] of k_prep, and the layer's basis.
 struct PrepIn {
   const void* X;
   int x_dtype;
   long ldx;
+  int basis;       // BASIS_CHEBY / BASIS_RBF / BASIS_BSPLINE
+  BasisParams bp;  // RBF / B-spline parameters
 };
+
+// Basis function k of the layer at input v, in fp32 (k_prep): Chebyshev T_k(clamp(v, -1, 1)) by the
+// recurrence (fused_kan.metal:216-236); the Gaussian RBF exp(-(v - c_k)^2 inv_den) as
+// exp2(neg_l (v - c_k)^2), neg_l = -inv_den log2(e) (fused_kan.metal:153-165); the clamped uniform
+// cubic B-spline (fused_kan.metal:254-275, with the formulas of BasisGen<BASIS_BSPLINE>).
+__device__ __forceinline__ float prep_basis(const PrepIn& in, float v, int k) {
+  if (in.basis == BASIS_RBF) {
+    const float d = v - in.bp.centers[k];
+    return exp2f(in.bp.neg_l * (d * d));
+  }
+  if (in.basis == BASIS_BSPLINE) {
+    const BasisParams& p = in.bp;
+    const float pos = (v - p.grid_min) * p.inv_h;
+    float fl = __builtin_floorf(pos);
+    fl = __builtin_fminf(__builtin_fmaxf(fl, 0.0f), (float)(p.grid_size - 1));
+    const float u = __builtin_fminf(__builtin_fmaxf(pos - fl, 0.0f), 1.0f);
+    const int d = k - (int)fl;
+    const float om = 1.0f - u, u2 = u * u, u3 = u2 * u, inv6 = 1.0f / 6.0f;
+    if (d == 0) return om * om * om * inv6;
+    if (d == 1) return (3.0f * u3 - 6.0f * u2 + 4.0f) * inv6;
+    if (d == 2) return (-3.0f * u3 + 3.0f * u2 + 3.0f * u + 1.0f) * inv6;
+    if (d == 3) return u3 * inv6;
+    return 0.0f;
+  }
+  return cheb_k(fminf(fmaxf(v, -1.0f), 1.0f), k);
+}
 
 __device__ __forceinline__ float prep_input(const PrepIn& in, int m, int i) {
   return load_any(in.X, (long)m * in.ldx + i, in.x_dtype);
@@ -341,13 +369,13 @@ __global__ void __launch_bounds__(256) k_prep(PrepIn in, int B, int MP, int D_in
       const int nf = (int)((p0 + 7) / K - i0) + 1;
 #pragma unroll
       for (int f = 0; f < 9; ++f)
-        if (f < nf && (i0 + f) * K < Jb) xin[f] = fminf(fmaxf(prep_input(in, m, (int)(i0 + f)), -1.0f), 1.0f);
+        if (f < nf && (i0 + f) * K < Jb) xin[f] = prep_input(in, m, (int)(i0 + f));
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const long j = p0 + unpack_order<QT>(e);
         if (j < Jb) {
           const long i = j / K;
-          v[e] = cheb_k(xin[i - i0], (int)(j - i * K));
+          v[e] = prep_basis(in, xin[i - i0], (int)(j - i * K));
         }
       }
     } else if (has_base) {
@@ -1467,7 +1495,7 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
   // rows B .. MP-1 are left as they are: the GEMVs read them only into
   // accumulator rows they never store
   dim3 grid((unsigned)((P.C_tot * 16 + 255) / 256), (unsigned)P.B);
-  PrepIn in{P.X, P.x_dtype, P.ldx};
+  PrepIn in{P.X, P.x_dtype, P.ldx, P.basis, P.bp};
   if (qt == Q_INT4)
     hipLaunchKernelGGL((k_prep<Q_INT4>), grid, dim3(256), 0, st, in, P.B, P.MP, P.D_in, P.K, P.has_base, P.Cb,
                        P.C_tot, P.Phi, P.S);

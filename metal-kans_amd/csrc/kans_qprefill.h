@@ -2,6 +2,7 @@
 // descriptors shared with the runtime.
 #pragma once
 #include <hip/hip_runtime.h>
+#include "kans_common.h"
 
 namespace kans {
 
@@ -20,14 +21,23 @@ namespace kans {
 //   params P[g][o]: the reference's group parameters, group g = j / group_size
 //          of the row's reduction index j = i*K + s; (scale, bias) float2 for
 //          INT8 / INT4 (group 64), scale float for ternary (group 32).
-// Every 8-code chunk lies in one group when 8*K divides the group size, so the
-// fused kernel loads one parameter set per chunk.  The kernel is built for
-// K in {1, 2, 4} (K = 8 would also fit group 64 but needs more registers than
-// a wave of the 256 x 256 tile has).
+// With K in {1, 2, 4, 8} the 8 codes of a chunk (features i0 .. i0 + 7 of one
+// slot, reduction indices i K + s) lie in one group of 64 (INT8 / INT4), and
+// in one group of 32 (ternary) except at K = 8, where codes 0-3 and 4-7 fall
+// in consecutive groups: the fused kernel loads one parameter set per chunk,
+// two for ternary at K = 8.  Other K (a chunk straddling a group boundary at a
+// data-dependent position) are not built.  Bases: Chebyshev for every such K;
+// the Gaussian RBF on uniform centres (the recurrence of BasisGen<BASIS_RBF_REC>)
+// and the cubic B-spline for K in {4, 8} (FastKAN's and BSplineKAN's default
+// K = 8).
 __host__ __device__ constexpr int qp_chunk_bytes(int qt) { return qt == 0 ? 4 : qt == 2 ? 8 : 2; }  // Q_INT4/TERN/INT8
 __host__ __device__ constexpr int qp_group(int qt) { return qt == 1 ? 32 : 64; }
 __host__ __device__ constexpr int qp_param_floats(int qt) { return qt == 1 ? 1 : 2; }
-inline bool qp_supported(int /*qt*/, int K) { return K == 1 || K == 2 || K == 4; }
+inline bool qp_supported(int /*qt*/, int K, int basis = BASIS_CHEBY, int rbf_rec = 1) {
+  if (basis == BASIS_CHEBY) return K == 1 || K == 2 || K == 4 || K == 8;
+  if (basis == BASIS_RBF && !rbf_rec) return false;
+  return K == 4 || K == 8;
+}
 
 enum QPEpi { QP_EPI_PLAIN = 0, QP_EPI_SWIGLU = 1 };
 
@@ -49,6 +59,8 @@ struct QPMat {
 // from m[0], 4..7 the same columns of m[1]).
 struct QPLaunch {
   int qt, K, has_base;
+  int basis = BASIS_CHEBY;  // BASIS_CHEBY / BASIS_RBF (uniform centres) / BASIS_BSPLINE
+  BasisParams bp{};         // RBF / B-spline parameters (bp.K = K)
   const void* X; long ldx; int x_dtype;
   QPMat m[2];
   int grp;

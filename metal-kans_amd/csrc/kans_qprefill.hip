@@ -87,6 +87,7 @@ __device__ __forceinline__ unsigned fmix2(unsigned u, float s, float off) {
 struct DqParams {
   float s, b1024, b64;  // affine: scale, bias - 1024 s, bias - 64 s
   unsigned s16x2;       // ternary: fp16(scale) in both halves
+  unsigned s16x2b;      // ternary at K = 8: fp16(scale) of codes 4-7 (the next group)
 };
 
 __device__ __forceinline__ DqParams dq_params_affine(float s, float b) {
@@ -94,16 +95,20 @@ __device__ __forceinline__ DqParams dq_params_affine(float s, float b) {
   p.s = s;
   p.b1024 = __builtin_fmaf(-1024.0f, s, b);
   p.b64 = __builtin_fmaf(-64.0f, s, b);
-  p.s16x2 = 0u;
+  p.s16x2 = p.s16x2b = 0u;
   return p;
 }
-__device__ __forceinline__ DqParams dq_params_tern(float s) {
-  DqParams p;
-  p.s = p.b1024 = p.b64 = 0.0f;
+__device__ __forceinline__ unsigned half2_of(float s) {
   const _Float16 h = (_Float16)s;
   unsigned short u;
   __builtin_memcpy(&u, &h, 2);
-  p.s16x2 = (unsigned)u | ((unsigned)u << 16);
+  return (unsigned)u | ((unsigned)u << 16);
+}
+__device__ __forceinline__ DqParams dq_params_tern(float s, float s_b) {
+  DqParams p;
+  p.s = p.b1024 = p.b64 = 0.0f;
+  p.s16x2 = half2_of(s);
+  p.s16x2b = half2_of(s_b);
   return p;
 }
 
@@ -131,8 +136,9 @@ __device__ __forceinline__ uint4 dq_int8(unsigned w0, unsigned w1, const DqParam
 // Ternary chunk in layout A (LB = 0: code 2p at bit 2p, 2p+1 at 16+2p) or B
 // (LB = 1: bits 8+2p, 24+2p) -> 8 fp16 weights t * fp16(s).  v_perm_b32 picks
 // each value's high byte from {0xBC, 0x00, 0x3C, 0x00} (code 0 -> -1.0, 1 -> 0,
-// 2 -> +1.0, 3 -> 0); selector 12 yields the zero low bytes.
-template <int LB>
+// 2 -> +1.0, 3 -> 0); selector 12 yields the zero low bytes.  SPLIT: codes 4-7
+// (pairs 2, 3) take the next group's scale, s16x2b.
+template <int LB, bool SPLIT = false>
 __device__ __forceinline__ uint4 dq_tern(unsigned w, const DqParams& p, const DqConsts<Q_TERN>& k) {
   constexpr unsigned kTable = 0x003C00BCu;
   unsigned o[4];
@@ -143,7 +149,7 @@ __device__ __forceinline__ uint4 dq_tern(unsigned w, const DqParams& p, const Dq
     const unsigned t = __builtin_amdgcn_perm(0u, kTable, sel);
     half2_t th, sh;
     __builtin_memcpy(&th, &t, 4);
-    __builtin_memcpy(&sh, &p.s16x2, 4);
+    __builtin_memcpy(&sh, (SPLIT && q >= 2) ? &p.s16x2b : &p.s16x2, 4);
     const half2_t r = th * sh;
     __builtin_memcpy(&o[q], &r, 4);
   }
@@ -199,6 +205,12 @@ __device__ __forceinline__ void store_any(void* Y, long i, int dt, float v) {
   else reinterpret_cast<__bf16*>(Y)[i] = (__bf16)v;
 }
 
+// emit<KN> of the B-spline table generator into the A fragments a
+template <int KN, typename G, typename Frag>
+__device__ __forceinline__ void gen_emit_tab(const G& g, Frag (&a)[1]) {
+  g.template emit<KN>(a);
+}
+
 struct QPArgs {
   const void* X;
   long ldx;
@@ -212,16 +224,18 @@ struct QPArgs {
   float* part;
   int B, D_in, m_tiles, n_tiles, nfb, fb_per_split;
   int epi, round16;
+  BasisParams bp;  // RBF / B-spline parameters
 };
 
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// The fused kernel.  QT: Q_INT4 / Q_INT8 / Q_TERN; KQ: Chebyshev coefficients
-// (1, 2, 4, 8); HB: SiLU base branch.  Grid: m_tiles * n_tiles workgroups (x)
-// by feature splits (y), 512 threads.
+// The fused kernel.  QT: Q_INT4 / Q_INT8 / Q_TERN; KQ: basis functions per
+// feature (1, 2, 4, 8); HB: SiLU base branch; BASIS: the A-fragment generator
+// (BASIS_CHEBY_POST, BASIS_RBF_REC, BASIS_BSPLINE; see BasisGen).  Grid:
+// m_tiles * n_tiles workgroups (x) by feature splits (y), 512 threads.
 // ---------------------------------------------------------------------------
-template <int QT, int KQ, int HB>
+template <int QT, int KQ, int HB, int BASIS = BASIS_CHEBY_POST>
 __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   constexpr int KP = KQ + HB;
   constexpr int NV = 8;
@@ -232,7 +246,10 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   constexpr int NCB = QT == Q_TERN ? (KQ == 1 ? 1 : KQ / 2) : (KQ * CB) / 4;  // basis code dwords per block
   constexpr int NCW = QT == Q_INT8 ? 2 : 1;                                     // base code dwords
   typedef half8 frag;
-  static_assert(KQ == 1 || KQ == 2 || KQ == 4, "8 * K must divide the quantization group");
+  static_assert(KQ == 1 || KQ == 2 || KQ == 4 || KQ == 8, "a chunk must lie in one or two whole groups");
+  // ternary at K = 8: codes 0-3 and 4-7 of a chunk in consecutive groups of 32
+  constexpr bool TSPLIT = QT == Q_TERN && 8 * KQ > GS;
+  constexpr int PFB = TSPLIT ? 2 : PF;  // parameter floats per basis chunk
 
   __shared__ uint4 stage0[KP * SLOT];
   __shared__ uint4 stage1[KP * SLOT];
@@ -266,7 +283,7 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   struct QRegs {
     unsigned cb[NCB];
     unsigned cw[NCW];
-    float pb[PF], pw[PF];
+    float pb[PFB], pw[PF];
   };
   // chunk words of segment / slot group g of feature block fbq (clamped into
   // the split: loads past it re-read the last block, in bounds).  Codes are
@@ -277,11 +294,13 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   // Every address is a wave-uniform base (feature block, column block, slot
   // group) plus this lane's fixed byte offset, so the loads take the
   // scalar-base + 32-bit vector-offset form and cost no per-block VALU.
-  // Group of a lane's chunk: g = (16 f + 8 hh) K / GS; with GS = 64 (INT4 /
-  // INT8, K <= 4) or GS = 32 and K <= 2 the hh term never crosses a group
-  // boundary, with GS = 32 and K = 4 it adds hh (base segment, K = 1: never).
+  // Group of a lane's chunk: g = (16 f + 8 hh) K / GS = 16 f K / GS + hh (8 K / GS)
+  // (8 K is a multiple of GS or smaller than it, and 16 f K of 8 K): the hh
+  // term is 0 for 8 K < GS, hh for 8 K = GS (INT at K = 8, ternary at K = 4)
+  // and 2 hh for ternary at K = 8, whose codes 4-7 use group g + 1 (base
+  // segment, K = 1: 0).
   const unsigned cb_off = (unsigned)lane * WB, cw_off = (unsigned)lane * CB;
-  const unsigned pb_off = (unsigned)(((QT == Q_TERN && KQ == 4 ? hh * M.ldp : 0) + o) * PF * 4);
+  const unsigned pb_off = (unsigned)((((8 * KQ) / GS) * hh * M.ldp + o) * PF * 4);
   const unsigned pw_off = (unsigned)(o * PF * 4);
   auto load_cb = [&](int fbq, int g, QRegs& r) __attribute__((always_inline)) {
     const int f = min(fbq, fb_end - 1);
@@ -297,6 +316,7 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     const char* pb = reinterpret_cast<const char*>(M.pb + (long)((16 * f * KQ) / GS) * M.ldp * PF) + pb_off;
     r.pb[0] = reinterpret_cast<const float*>(pb)[0];
     if constexpr (PF == 2) r.pb[1] = reinterpret_cast<const float*>(pb)[1];
+    if constexpr (TSPLIT) r.pb[1] = reinterpret_cast<const float*>(pb + M.ldp * PF * 4)[0];  // group g + 1
     if constexpr (HB) {
       const char* pw = reinterpret_cast<const char*>(M.pw + (long)((16 * f) / GS) * M.ldp * PF) + pw_off;
       r.pw[0] = reinterpret_cast<const float*>(pw)[0];
@@ -332,13 +352,13 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
       if constexpr (QT == Q_INT4) return dq_int4(r.cb[k], pb, dk);
       else if constexpr (QT == Q_INT8) return dq_int8(r.cb[2 * k], r.cb[2 * k + 1], pb, dk);
       else if constexpr (KQ == 1) return dq_tern<0>(tern_spread(r.cb[0]), pb, dk);
-      else return dq_tern<k & 1>(r.cb[k / 2], pb, dk);
+      else return dq_tern<k & 1, TSPLIT>(r.cb[k / 2], pb, dk);
     }
   };
   auto params_of = [&](const QRegs& r, DqParams& pb, DqParams& pw) {
     if constexpr (QT == Q_TERN) {
-      pb = dq_params_tern(r.pb[0]);
-      if constexpr (HB) pw = dq_params_tern(r.pw[0]);
+      pb = dq_params_tern(r.pb[0], r.pb[PFB - 1]);
+      if constexpr (HB) pw = dq_params_tern(r.pw[0], r.pw[0]);
     } else {
       pb = dq_params_affine(r.pb[0], r.pb[1]);
       if constexpr (HB) pw = dq_params_affine(r.pw[0], r.pw[1]);
@@ -413,6 +433,13 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
 
+  __shared__ uint4 bs_sel[kBsplineTabG];  // B-spline table: perm selectors per span (kTab)
+  if constexpr (BASIS == BASIS_BSPLINE_TAB) {
+    if (tid < kBsplineTabG)
+      bs_sel[tid] = make_uint4(bspline_tab_selector(tid, 0), bspline_tab_selector(tid, 1),
+                               bspline_tab_selector(tid, 2), bspline_tab_selector(tid, 3));
+  }
+
   // ---- prologue: block fb_begin decoded into stage0, fb_begin + 1 in registers
   QRegs R;
   load_all(fb_begin, R);
@@ -435,9 +462,19 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  BasisGen<BASIS_CHEBY_POST, NV> gen;
-  BasisParams bp{};
+  // B-spline with G = 5 (K = 8): the per-input table of BsplineTab (one v_perm_b32 per two values and
+  // slot; its 5 selector rows in LDS, written before the prologue's barrier)
+  constexpr bool kTab = BASIS == BASIS_BSPLINE_TAB;
+  static_assert(!kTab || KQ == kBsplineTabG + 3, "B-spline table: G = 5");
+  typedef typename std::conditional<kTab, BsplineTab<_Float16, NV>, BasisGen<kTab ? BASIS_CHEBY_POST : BASIS, NV>>::type Gen;
+  Gen gen;
+  const BasisParams& bp = A.bp;
   frag af[2], bf[kQNB];
+  // emit basis KN of the table generator into A fragment a
+  auto tab_emit = [&](auto KNC, frag& a) __attribute__((always_inline)) {
+    frag(&a1)[1] = *reinterpret_cast<frag(*)[1]>(&a);
+    gen_emit_tab<decltype(KNC)::value>(gen, a1);
+  };
 
   // One feature block: MFMAs of block fb from `cur`, decode of block fb + 1 (in
   // R) into `nxt`, R refilled with block fb + 2.
@@ -450,16 +487,20 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     const bool tail = is_tail(fb + 1);
     load_params(fb + 2, R);
     bread(bf, cur, 0);
-    gen.begin(xf, bp, HB != 0);
+    if constexpr (kTab) gen.begin(xf, bp, bs_sel);
+    else gen.begin(xf, bp, HB != 0);
     {
       float v[NV];
       if constexpr (HB) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) v[i] = silu_f32(xf[i]);
+        pack(af[0], v);
+      } else if constexpr (kTab) {
+        tab_emit(std::integral_constant<int, 0>{}, af[0]);
       } else {
         gen.template step<0>(0, bp, v);
+        pack(af[0], v);
       }
-      pack(af[0], v);
     }
     // slot 0's B-fragment reads stay ahead of the slots' scheduling regions:
     // inside slot 0's the scheduler placed each just before its MFMA, which
@@ -468,11 +509,15 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     static_for<0, KP>([&](auto SCC) __attribute__((always_inline)) {
       constexpr int SC = decltype(SCC)::value;
       constexpr int P = SC & 1;
-      // basis values of slot SC + 1 (T_{SC + 1 - HB}) into the other A fragment
+      // basis values of slot SC + 1 (basis function SC + 1 - HB) into the other A fragment
       if constexpr (SC + 1 < KP) {
-        float v[NV];
-        gen.template step<P ^ 1>(0, bp, v);
-        pack(af[P ^ 1], v);
+        if constexpr (kTab) {
+          tab_emit(std::integral_constant<int, SC + 1 - HB>{}, af[P ^ 1]);
+        } else {
+          float v[NV];
+          gen.template step<P ^ 1>(SC + 1 - HB, bp, v);
+          pack(af[P ^ 1], v);
+        }
       }
       // decode slot SC of block fb + 1, then refill its code word with block fb + 2
       const uint4 d = dq_slot(SCC, R, pb, pw);
@@ -748,28 +793,45 @@ long qp_part_floats(const QPLaunch& L) {
   return (long)L.splits * L.B * n_tiles * 256;
 }
 
-template <int QT, int KQ, int HB>
+template <int QT, int KQ, int HB, int BASIS>
 static void qp_go(const QPArgs& A, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((kan_qfused_block<QT, KQ, HB>), grid, dim3(kQThreads), 0, st, A);
+  hipLaunchKernelGGL((kan_qfused_block<QT, KQ, HB, BASIS>), grid, dim3(kQThreads), 0, st, A);
 }
 
-template <int QT>
+// Instantiated (QT, K, basis) combinations: qp_supported.
+template <int QT, int BASIS>
 static hipError_t qp_dispatch_k(const QPLaunch& L, const QPArgs& A, dim3 grid, hipStream_t st) {
 #define QP_K(KV)                                                   \
   if (L.K == KV) {                                                 \
-    if (L.has_base) qp_go<QT, KV, 1>(A, grid, st);                 \
-    else qp_go<QT, KV, 0>(A, grid, st);                            \
+    if (L.has_base) qp_go<QT, KV, 1, BASIS>(A, grid, st);          \
+    else qp_go<QT, KV, 0, BASIS>(A, grid, st);                     \
     return hipGetLastError();                                      \
   }
-  QP_K(1)
-  QP_K(2)
-  QP_K(4)
+  if constexpr (BASIS == BASIS_CHEBY_POST) {
+    QP_K(1)
+    QP_K(2)
+  }
+  if constexpr (BASIS != BASIS_BSPLINE_TAB) QP_K(4)
+  if constexpr (BASIS != BASIS_BSPLINE) QP_K(8)
 #undef QP_K
   return hipErrorInvalidValue;
 }
 
+template <int QT>
+static hipError_t qp_dispatch_basis(const QPLaunch& L, const QPArgs& A, dim3 grid, hipStream_t st) {
+  switch (L.basis) {
+    case BASIS_CHEBY: return qp_dispatch_k<QT, BASIS_CHEBY_POST>(L, A, grid, st);
+    case BASIS_RBF: return qp_dispatch_k<QT, BASIS_RBF_REC>(L, A, grid, st);
+    default:  // G = 5 (K = 8): the basis table; K = 4 (G = 1): per-value selection
+      if (L.K == kBsplineTabG + 3) return qp_dispatch_k<QT, BASIS_BSPLINE_TAB>(L, A, grid, st);
+      return qp_dispatch_k<QT, BASIS_BSPLINE>(L, A, grid, st);
+  }
+}
+
 hipError_t qp_launch(const QPLaunch& L, hipStream_t st) {
-  if (!qp_supported(L.qt, L.K) || (L.grp != 4 && L.grp != 8) || L.B <= 0) return hipErrorInvalidValue;
+  if (!qp_supported(L.qt, L.K, L.basis, L.bp.rbf_rec) || (L.grp != 4 && L.grp != 8) || L.B <= 0 ||
+      (L.basis != BASIS_CHEBY && (L.grp != 8 || L.bp.K != L.K)))
+    return hipErrorInvalidValue;
   QPArgs A{};
   A.X = L.X;
   A.ldx = L.ldx;
@@ -792,12 +854,13 @@ hipError_t qp_launch(const QPLaunch& L, hipStream_t st) {
   A.part = nsp > 1 ? L.part : nullptr;
   A.epi = L.epi;
   A.round16 = L.round16;
+  A.bp = L.bp;
   const dim3 grid((unsigned)(A.m_tiles * A.n_tiles), (unsigned)nsp);
   hipError_t e;
   switch (L.qt) {
-    case Q_INT4: e = qp_dispatch_k<Q_INT4>(L, A, grid, st); break;
-    case Q_INT8: e = qp_dispatch_k<Q_INT8>(L, A, grid, st); break;
-    default: e = qp_dispatch_k<Q_TERN>(L, A, grid, st); break;
+    case Q_INT4: e = qp_dispatch_basis<Q_INT4>(L, A, grid, st); break;
+    case Q_INT8: e = qp_dispatch_basis<Q_INT8>(L, A, grid, st); break;
+    default: e = qp_dispatch_basis<Q_TERN>(L, A, grid, st); break;
   }
   if (e != hipSuccess || nsp <= 1) return e;
   const long n = (long)L.B * L.m[0].D_out;

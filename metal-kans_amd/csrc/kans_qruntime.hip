@@ -25,6 +25,8 @@ int dequant_ternary_device(const uint32_t* p, const float* s, float* out, int D_
 struct kans_qlayer {
   int quant;                 // Q_INT4 / Q_TERN / Q_INT8
   int D_in, D_out, K, has_base, has_bias, group;
+  int basis = BASIS_CHEBY;   // basis expansion (kans_qlayer_set_rbf / _bspline; Chebyshev by default)
+  BasisParams bp{};          // its parameters (bp.K = K)
   int Cb, Cw, C_tot;         // superchunks: basis, base, total
   int nw;                    // 16-row blocks per decode row group (qrow_blocks)
   int nrb_pad;               // 16-row blocks, padded to a multiple of nw
@@ -253,8 +255,15 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, _Fl
   P.C_tot = L->C_tot;
   P.Phi = phi;
   P.S = S;
+  P.basis = L->basis;
+  P.bp = L->bp;
   HIP_TRY(qprep(L->quant, P, st));
   return 0;
+}
+
+// Whether the fused prefill kernel covers this layer (tiles built, K and basis instantiated).
+bool prefill_ok(const kans_qlayer* L) {
+  return L->prefill && qp_supported(L->quant, L->K, L->basis, L->bp.rbf_rec);
 }
 
 // GEMV of layer a (and b, sharing a's activations phi / S): split-K partial sums
@@ -332,14 +341,18 @@ int check_y(const void* Y, int y_dtype, long ldy, int D_out) {
 // Fused prefill forward of one layer (kans_qprefill.hip), any batch.
 int prefill_layer_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
                          hipStream_t st) {
-  if (!L->prefill)
-    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4} (K = %d)", L->K);
+  if (!prefill_ok(L))
+    return kans_fail(KANS_ERR_UNSUPPORTED,
+                     "the fused quantized prefill path takes K in {1, 2, 4, 8} (Chebyshev) or {4, 8} (RBF on uniform "
+                     "centres, B-spline); this layer has K = %d, basis %d", L->K, L->basis);
   int rc = check_prefill_x(X, x_dtype, ldx, L->D_in);
   if (rc) return rc;
   QPLaunch P{};
   P.qt = L->quant;
   P.K = L->K;
   P.has_base = L->has_base;
+  P.basis = L->basis;
+  P.bp = L->bp;
   P.X = X;
   P.ldx = ldx;
   P.x_dtype = x_dtype;
@@ -390,9 +403,9 @@ struct GatedPrefill {
 int plan_gated_prefill(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
                        int round16, GatedPrefill& GP) {
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
-  if (!g->prefill || !u->prefill || !d->prefill)
-    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4} (K = %d, %d)", g->K,
-                     d->K);
+  if (!prefill_ok(g) || !prefill_ok(u) || !prefill_ok(d))
+    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4, 8} (K = %d, %d)",
+                     g->K, d->K);
   if (g->has_bias && u->has_bias && g->bias_dtype != u->bias_dtype)
     return kans_fail(KANS_ERR_UNSUPPORTED, "gate and up biases of different dtypes");
   int rc = check_prefill_x(X, x_dtype, ldx, g->D_in);
@@ -869,8 +882,44 @@ int kans_qlayer_forward_host(kans_qlayer* L, const void* X, int x_dtype, void* Y
   });
 }
 
+int kans_qlayer_set_rbf(kans_qlayer* L, const float* centers, float inv_denominator) {
+  if (!L || !centers) return kans_fail(KANS_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  BasisParams bp{};
+  bp.K = L->K;
+  if (!kans_set_rbf_params(bp, centers, inv_denominator))
+    return kans_fail(KANS_ERR_ARG, "RBF inv_denominator must be finite and >= 0");
+  L->bp = bp;
+  L->basis = BASIS_RBF;
+  return 0;
+}
+
+int kans_qlayer_set_bspline(kans_qlayer* L, int grid_size, float grid_min, float inv_h) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  if (grid_size <= 0 || grid_size + 3 != L->K)
+    return kans_fail(KANS_ERR_ARG, "grid_size=%d inconsistent with K=%d (K = G + 3)", grid_size, L->K);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  BasisParams bp{};
+  bp.K = L->K;
+  bp.grid_size = grid_size;
+  bp.grid_min = grid_min;
+  bp.inv_h = inv_h;
+  L->bp = bp;
+  L->basis = BASIS_BSPLINE;
+  return 0;
+}
+
+int kans_qlayer_fused(const kans_qlayer* L, int B) {
+  if (!L) return 0;
+  if (B <= 0) return 1;
+  if (B <= kMaxDecodeB && L->decode) return 1;
+  return prefill_ok(L) ? 1 : 0;
+}
+
 int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out) {
   if (!gate || !up || !down || !out) return kans_fail(KANS_ERR_ARG, "null argument");
+  if (gate->basis != BASIS_CHEBY || up->basis != BASIS_CHEBY || down->basis != BASIS_CHEBY)
+    return kans_fail(KANS_ERR_ARG, "the GatedKAN block takes Chebyshev layers (gated_kan.py:36-84)");
   if (gate->quant != up->quant || gate->quant != down->quant)
     return kans_fail(KANS_ERR_ARG, "gate, up and down must share one quantization format");
   if (gate->D_in != up->D_in || gate->D_out != up->D_out || gate->K != up->K || gate->has_base != up->has_base ||

@@ -160,6 +160,17 @@ static void set_rbf_table(BasisParams& bp) {
   bp.rbf_rec = 1;
 }
 
+// RBF basis parameters of K centres and 1/(2h^2) (for the quantized layers, kans_qruntime.hip);
+// false for an inv_denominator the layers refuse.
+bool kans::kans_set_rbf_params(BasisParams& bp, const float* centers, float inv_den) {
+  if (!rbf_inv_den_ok(inv_den)) return false;
+  for (int k = 0; k < bp.K; ++k) bp.centers[k] = centers[k];
+  bp.have_centers = 1;
+  bp.neg_l = -inv_den * kLog2e;
+  set_rbf_table(bp);
+  return true;
+}
+
 static int validate_dims(int basis, int dtype, int D_in, int D_out, int K, int has_base, int has_bias) {
   if (basis < 0 || basis > 2) return kans_fail(KANS_ERR_ARG, "unknown basis %d", basis);
   if (dtype < 0 || dtype > 2) return kans_fail(KANS_ERR_ARG, "unknown dtype %d", dtype);

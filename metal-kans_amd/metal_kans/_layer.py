@@ -132,9 +132,9 @@ class KANLayerBase:
             raise ValueError(f"Expected in_features={self.in_features}, got {D_in}")
 
         # a layer quantized from fp16 runs on its packed weights (fused quantized kernels)
-        from ._qengine import fused_batch_ok, layer_engine
+        from ._qengine import layer_engine
         qeng = layer_engine(self) if B > 0 else None
-        if qeng is not None and fused_batch_ok(qeng.fmt, qeng.K, B):
+        if qeng is not None and qeng.fused(B):
             y = qeng.forward_host(x, np.float16)
             if len(orig_shape) > 2:
                 return y.reshape(*orig_shape[:-1], self.out_features)

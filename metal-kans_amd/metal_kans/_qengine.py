@@ -1,14 +1,16 @@
-"""Device-resident quantized Chebyshev layers and GatedKAN blocks.
+"""Device-resident quantized KAN layers (Chebyshev, Gaussian RBF, B-spline) and GatedKAN blocks.
 
 A layer quantized with ``to_int8`` / ``to_int4`` (group 64) or ``to_ternary``
-(group 32) keeps its packed weights in ``_w_cheby_quantized`` /
-``_w_cheby_ternary`` (and the ``w_base`` counterparts), in the reference's
-formats (quantization.py:13-99, 191-246).  ``QLayerEngine`` uploads those packed
-arrays once and runs the fused kernels on them, which move the packed bytes
-instead of dequantized fp32 weights: the decode GEMVs for batches of at most
-``MAX_DECODE_B`` rows and the fused prefill kernel for larger batches
-(Chebyshev degree K in ``PREFILL_K``).  The engine is rebuilt when the packed
-objects change (a new ``to_int8`` / ``to_int4`` / ``to_ternary``).
+(group 32) keeps its packed weights in ``_<attr>_quantized`` /
+``_<attr>_ternary`` for its basis weight ``<attr>`` (``w_cheby``, ``w_rbf``,
+``w_spline``) and ``w_base``, in the reference's formats (quantization.py:13-99,
+191-246).  ``QLayerEngine`` uploads those packed arrays once and runs the fused
+kernels on them, which move the packed bytes instead of dequantized fp32
+weights: the decode GEMVs for batches of at most ``MAX_DECODE_B`` rows (every
+basis and K) and the fused prefill kernel for larger batches where it is built
+(``kans_qlayer_fused``).  The engine is rebuilt when the packed objects or the
+basis parameters change (a new ``to_int8`` / ``to_int4`` / ``to_ternary``, a new
+grid).
 """
 from __future__ import annotations
 
@@ -21,14 +23,15 @@ from . import device
 from ._engine import DT_BF16, DT_F16, DT_F32
 
 MAX_DECODE_B = 32
-# Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for
-PREFILL_K = (1, 2, 4)
+# Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for (the GatedKAN block)
+PREFILL_K = (1, 2, 4, 8)
 KANS_ERR_UNSUPPORTED = -5
 
 
 def fused_batch_ok(fmt: str, K: int, B: int) -> bool:
-    """Whether a batch of B rows of a layer / block in packed format ``fmt`` with K coefficients runs on the
-    fused quantized kernels (else the caller uses the dequantized weights)."""
+    """Whether a batch of B rows of a Chebyshev GatedKAN block in packed format ``fmt`` with K coefficients
+    runs on the fused quantized kernels (else the caller uses the dequantized weights).  Single layers ask
+    their engine (``QLayerEngine.fused``)."""
     if B <= 0:
         return False
     if B <= MAX_DECODE_B:
@@ -37,8 +40,8 @@ def fused_batch_ok(fmt: str, K: int, B: int) -> bool:
 
 
 def packed_format(layer) -> Optional[str]:
-    """'int8' / 'int4' / 'ternary' when every weight matrix of a Chebyshev layer is packed in a format the fused
-    kernels read (INT8 / INT4 with group 64, ternary with group 32), else None."""
+    """'int8' / 'int4' / 'ternary' when every weight matrix of a KAN layer (its basis weight and W_base) is
+    packed in a format the fused kernels read (INT8 / INT4 with group 64, ternary with group 32), else None."""
     from .quantization import QuantizedWeight, TernaryQuantizedWeight
 
     def fmt(attr):
@@ -57,7 +60,7 @@ def packed_format(layer) -> Optional[str]:
             return "ternary"
         return None
 
-    f = fmt("w_cheby")
+    f = fmt(getattr(layer, "_weight_attr", "w_cheby"))
     if f is None:
         return None
     if getattr(layer, "has_base", False) and fmt("w_base") != f:
@@ -67,13 +70,14 @@ def packed_format(layer) -> Optional[str]:
 
 def _key(layer, fmt):
     suffix = "_ternary" if fmt == "ternary" else "_quantized"
-    objs = [getattr(layer, "_w_cheby" + suffix, None), getattr(layer, "_w_base" + suffix, None),
+    attr = "_" + getattr(layer, "_weight_attr", "w_cheby")
+    objs = [getattr(layer, attr + suffix, None), getattr(layer, "_w_base" + suffix, None),
             getattr(layer, "bias", None) if layer.has_bias else None]
-    return tuple(id(o) for o in objs)
+    return tuple(id(o) for o in objs) + (layer._basis_params(),)
 
 
 class QLayerEngine:
-    """Owns a ``kans_qlayer`` handle built from a quantized ChebyKAN layer."""
+    """Owns a ``kans_qlayer`` handle built from a quantized KAN layer (ChebyKAN, FastKAN, BSplineKAN)."""
 
     def __init__(self, layer, fmt: str):
         self.fmt = fmt
@@ -82,14 +86,15 @@ class QLayerEngine:
         lib = device.get_metal_bridge()
         self.handle = ctypes.c_void_p()
         has_base, has_bias = int(bool(layer.has_base)), int(bool(layer.has_bias))
-        K = int(layer.degree)
+        K = int(layer._num_basis())
+        attr = "_" + layer._weight_attr
         bias = None
         if has_bias:
             bias = np.ascontiguousarray(layer.bias, dtype=np.float32)
         bias_ptr = bias.ctypes.data if bias is not None else None
         self.K = K
         if fmt in ("int4", "int8"):
-            w = layer._w_cheby_quantized
+            w = getattr(layer, attr + "_quantized")
             wb = layer._w_base_quantized if has_base else None
             arrs = [np.ascontiguousarray(w.qweight), np.ascontiguousarray(w.scales, dtype=np.float32),
                     np.ascontiguousarray(w.biases, dtype=np.float32)]
@@ -100,7 +105,7 @@ class QLayerEngine:
             device.check(getattr(lib, name)(self.d_in, self.d_out, K, has_base, has_bias, 64, *ptr, bias_ptr, DT_F32,
                                             ctypes.byref(self.handle)), name)
         else:
-            w = layer._w_cheby_ternary
+            w = getattr(layer, attr + "_ternary")
             wb = layer._w_base_ternary if has_base else None
             arrs = [np.ascontiguousarray(w.w_packed), np.ascontiguousarray(w.scales, dtype=np.float32)]
             barrs = ([np.ascontiguousarray(wb.w_packed), np.ascontiguousarray(wb.scales, dtype=np.float32)]
@@ -109,6 +114,15 @@ class QLayerEngine:
             device.check(lib.kans_qlayer_create_ternary(self.d_in, self.d_out, K, has_base, has_bias, 32, *ptr,
                                                         bias_ptr, DT_F32, ctypes.byref(self.handle)),
                          "kans_qlayer_create_ternary")
+        # the layer's basis (the same parameters its dense forward uses, _basis_params)
+        params = layer._basis_params()
+        if layer._basis == "rbf":
+            centers = np.ascontiguousarray(params[0], dtype=np.float32)
+            device.check(lib.kans_qlayer_set_rbf(self.handle, centers.ctypes.data, float(params[1])),
+                         "kans_qlayer_set_rbf")
+        elif layer._basis == "bspline":
+            device.check(lib.kans_qlayer_set_bspline(self.handle, int(params[0]), float(params[1]),
+                                                     float(params[2])), "kans_qlayer_set_bspline")
 
     def __del__(self):
         try:
@@ -119,6 +133,10 @@ class QLayerEngine:
 
     def current(self, layer) -> bool:
         return packed_format(layer) == self.fmt and _key(layer, self.fmt) == self.key
+
+    def fused(self, B: int) -> bool:
+        """Whether a forward of B rows runs on the fused packed-weight kernels (kans_qlayer_fused)."""
+        return B > 0 and device.get_metal_bridge().kans_qlayer_fused(self.handle, int(B)) == 1
 
     def forward_host(self, x: np.ndarray, out_dtype) -> np.ndarray:
         x = np.ascontiguousarray(x)
@@ -134,10 +152,11 @@ class QLayerEngine:
 
 
 def layer_engine(layer) -> Optional["QLayerEngine"]:
-    """The fused quantized engine of a Chebyshev layer that computes in fp16 after ``to_int8`` / ``to_int4`` /
-    ``to_ternary`` (cached on the layer, rebuilt when its packed weights change), else None."""
-    if getattr(layer, "_basis", "") != "cheby" or getattr(layer, "_quantized_from", None) != "float16" \
-            or layer._resolve_compute() != "float16":
+    """The fused quantized engine of a KAN layer (Chebyshev, RBF, B-spline) that computes in fp16 after
+    ``to_int8`` / ``to_int4`` / ``to_ternary`` (cached on the layer, rebuilt when its packed weights or basis
+    parameters change), else None."""
+    if getattr(layer, "_basis", "") not in ("cheby", "rbf", "bspline") \
+            or getattr(layer, "_quantized_from", None) != "float16" or layer._resolve_compute() != "float16":
         return None
     fmt = packed_format(layer)
     if fmt is None:

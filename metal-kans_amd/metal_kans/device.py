@@ -106,6 +106,9 @@ SIGNATURES = {
     "kans_qlayer_create_int8": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P, c_int, P]),
     "kans_qlayer_create_ternary": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P]),
     "kans_qlayer_destroy": (c_int, [P]),
+    "kans_qlayer_set_rbf": (c_int, [P, P, ctypes.c_float]),
+    "kans_qlayer_set_bspline": (c_int, [P, c_int, ctypes.c_float, ctypes.c_float]),
+    "kans_qlayer_fused": (c_int, [P, c_int]),
     "kans_qlayer_forward": (c_int, [P, P, c_int, c_long, P, c_int, c_long, c_int, P]),
     "kans_qlayer_forward_host": (c_int, [P, P, c_int, P, c_int, c_int]),
     "kans_gated_create": (c_int, [P, P, P, P]),

@@ -13,8 +13,10 @@ oracle on the oracle-dequantized weights:
 
 Shapes cover ragged D_in (the last feature block is partly padding, inside an
 affine group), ragged D_out (N-tile padding), several feature blocks per
-split, feature splits (few row tiles), K in {1, 2, 4}, with and without the
-base / bias branches, fp16 and fp32 inputs and fp32 / fp16 / bf16 outputs.
+split, feature splits (few row tiles), K in {1, 2, 4, 8} (Chebyshev) and {4, 8}
+(Gaussian RBF on uniform centres, cubic B-spline), with and without the base /
+bias branches, fp16 and fp32 inputs and fp32 / fp16 / bf16 outputs.  The same
+RBF / B-spline layers are checked through the decode GEMVs (B <= 32, every K).
 """
 import ctypes
 
@@ -51,7 +53,31 @@ def quantize(lib, fmt, W):
     return (p, s), O.dequantize_ternary(p, s, W.shape, 32)
 
 
-def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed):
+def basis_params(kind, K, rng=None, uniform=True):
+    """Oracle parameters of a layer of `kind` with K basis functions: RBF centres on [-1.5, 1.5] (uniform, or
+    moved off the grid) with the reference's inv_den = 1 / (2 h^2); B-spline G = K - 3 on [-1, 1]."""
+    if kind == "cheby":
+        return {"K": K}
+    if kind == "rbf":
+        c = np.linspace(-1.5, 1.5, K).astype(np.float32)
+        if not uniform:
+            c = c + np.linspace(0.0, 0.4, K).astype(np.float32) ** 2
+        h = 3.0 / (K - 1)
+        return {"grid": c.astype(np.float64), "inv_den": float(np.float32(1.0 / (2.0 * h * h)))}
+    G = K - 3
+    return {"G": G, "grid_min": -1.0, "inv_h": float(np.float32(G / 2.0))}
+
+
+def set_basis(lib, h, kind, params):
+    if kind == "rbf":
+        c = np.ascontiguousarray(params["grid"], np.float32)
+        assert lib.kans_qlayer_set_rbf(h, c.ctypes.data, params["inv_den"]) == 0, lib.kans_last_error()
+    elif kind == "bspline":
+        assert lib.kans_qlayer_set_bspline(h, params["G"], params["grid_min"], params["inv_h"]) == 0, \
+            lib.kans_last_error()
+
+
+def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed, kind="cheby", uniform=True):
     rng = np.random.default_rng(seed)
     W = rng.normal(0, 0.5 / np.sqrt(d_in * K), (d_out, d_in * K)).astype(np.float32)
     Wb = rng.normal(0, 0.5 / np.sqrt(d_in), (d_out, d_in)).astype(np.float32)
@@ -68,24 +94,29 @@ def make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed):
         rc = fn(d_in, d_out, K, int(base), int(bias), 64, *[ptr(a) for a in pw], *[ptr(a) for a in pb],
                 ptr(bv) if bias else None, 0, ctypes.byref(h))
     assert rc == 0, lib.kans_last_error()
-    return h, {"W": dw, "W_base": db, "bias": bv if bias else None, "K": K}
+    params = basis_params(kind, K, uniform=uniform)
+    set_basis(lib, h, kind, params)
+    return h, {"W": dw, "W_base": db, "bias": bv if bias else None, "K": K, "kind": kind, "params": params}
 
 
 def oracle(L, x):
     """float64 forward on the original inputs and the dequantized weights."""
-    return O.kan_forward("cheby", x, L["W"], L["W_base"], L["bias"], {"K": L["K"]})
+    return O.kan_forward(L.get("kind", "cheby"), x, L["W"], L["W_base"], L["bias"], L.get("params", {"K": L["K"]}))
 
 
-def _oracle_rounded(L, x):
-    """float64 forward with the fp16 MFMA operands: dequantized weights, T_k(clamp x) and SiLU(x) rounded to
-    fp16 (the basis evaluated from x in fp32, as the kernel does)."""
+def _oracle_rounded(L, x, weights16=True):
+    """float64 forward with the fp16 MFMA operands: the basis values and SiLU(x) (evaluated from x in fp32,
+    as the kernel does) rounded to fp16, and the dequantized weights rounded to fp16 too (prefill; the
+    decode GEMVs apply the group parameters in fp32 and feed the weights exactly: weights16=False)."""
     r16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)  # noqa: E731
+    rw = r16 if weights16 else (lambda a: np.asarray(a, np.float64))  # noqa: E731
     x32 = np.asarray(x, np.float32)
     B, d_in = x32.shape
-    phi = r16(O.cheby_basis(x32, L["K"], np.float32).reshape(B, -1))
-    y = phi @ r16(L["W"]).T
+    kind = L.get("kind", "cheby")
+    phi = r16(O.basis(kind, x32, L.get("params", {"K": L["K"]}), np.float32).reshape(B, -1))
+    y = phi @ rw(L["W"]).T
     if L["W_base"] is not None:
-        y += r16(O.silu(x32)) @ r16(L["W_base"]).T
+        y += r16(O.silu(x32)) @ rw(L["W_base"]).T
     if L["bias"] is not None:
         y += L["bias"].astype(np.float64)
     return y
@@ -105,7 +136,7 @@ def run(lib, h, x, d_out, y_dt="float32"):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
-@pytest.mark.parametrize("K", [1, 2, 4])
+@pytest.mark.parametrize("K", [1, 2, 4, 8])
 @pytest.mark.parametrize("base,bias", [(True, False), (False, True), (True, True)])
 @pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300), (600, 48, 33)])
 def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
@@ -121,6 +152,68 @@ def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
         assert e16 <= 2e-2 and eop <= 2e-3, (e16, eop)
         y2 = run(lib, h, x, d_out)
         np.testing.assert_array_equal(y.view(np.uint32), y2.view(np.uint32))
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+@pytest.mark.parametrize("kind,K", [("rbf", 8), ("rbf", 4), ("bspline", 8), ("bspline", 4)])
+@pytest.mark.parametrize("base,bias", [(True, True), (False, False)])
+@pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300)])
+def test_qlayer_prefill_bases(gpu, fmt, kind, K, base, bias, B, d_in, d_out):
+    """Quantized FastKAN (uniform centres: the RBF recurrence) and BSplineKAN layers on the fused prefill
+    kernel (K = 8: B-spline basis table), inputs beyond the grid included."""
+    lib = gpu
+    print(f"case {kind} K={K} {fmt} base={base} bias={bias} B={B} {d_in}->{d_out}", flush=True)
+    h, L = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=B + d_in + 3 * K, kind=kind)
+    try:
+        assert lib.kans_qlayer_fused(h, B) == 1
+        x = np.random.default_rng(K + d_out).uniform(-2.0, 2.0, (B, d_in)).astype(np.float32)
+        y = run(lib, h, x, d_out)
+        e16 = O.rel_err(y, oracle(L, x))
+        eop = O.rel_err(y, _oracle_rounded(L, x))
+        print(f"  rel err {e16:.2e} (16-bit bar), {eop:.2e} vs operand-rounded oracle")
+        assert e16 <= 2e-2 and eop <= 2e-3, (e16, eop)
+        y2 = run(lib, h, x, d_out)
+        np.testing.assert_array_equal(y.view(np.uint32), y2.view(np.uint32))
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+@pytest.mark.parametrize("kind,K,uniform", [("rbf", 8, True), ("rbf", 5, False), ("bspline", 8, True),
+                                            ("bspline", 6, True), ("cheby", 9, True)])
+def test_qlayer_decode_bases(gpu, fmt, kind, K, uniform):
+    """The decode GEMVs (B <= 32) for every basis and K: the activation basis (k_prep) evaluates the RBF and
+    B-spline functions; against the oracle with the fp16 basis operands and exact weights."""
+    lib = gpu
+    h, L = make_qlayer(lib, fmt, 90, 70, K, True, True, seed=K + 11, kind=kind, uniform=uniform)
+    try:
+        for B in (1, 2, 5, 32):
+            assert lib.kans_qlayer_fused(h, B) == 1
+            x = np.random.default_rng(B + K).uniform(-2.0, 2.0, (B, 90)).astype(np.float32)
+            y = run(lib, h, x, 70)
+            e16 = O.rel_err(y, oracle(L, x))
+            eop = O.rel_err(y, _oracle_rounded(L, x, weights16=False))
+            print(f"{kind} K={K} {fmt} B={B}: rel err {e16:.2e}, {eop:.2e} vs fp16-basis oracle")
+            assert e16 <= 2e-2 and eop <= 3e-4, (e16, eop)
+    finally:
+        lib.kans_qlayer_destroy(h)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "ternary"])
+@pytest.mark.parametrize("kind,K,uniform", [("rbf", 8, False), ("rbf", 6, True), ("bspline", 6, True)])
+def test_qlayer_prefill_bases_unsupported(gpu, fmt, kind, K, uniform):
+    """RBF on non-uniform centres and K outside {4, 8}: decode batches run, larger ones report
+    KANS_ERR_UNSUPPORTED (-5) and kans_qlayer_fused says so."""
+    lib = gpu
+    h, L = make_qlayer(lib, fmt, 40, 24, K, True, False, seed=2, kind=kind, uniform=uniform)
+    try:
+        assert lib.kans_qlayer_fused(h, 33) == 0 and lib.kans_qlayer_fused(h, 32) == 1
+        x = np.random.default_rng(0).uniform(-1, 1, (33, 40)).astype(np.float32)
+        y = np.zeros((33, 24), np.float32)
+        assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 0, y.ctypes.data, 0, 33) == -5
+        assert O.rel_err(run(lib, h, x[:8], 24), _oracle_rounded(L, x[:8], weights16=False)) <= 3e-4
     finally:
         lib.kans_qlayer_destroy(h)
 
@@ -147,8 +240,8 @@ def test_qlayer_prefill_io_dtypes(gpu, fmt):
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 def test_qlayer_prefill_rejects_unsupported_K(gpu, fmt):
-    """K outside {1, 2, 4}: the layer decodes small batches (any K) and reports KANS_ERR_UNSUPPORTED (-5) for
-    batches the prefill kernel would take."""
+    """K outside {1, 2, 4, 8}: the layer decodes small batches (any K) and reports KANS_ERR_UNSUPPORTED (-5)
+    for batches the prefill kernel would take."""
     lib = gpu
     rng = np.random.default_rng(0)
     h, L = make_qlayer(lib, fmt, 24, 40, 3, True, False, seed=1)
@@ -158,6 +251,7 @@ def test_qlayer_prefill_rejects_unsupported_K(gpu, fmt):
         assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 0, y.ctypes.data, 0, 33) == -5
         y8 = run(lib, h, x[:8], 40)          # decode path: any K
         assert O.rel_err(y8, _oracle_rounded(L, x[:8])) <= 2e-3
+        assert lib.kans_qlayer_fused(h, 33) == 0 and lib.kans_qlayer_fused(h, 8) == 1
     finally:
         lib.kans_qlayer_destroy(h)
 
@@ -185,13 +279,14 @@ def gated_oracle(specs, x, round16):
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 @pytest.mark.parametrize("B", [33, 300])
-@pytest.mark.parametrize("d,hdim,bias", [(64, 160, False), (96, 150, True), (256, 520, False)])
+@pytest.mark.parametrize("d,hdim,bias,K", [(64, 160, False, 4), (96, 150, True, 4), (256, 520, False, 4),
+                                           (96, 200, True, 8)])
 @pytest.mark.parametrize("round16", [1, 0])
-def test_gated_prefill(gpu, fmt, B, d, hdim, bias, round16):
+def test_gated_prefill(gpu, fmt, B, d, hdim, bias, K, round16):
     """gate|up in one launch (column-paired tile, SwiGLU epilogue), then down: against the oracle block."""
     lib = gpu
-    print(f"case gated {fmt} B={B} d={d} h={hdim} bias={bias} round16={round16}", flush=True)
-    blk, layers, specs = make_block(lib, fmt, d, hdim, bias=bias, seed=B + d)
+    print(f"case gated {fmt} B={B} d={d} h={hdim} bias={bias} K={K} round16={round16}", flush=True)
+    blk, layers, specs = make_block(lib, fmt, d, hdim, K=K, bias=bias, seed=B + d)
     try:
         x = np.random.default_rng(B).normal(0, 1, (B, d)).astype(np.float16)
         y = np.zeros((B, d), np.float16)
@@ -266,3 +361,37 @@ def test_python_gatedkan_prefill(gpu, quant):
              for k in (blk.gate_kan, blk.up_kan, blk.down_kan)]
     ref = gated_oracle(specs, x.reshape(-1, 96).astype(np.float64), 1)
     assert O.rel_err(out.reshape(-1, 96).astype(np.float32), ref) <= 2e-2
+
+
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+@pytest.mark.parametrize("kind", ["rbf", "bspline", "rbf5"])
+def test_python_quantized_fastkan_bsplinekan(gpu, quant, kind):
+    """FastKAN(...).half().to_<quant>() and BSplineKAN(...).half().to_<quant>() keep fp16 compute and run on
+    their packed weights: the decode GEMVs at B = 5 and the prefill kernel at B = 300 (K = 8); a 5-centre
+    FastKAN (no prefill kernel for K = 5) takes the packed path at B = 5 and the dequantized weights at
+    B = 300, equally correct."""
+    import metal_kans as mk
+    np.random.seed(8)
+    if kind == "bspline":
+        L = mk.BSplineKAN(72, 40, grid_size=5)
+    else:
+        L = mk.FastKAN(72, 40, num_centers=5 if kind == "rbf5" else 8, grid_range=(-2.0, 2.0))
+    L.bias = np.random.normal(0, 0.1, 40).astype(np.float32)
+    L.half()
+    getattr(mk, f"to_{quant}")(L)
+    params = ({"G": L.grid_size, "grid_min": float(L.grid_params[0]), "inv_h": float(L.grid_params[1])}
+              if kind == "bspline" else {"grid": np.asarray(L.grid, np.float64), "inv_den": L.inv_denominator})
+    spec = {"W": getattr(L, L._weight_attr), "W_base": L.w_base, "bias": L.bias.astype(np.float32),
+            "K": L._num_basis(), "kind": L._basis, "params": params}
+    for B in (5, 300):
+        x = np.random.default_rng(B).normal(0, 1, (B, 72)).astype(np.float32)
+        y = L(x)
+        assert y.dtype == np.float16 and y.shape == (B, 40)
+        eng = L.__dict__.get("_qlayer_engine")
+        assert eng is not None
+        assert eng.fused(B) == (B <= 32 or kind != "rbf5")
+        assert O.rel_err(y.astype(np.float32), oracle(spec, x)) <= 2e-2
+        if eng.fused(B):
+            # fp16 output: its own rounding is up to 2^-12 of |y| (the C-level tests above check fp32 outputs)
+            ref = _oracle_rounded(spec, x, weights16=B > 32)
+            assert O.rel_err(y.astype(np.float32), ref) <= (2e-3 if B > 32 else 1e-3)
