@@ -29,13 +29,16 @@ namespace kans {
 // data-dependent position) are not built.  Bases: Chebyshev for every such K;
 // the Gaussian RBF on uniform centres (the recurrence of BasisGen<BASIS_RBF_REC>)
 // and the cubic B-spline for K in {4, 8} (FastKAN's and BSplineKAN's default
-// K = 8).
+// K = 8), except INT8 B-spline at K = 8: with the code words of a whole block
+// in registers that kernel spills (measured 2.2x the dense fp16 kernel's time
+// on the dequantized weights, where the other K = 8 kernels take 1.08-1.20x).
 __host__ __device__ constexpr int qp_chunk_bytes(int qt) { return qt == 0 ? 4 : qt == 2 ? 8 : 2; }  // Q_INT4/TERN/INT8
 __host__ __device__ constexpr int qp_group(int qt) { return qt == 1 ? 32 : 64; }
 __host__ __device__ constexpr int qp_param_floats(int qt) { return qt == 1 ? 1 : 2; }
-inline bool qp_supported(int /*qt*/, int K, int basis = BASIS_CHEBY, int rbf_rec = 1) {
+inline bool qp_supported(int qt, int K, int basis = BASIS_CHEBY, int rbf_rec = 1) {
   if (basis == BASIS_CHEBY) return K == 1 || K == 2 || K == 4 || K == 8;
   if (basis == BASIS_RBF && !rbf_rec) return false;
+  if (basis == BASIS_BSPLINE && K == 8 && qt == 2 /* Q_INT8 */) return false;
   return K == 4 || K == 8;
 }
 

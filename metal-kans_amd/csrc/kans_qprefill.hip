@@ -812,7 +812,7 @@ static hipError_t qp_dispatch_k(const QPLaunch& L, const QPArgs& A, dim3 grid, h
     QP_K(2)
   }
   if constexpr (BASIS != BASIS_BSPLINE_TAB) QP_K(4)
-  if constexpr (BASIS != BASIS_BSPLINE) QP_K(8)
+  if constexpr (BASIS != BASIS_BSPLINE && !(QT == Q_INT8 && BASIS == BASIS_BSPLINE_TAB)) QP_K(8)
 #undef QP_K
   return hipErrorInvalidValue;
 }
