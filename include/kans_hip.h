@@ -300,8 +300,8 @@ int kans_qlayer_set_rbf(kans_qlayer* layer, const float* centers, float inv_deno
 int kans_qlayer_set_bspline(kans_qlayer* layer, int grid_size, float grid_min, float inv_h);
 /* 1 when a forward of B rows runs on the fused packed-weight kernels: B <= 32 always (decode GEMVs, every
  * basis and K); larger B when the prefill kernel is built for the layer's K and basis (Chebyshev K in
- * {1, 2, 4, 8}; RBF on uniform centres and B-spline K in {4, 8}); 0 when such a forward returns
- * KANS_ERR_UNSUPPORTED. */
+ * {1, 2, 4, 8}; RBF on uniform centres and B-spline K in {4, 8}, except INT8 B-spline at K = 8); 0 when
+ * such a forward returns KANS_ERR_UNSUPPORTED. */
 int kans_qlayer_fused(const kans_qlayer* layer, int B);
 /* device pointers; x_dtype / y_dtype any of KANS_DT_* (the prefill path reads fp16 / fp32 X, 16-byte aligned,
  * ldx % 8 == 0 and ldx >= round_up(D_in, 8)) */

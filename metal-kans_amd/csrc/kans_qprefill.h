@@ -31,7 +31,8 @@ namespace kans {
 // and the cubic B-spline for K in {4, 8} (FastKAN's and BSplineKAN's default
 // K = 8), except INT8 B-spline at K = 8: with the code words of a whole block
 // in registers that kernel spills (measured 2.2x the dense fp16 kernel's time
-// on the dequantized weights, where the other K = 8 kernels take 1.08-1.20x).
+// on the dequantized weights, where the other K = 8 kernels take 1.09-1.21x,
+// INT8 Chebyshev 1.38x).
 __host__ __device__ constexpr int qp_chunk_bytes(int qt) { return qt == 0 ? 4 : qt == 2 ? 8 : 2; }  // Q_INT4/TERN/INT8
 __host__ __device__ constexpr int qp_group(int qt) { return qt == 1 ? 32 : 64; }
 __host__ __device__ constexpr int qp_param_floats(int qt) { return qt == 1 ? 1 : 2; }

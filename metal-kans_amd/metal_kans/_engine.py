@@ -14,10 +14,10 @@ change.  A change is detected by
   finite-difference loops of the reference's tests are always seen.
 
 Two cases skip the content check of large arrays: a read-only array (numpy
-refuses in-place writes to it; the quantizers hand out their dequantized
-weights that way), and a layer whose weights were declared frozen with
-``layer.freeze_weights()`` (an explicit opt-in for inference loops, where the
-hash would cost ~5 ms per 37 MB of weights).
+refuses in-place writes to it and to every array it views), and a layer whose
+weights were declared frozen with ``layer.freeze_weights()`` (an explicit
+opt-in for inference loops, where the hash would cost ~5 ms per 37 MB of
+weights).
 """
 from __future__ import annotations
 
