@@ -27,6 +27,16 @@ struct DenseLaunch {
 // (kans_runtime.hip).
 bool kans_set_rbf_params(BasisParams& bp, const float* centers, float inv_den);
 
+// Host <-> device staging through pinned memory, the host copies split over worker threads and
+// overlapped with the DMAs (kans_staging.hip; call with the library lock held).
+// stage_in: `rows` rows of `row_bytes` bytes, contiguous in host src, into device rows of `pitch` bytes
+// (the tail of each row zeroed) through the pinned buffer `pin` (>= rows * pitch bytes).  Returns once
+// every DMA is enqueued on st; `pin` stays in use until st has passed them.
+int stage_in(void* dst, const void* src, size_t row_bytes, size_t pitch, long rows, void* pin, hipStream_t st);
+// stage_out: `bytes` from device src, after the work already on st, into host dst through the pinned
+// buffer `pin` (>= bytes).  Returns when dst holds them.
+int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t st);
+
 }  // namespace kans
 
 int kans_fail(int code, const char* fmt, ...);

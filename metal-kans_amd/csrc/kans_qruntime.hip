@@ -622,21 +622,28 @@ int kans_noalloc_setup(int device) {
 
 namespace {
 
-// Host-pointer forward through grow-only device staging: X [B][D_in] is copied
-// to rows of round_up(D_in, 8) elements (what the prefill kernel reads).
+// Host-pointer forward through grow-only device buffers and the library's
+// pinned staging (stage_in / stage_out): X [B][D_in] is copied to rows of
+// round_up(D_in, 8) elements (what the prefill kernel reads), the tail of
+// each row zeroed.
 template <typename Fwd>
 int host_forward(DevBuf& hx, DevBuf& hy, const void* X, int x_dtype, int D_in, void* Y, int y_dtype, int D_out, int B,
                  Fwd&& fwd) {
   hipStream_t st = kans_default_stream();
   const long ldx = round_up(D_in, 8);
   const size_t xe = dt_bytes(x_dtype), ye = dt_bytes(y_dtype);
+  const size_t xbytes = (size_t)B * ldx * xe, ybytes = (size_t)B * D_out * ye;
   int rc;
-  if ((rc = hx.reserve((size_t)B * ldx * xe)) || (rc = hy.reserve((size_t)B * D_out * ye))) return rc;
-  HIP_TRY(hipMemcpy2DAsync(hx.p, ldx * xe, X, (size_t)D_in * xe, (size_t)D_in * xe, B, hipMemcpyHostToDevice, st));
-  if ((rc = fwd(hx.p, ldx, hy.p))) return rc;
-  HIP_TRY(hipMemcpyAsync(Y, hy.p, (size_t)B * D_out * ye, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return 0;
+  if ((rc = hx.reserve(xbytes)) || (rc = hy.reserve(ybytes))) return rc;
+  void* pin_in;
+  void* pin_out;
+  if ((rc = kans_pinned_stage(0, xbytes, &pin_in)) || (rc = kans_pinned_stage(1, ybytes, &pin_out))) return rc;
+  if ((rc = stage_in(hx.p, X, (size_t)D_in * xe, (size_t)ldx * xe, B, pin_in, st))) return rc;
+  if ((rc = fwd(hx.p, ldx, hy.p))) {
+    (void)hipStreamSynchronize(st);  // the input DMAs read pin_in; finish them before another call reuses it
+    return rc;
+  }
+  return stage_out(Y, hy.p, ybytes, pin_out, st);
 }
 
 // INT4 / INT8 layer from the reference arrays: decode records and prefill

@@ -505,38 +505,37 @@ static int layer_forward_host_locked(kans_layer* L, const void* X, void* Y, int 
   int rc;
   if ((rc = L->x_d.reserve(xbytes))) return rc;
   if ((rc = L->y_d.reserve(ybytes))) return rc;
-  void* pin_in;
-  void* pin_out;
-  if (g_async) {
-    HIP_TRY(hipHostMalloc(&pin_in, xbytes, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc(&pin_out, ybytes, hipHostMallocDefault));
-  } else {
-    if ((rc = pinned_reserve(g_pin_in, xbytes))) return rc;
-    if ((rc = pinned_reserve(g_pin_out, ybytes))) return rc;
-    pin_in = g_pin_in.p;
-    pin_out = g_pin_out.p;
-  }
-  if (ldx == L->D_in) {
-    memcpy(pin_in, X, xbytes);
-  } else {  // pad each row with zeros to a multiple of 8 features
-    const size_t rb = (size_t)L->D_in * xes, pb = (size_t)ldx * xes;
-    for (int r = 0; r < B; ++r) {
-      memcpy((char*)pin_in + r * pb, (const char*)X + r * rb, rb);
-      memset((char*)pin_in + r * pb + rb, 0, pb - rb);
-    }
-  }
-  HIP_TRY(hipMemcpyAsync(L->x_d.p, pin_in, xbytes, hipMemcpyHostToDevice, g_stream));
   if ((rc = layer_reserve_locked(L, B))) return rc;
-  if ((rc = layer_launch_locked(L, L->x_d.p, ldx, L->y_d.p, L->D_out, B, g_stream, x_dtype, L->dtype))) return rc;
-  HIP_TRY(hipMemcpyAsync(pin_out, L->y_d.p, ybytes, hipMemcpyDeviceToHost, g_stream));
-  if (g_async) {
-    g_pending.push_back({pin_out, Y, ybytes});
+  // rows padded with zeros to a multiple of 8 features
+  const size_t row_in = (size_t)L->D_in * xes, pitch_in = (size_t)ldx * xes;
+  if (g_async) {  // per-call pinned buffers; the result lands in Y at metal_kan_sync
+    void* pin_in;
+    void* pin_out;
+    HIP_TRY(hipHostMalloc(&pin_in, xbytes, hipHostMallocDefault));
+    if (hipHostMalloc(&pin_out, ybytes, hipHostMallocDefault) != hipSuccess) {
+      (void)hipHostFree(pin_in);
+      return kans_fail(KANS_ERR_HIP, "hipHostMalloc of %zu bytes failed", ybytes);
+    }
+    // both buffers are freed at the next sync; Y is registered only once every step is enqueued
     g_pending.push_back({pin_in, nullptr, 0});
+    g_pending.push_back({pin_out, nullptr, 0});
+    const size_t out_idx = g_pending.size() - 1;
+    if ((rc = stage_in(L->x_d.p, X, row_in, pitch_in, B, pin_in, g_stream))) return rc;
+    if ((rc = layer_launch_locked(L, L->x_d.p, ldx, L->y_d.p, L->D_out, B, g_stream, x_dtype, L->dtype)))
+      return rc;
+    HIP_TRY(hipMemcpyAsync(pin_out, L->y_d.p, ybytes, hipMemcpyDeviceToHost, g_stream));
+    g_pending[out_idx].dst = Y;
+    g_pending[out_idx].bytes = ybytes;
     return 0;
   }
-  HIP_TRY(hipStreamSynchronize(g_stream));
-  memcpy(Y, pin_out, ybytes);
-  return 0;
+  if ((rc = pinned_reserve(g_pin_in, xbytes))) return rc;
+  if ((rc = pinned_reserve(g_pin_out, ybytes))) return rc;
+  if ((rc = stage_in(L->x_d.p, X, row_in, pitch_in, B, g_pin_in.p, g_stream))) return rc;
+  if ((rc = layer_launch_locked(L, L->x_d.p, ldx, L->y_d.p, L->D_out, B, g_stream, x_dtype, L->dtype))) {
+    (void)hipStreamSynchronize(g_stream);  // the input DMAs read g_pin_in; finish them before it is reused
+    return rc;
+  }
+  return stage_out(Y, L->y_d.p, ybytes, g_pin_out.p, g_stream);
 }
 
 static int sync_locked() {
@@ -1134,40 +1133,39 @@ int kans_chain_forward_host_ex(kans_chain* C, const void* X, int x_dtype, void* 
   if (B == 0) return 0;
   std::lock_guard<std::mutex> lk(g_mu);
   C->in_dtype = x_dtype;
-  const bool async = g_async != 0;
-  // async mode: kernels-only graph with per-call pinned staging (results land at metal_kan_sync)
-  int rc = chain_graph_ready(C, B, !async);
+  // the kernels-only graph; the host arrays are staged around it (stage_in / stage_out)
+  int rc = chain_graph_ready(C, B, false);
   if (rc) return rc;
   const size_t es = dtype_size(C->dtype);
   const size_t xes = dtype_size(x_dtype);
   const int D0 = C->layers[0]->D_in;
   const size_t in_bytes = (size_t)B * C->ld_in * xes, out_bytes = (size_t)B * C->ld_out * es;
-  void* pin_in = C->pin_in.p;
-  void* pin_out = C->pin_out.p;
-  if (async) {
+  const size_t row_in = (size_t)D0 * xes, pitch_in = (size_t)C->ld_in * xes;
+  if (g_async) {  // per-call pinned buffers; the result lands in Y at metal_kan_sync
+    void* pin_in;
+    void* pin_out;
     HIP_TRY(hipHostMalloc(&pin_in, in_bytes, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault));
-  }
-  if (C->ld_in == D0) {
-    memcpy(pin_in, X, (size_t)B * D0 * xes);
-  } else {
-    for (int r = 0; r < B; ++r) {
-      memcpy((char*)pin_in + (size_t)r * C->ld_in * xes, (const char*)X + (size_t)r * D0 * xes, (size_t)D0 * xes);
-      memset((char*)pin_in + ((size_t)r * C->ld_in + D0) * xes, 0, (size_t)(C->ld_in - D0) * xes);
+    if (hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault) != hipSuccess) {
+      (void)hipHostFree(pin_in);
+      return kans_fail(KANS_ERR_HIP, "hipHostMalloc of %zu bytes failed", out_bytes);
     }
-  }
-  if (async) {
-    HIP_TRY(hipMemcpyAsync(C->x_d.p, pin_in, in_bytes, hipMemcpyHostToDevice, g_stream));
+    // both buffers are freed at the next sync; Y is registered only once every step is enqueued
+    g_pending.push_back({pin_in, nullptr, 0});
+    g_pending.push_back({pin_out, nullptr, 0});
+    const size_t out_idx = g_pending.size() - 1;
+    if ((rc = stage_in(C->x_d.p, X, row_in, pitch_in, B, pin_in, g_stream))) return rc;
     HIP_TRY(hipGraphLaunch(C->exec, g_stream));
     HIP_TRY(hipMemcpyAsync(pin_out, C->y_d.p, out_bytes, hipMemcpyDeviceToHost, g_stream));
-    g_pending.push_back({pin_out, Y, out_bytes});
-    g_pending.push_back({pin_in, nullptr, 0});
+    g_pending[out_idx].dst = Y;
+    g_pending[out_idx].bytes = out_bytes;
     return 0;
   }
-  HIP_TRY(hipGraphLaunch(C->exec, g_stream));
-  HIP_TRY(hipStreamSynchronize(g_stream));
-  memcpy(Y, pin_out, out_bytes);
-  return 0;
+  if ((rc = stage_in(C->x_d.p, X, row_in, pitch_in, B, C->pin_in.p, g_stream))) return rc;
+  if (hipGraphLaunch(C->exec, g_stream) != hipSuccess) {
+    (void)hipStreamSynchronize(g_stream);  // the input DMAs read pin_in; finish them before it is reused
+    return kans_fail(KANS_ERR_HIP, "hipGraphLaunch failed");
+  }
+  return stage_out(Y, C->y_d.p, out_bytes, C->pin_out.p, g_stream);
 }
 
 int kans_chain_forward_host(kans_chain* C, const void* X, void* Y, int B) {
@@ -1482,37 +1480,37 @@ int kans_gated_dense_forward_host(kans_gated_dense* D, const void* X, int x_dtyp
   if (B == 0) return 0;
   std::lock_guard<std::mutex> lk(g_mu);
   D->in_dtype = x_dtype;
-  const bool async = g_async != 0;
-  int rc = dgated_graph_ready(D, B, !async);
+  // the kernels-only graph; the host arrays are staged around it (stage_in / stage_out)
+  int rc = dgated_graph_ready(D, B, false);
   if (rc) return rc;
   const size_t es = dtype_size(D->dtype), xes = dtype_size(x_dtype);
   const size_t in_bytes = (size_t)B * D->ld_in * xes, out_bytes = (size_t)B * D->ld_out * es;
-  void* pin_in = D->pin_in.p;
-  void* pin_out = D->pin_out.p;
-  if (async) {
+  const size_t row_in = (size_t)D->d * xes, pitch_in = (size_t)D->ld_in * xes;
+  if (g_async) {  // per-call pinned buffers; the result lands in Y at metal_kan_sync
+    void* pin_in;
+    void* pin_out;
     HIP_TRY(hipHostMalloc(&pin_in, in_bytes, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault));
-  }
-  if (D->ld_in == D->d) {
-    memcpy(pin_in, X, (size_t)B * D->d * xes);
-  } else {
-    for (int r = 0; r < B; ++r) {
-      memcpy((char*)pin_in + (size_t)r * D->ld_in * xes, (const char*)X + (size_t)r * D->d * xes, (size_t)D->d * xes);
-      memset((char*)pin_in + ((size_t)r * D->ld_in + D->d) * xes, 0, (size_t)(D->ld_in - D->d) * xes);
+    if (hipHostMalloc(&pin_out, out_bytes, hipHostMallocDefault) != hipSuccess) {
+      (void)hipHostFree(pin_in);
+      return kans_fail(KANS_ERR_HIP, "hipHostMalloc of %zu bytes failed", out_bytes);
     }
-  }
-  if (async) {
-    HIP_TRY(hipMemcpyAsync(D->x_d.p, pin_in, in_bytes, hipMemcpyHostToDevice, g_stream));
+    // both buffers are freed at the next sync; Y is registered only once every step is enqueued
+    g_pending.push_back({pin_in, nullptr, 0});
+    g_pending.push_back({pin_out, nullptr, 0});
+    const size_t out_idx = g_pending.size() - 1;
+    if ((rc = stage_in(D->x_d.p, X, row_in, pitch_in, B, pin_in, g_stream))) return rc;
     HIP_TRY(hipGraphLaunch(D->exec, g_stream));
     HIP_TRY(hipMemcpyAsync(pin_out, D->y_d.p, out_bytes, hipMemcpyDeviceToHost, g_stream));
-    g_pending.push_back({pin_out, Y, out_bytes});
-    g_pending.push_back({pin_in, nullptr, 0});
+    g_pending[out_idx].dst = Y;
+    g_pending[out_idx].bytes = out_bytes;
     return 0;
   }
-  HIP_TRY(hipGraphLaunch(D->exec, g_stream));
-  HIP_TRY(hipStreamSynchronize(g_stream));
-  memcpy(Y, pin_out, out_bytes);
-  return 0;
+  if ((rc = stage_in(D->x_d.p, X, row_in, pitch_in, B, D->pin_in.p, g_stream))) return rc;
+  if (hipGraphLaunch(D->exec, g_stream) != hipSuccess) {
+    (void)hipStreamSynchronize(g_stream);  // the input DMAs read pin_in; finish them before it is reused
+    return kans_fail(KANS_ERR_HIP, "hipGraphLaunch failed");
+  }
+  return stage_out(Y, D->y_d.p, out_bytes, D->pin_out.p, g_stream);
 }
 
 // Mean ms per graph replay on the block's device buffers (include_copies: with the pinned H2D / D2H copies;
