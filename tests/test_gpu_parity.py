@@ -686,6 +686,70 @@ def test_full_size_sampled_rows(gpu, kind, K):
     assert O.rel_err(y[rows], y_ref) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_host_staging_large_ragged(gpu, dtype):
+    """Host arrays large enough for the pipelined, multi-threaded staging (several ~2 MB pieces, a short
+    last one) with D_in = 1001, so every staged row is padded to 1008 columns: the synchronous and the
+    async host call equal the device-array forward of the same layer and batch bit for bit, and sampled
+    rows match the float64 oracle."""
+    import bench
+    import metal_kans as mk
+    B, d_in, d_out = 4099, 1001, 515
+    L = make_layer(mk, "cheby", d_in, d_out, 4, seed=5)
+    rng = np.random.default_rng(7)
+    x = rng.uniform(-1.1, 1.1, (B, d_in)).astype(np.float32)
+    rows = np.sort(rng.choice(B, 32, replace=False))
+    y_ref = oracle_of(L, x[rows])
+    if dtype == "float16":
+        L.half()
+        x = x.astype(np.float16)
+    y = L(x)
+    mk.set_async(True)
+    try:
+        ya = L(x)
+        mk.sync()
+    finally:
+        mk.set_async(False)
+    np.testing.assert_array_equal(ya, y)
+    ldx = 1008
+    xp = np.zeros((B, ldx), x.dtype)
+    xp[:, :d_in] = x
+    xd, yd = bench.DevBuf(gpu, xp.nbytes), bench.DevBuf(gpu, y.nbytes)
+    try:
+        xd.upload(xp)
+        assert gpu.kans_layer_forward(L._engine().handle, xd.p, ldx, yd.p, d_out, B, None) == 0, gpu.kans_last_error()
+        assert gpu.kans_synchronize() == 0
+        y_dev = yd.download(np.empty_like(y))
+    finally:
+        xd.free()
+        yd.free()
+    np.testing.assert_array_equal(y_dev, y)
+    assert O.rel_err(y[rows].astype(np.float64), y_ref) <= TOL[dtype]
+
+
+def test_host_staging_large_chain(gpu):
+    """The chain's host path through the same staging (fp32 x of 16.5 MB, D_in = 1001): async equals
+    sync bit for bit, sampled rows match the float64 oracle chain."""
+    import metal_kans as mk
+    np.random.seed(11)
+    net = mk.MetalKAN([1001, 96, 40], basis_type="cheby", degree=4)
+    rng = np.random.default_rng(12)
+    x = rng.uniform(-1, 1, (4099, 1001)).astype(np.float32)
+    y = net(x)
+    mk.set_async(True)
+    try:
+        ya = net(x)
+        mk.sync()
+    finally:
+        mk.set_async(False)
+    np.testing.assert_array_equal(ya, y)
+    rows = np.sort(rng.choice(4099, 24, replace=False))
+    h = x[rows].astype(np.float64)
+    for L in net.layers:
+        h = oracle_of(L, h)
+    assert O.rel_err(y[rows].astype(np.float64), h) <= 1e-4
+
+
 # ---------------------------------------------------------------- GatedKAN on device activations
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("B", [1, 40, 300])
