@@ -1131,12 +1131,20 @@ __global__ void __launch_bounds__(256) k_qgemv_wg(QMatDev m0, QMatDev m1, int rg
   // three separate arrays per ring (not one indexed array): the compiler then
   // sees that reads of one stage do not depend on the copies into another,
   // and waits only for this stage's copies
-  __shared__ uint4 sa0[FR * 64], sa1[FR * 64], sa2[FR * 64];
-  __shared__ float2 ss0[32], ss1[32], ss2[32];
   // PR: each wave's group parameters (its records' 1 KB parameter block) take
   // the same route, so the register ring holds only code words (ternary MT = 2:
-  // 174 -> 150 registers, three waves per SIMD instead of two)
-  __shared__ float4 sp0[PR ? 4 * 64 : 1], sp1[PR ? 4 * 64 : 1], sp2[PR ? 4 * 64 : 1];
+  // 174 -> 150 registers, three waves per SIMD instead of two).  They sit in
+  // the same stage array as the activation fragments, after them: with a
+  // separate parameter array per stage the compiler could not tell the
+  // parameter reads of stage c from the copies in flight into stage c + 1, and
+  // made their first use wait for those copies (ternary: a vmcnt wait in the
+  // middle of every superchunk's multiply, which drained the ring).
+  constexpr int SPO = FR * 64;  // uint4 offset of the parameter blocks in a stage
+  __shared__ uint4 sa0[SPO + (PR ? 4 * 64 : 0)], sa1[SPO + (PR ? 4 * 64 : 0)], sa2[SPO + (PR ? 4 * 64 : 0)];
+  __shared__ float2 ss0[32], ss1[32], ss2[32];
+  float4* const sp0 = reinterpret_cast<float4*>(sa0 + SPO);
+  float4* const sp1 = reinterpret_cast<float4*>(sa1 + SPO);
+  float4* const sp2 = reinterpret_cast<float4*>(sa2 + SPO);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ks = blockIdx.x % ksplit;
