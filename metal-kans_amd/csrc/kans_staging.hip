@@ -18,10 +18,26 @@
 // holds the library lock; the calling thread also copies pieces whenever it
 // would otherwise wait, so the transfer completes even if no worker thread
 // could be started.  Transfers below kThreadedBytes take one copy and one DMA.
+//
+// The caller's output array is often freshly allocated (numpy's np.empty of a
+// large array is a fresh anonymous mapping), so the output copy spends most of
+// its time in first-touch page faults.  stage_out asks for transparent huge
+// pages on the page-aligned interior of the output first (madvise, a hint: it
+// changes no contents and is ignored for file-backed memory or where the
+// system disables them) and copies with up to kStageOutThreads threads.
+// Measured on the GPU box (16 CPUs, THP in madvise mode), 33.5 MB from pinned
+// memory into freshly malloc'ed memory: 4 threads 2.8 ms, with the hint 1.1 ms;
+// 8 threads 1.5 / 1.0 ms.  Copies into pinned memory saturate at 4 threads
+// (0.44 ms for 33.5 MB).
 #include "kans_api_internal.h"
+
+#include <sched.h>
+#include <sys/mman.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
+#include <cstdint>
 #include <cstring>
 #include <memory>
 #include <system_error>
@@ -34,6 +50,31 @@ namespace {
 constexpr size_t kPieceBytes = size_t(2) << 20;
 constexpr size_t kThreadedBytes = size_t(4) << 20;
 constexpr int kStageThreads = 4;
+constexpr int kStageOutThreads = 8;
+
+// CPUs this process may run on (its affinity mask), at least 1.
+int cpu_share() {
+  static const int n = [] {
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    if (sched_getaffinity(0, sizeof set, &set) == 0 && CPU_COUNT(&set) > 0) return (int)CPU_COUNT(&set);
+    const unsigned h = std::thread::hardware_concurrency();
+    return h > 0 ? (int)h : 1;
+  }();
+  return n;
+}
+
+// Worker threads for a transfer of n pieces: at most `cap`, at most one per piece, and leaving half of
+// the process's CPUs to the rest of the program.
+int workers_for(int n, int cap) { return std::max(1, std::min({cap, n, cpu_share() / 2})); }
+
+void hint_huge_pages(void* dst, size_t bytes) {
+  const long pg = sysconf(_SC_PAGESIZE);
+  if (pg <= 0) return;
+  const uintptr_t a = ((uintptr_t)dst + (uintptr_t)pg - 1) & ~((uintptr_t)pg - 1);
+  const uintptr_t e = ((uintptr_t)dst + bytes) & ~((uintptr_t)pg - 1);
+  if (e > a) (void)madvise((void*)a, e - a, MADV_HUGEPAGE);
+}
 
 // Pieces of `rows` rows of `pitch` bytes: piece k is rows [r0(k), r1(k)).
 struct Pieces {
@@ -108,7 +149,7 @@ int stage_in(void* dst, const void* src, size_t row_bytes, size_t pitch, long ro
     done[k].store(1, std::memory_order_release);
   };
   std::vector<std::thread> th;
-  start_workers(th, std::min(kStageThreads, P.n), [&] {
+  start_workers(th, workers_for(P.n, kStageThreads), [&] {
     for (int k; (k = next.fetch_add(1)) < P.n;) copy_piece(k);
   });
   hipError_t err = hipSuccess;
@@ -145,6 +186,7 @@ int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t s
   const Pieces P((long)bytes, 1);  // one-byte rows: pieces of kPieceBytes
   int rc = piece_events(P.n);
   if (rc) return rc;
+  hint_huge_pages(d, bytes);
   for (int k = 0; k < P.n; ++k) {
     hipError_t e = hipMemcpyAsync(p + P.r0(k), s + P.r0(k), (size_t)(P.r1(k) - P.r0(k)), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipEventRecord(g_piece_events[k], st);
@@ -166,7 +208,7 @@ int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t s
     }
   };
   std::vector<std::thread> th;
-  start_workers(th, std::min(kStageThreads, P.n), drain);
+  start_workers(th, workers_for(P.n, kStageOutThreads), drain);
   hipError_t err = hipSuccess;
   for (int k = 0; k < P.n; ++k) {
     if (err == hipSuccess) err = hipEventSynchronize(g_piece_events[k]);
