@@ -4,6 +4,7 @@
 #include "kans_common.h"
 #include "../../include/kans_hip.h"
 #include <mutex>
+#include <vector>
 
 namespace kans {
 
@@ -36,6 +37,20 @@ int stage_in(void* dst, const void* src, size_t row_bytes, size_t pitch, long ro
 // stage_out: `bytes` from device src, after the work already on st, into host dst through the pinned
 // buffer `pin` (>= bytes).  Returns when dst holds them.
 int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t st);
+// The same in two parts, for transfers from several streams: stage_out_enqueue adds the device -> pinned
+// copies of one range (after the work already on st) to `out`; stage_out_drain waits for the pieces in
+// the order they were added and copies each into host memory as it lands.
+struct StagedOut {
+  struct Piece {
+    char* dst;
+    const char* pin;
+    size_t bytes;
+  };
+  std::vector<Piece> pieces;
+  size_t bytes = 0;
+};
+int stage_out_enqueue(StagedOut& out, void* dst, const void* src, size_t bytes, void* pin, hipStream_t st);
+int stage_out_drain(StagedOut& out);
 
 }  // namespace kans
 

@@ -172,55 +172,84 @@ int stage_in(void* dst, const void* src, size_t row_bytes, size_t pitch, long ro
   return 0;
 }
 
-int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t st) {
+int stage_out_enqueue(StagedOut& out, void* dst, const void* src, size_t bytes, void* pin, hipStream_t st) {
   if (bytes == 0) return 0;
   char* p = (char*)pin;
   char* d = (char*)dst;
   const char* s = (const char*)src;
-  if (bytes < kThreadedBytes) {
-    HIP_TRY(hipMemcpyAsync(p, s, bytes, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
-    memcpy(d, p, bytes);
-    return 0;
-  }
   const Pieces P((long)bytes, 1);  // one-byte rows: pieces of kPieceBytes
-  int rc = piece_events(P.n);
+  const int base = (int)out.pieces.size();
+  int rc = piece_events(base + P.n);
   if (rc) return rc;
-  hint_huge_pages(d, bytes);
+  if (bytes >= kThreadedBytes) hint_huge_pages(d, bytes);
+  out.bytes += bytes;
   for (int k = 0; k < P.n; ++k) {
-    hipError_t e = hipMemcpyAsync(p + P.r0(k), s + P.r0(k), (size_t)(P.r1(k) - P.r0(k)), hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipEventRecord(g_piece_events[k], st);
+    const size_t len = (size_t)(P.r1(k) - P.r0(k));
+    hipError_t e = hipMemcpyAsync(p + P.r0(k), s + P.r0(k), len, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipEventRecord(g_piece_events[base + k], st);
     if (e != hipSuccess) {
       (void)hipStreamSynchronize(st);
       return kans_fail(KANS_ERR_HIP, "enqueueing a staged output piece failed: %s", hipGetErrorString(e));
     }
+    out.pieces.push_back({d + P.r0(k), p + P.r0(k), len});
+  }
+  return 0;
+}
+
+int stage_out_drain(StagedOut& out) {
+  const int n = (int)out.pieces.size();
+  if (n == 0) return 0;
+  if (out.bytes < kThreadedBytes) {  // small: wait for everything, one copy per piece
+    hipError_t e = hipSuccess;
+    for (int k = 0; k < n && e == hipSuccess; ++k) e = hipEventSynchronize(g_piece_events[k]);
+    if (e != hipSuccess) return kans_fail(KANS_ERR_HIP, "hipEventSynchronize: %s", hipGetErrorString(e));
+    for (const auto& pc : out.pieces) memcpy(pc.dst, pc.pin, pc.bytes);
+    out.pieces.clear();
+    out.bytes = 0;
+    return 0;
   }
   // ready[k]: 0 in flight, 1 in pinned memory, 2 abandoned (an event wait failed)
-  std::unique_ptr<std::atomic<int>[]> ready(new std::atomic<int>[P.n]);
-  for (int k = 0; k < P.n; ++k) ready[k].store(0, std::memory_order_relaxed);
+  std::unique_ptr<std::atomic<int>[]> ready(new std::atomic<int>[n]);
+  for (int k = 0; k < n; ++k) ready[k].store(0, std::memory_order_relaxed);
   std::atomic<int> next{0};
   auto drain = [&] {
-    for (int k; (k = next.fetch_add(1)) < P.n;) {
+    for (int k; (k = next.fetch_add(1)) < n;) {
       int r;
       while ((r = ready[k].load(std::memory_order_acquire)) == 0) std::this_thread::yield();
       if (r != 1) continue;
-      memcpy(d + P.r0(k), p + P.r0(k), (size_t)(P.r1(k) - P.r0(k)));
+      memcpy(out.pieces[k].dst, out.pieces[k].pin, out.pieces[k].bytes);
     }
   };
   std::vector<std::thread> th;
-  start_workers(th, workers_for(P.n, kStageOutThreads), drain);
+  start_workers(th, workers_for(n, kStageOutThreads), drain);
   hipError_t err = hipSuccess;
-  for (int k = 0; k < P.n; ++k) {
+  for (int k = 0; k < n; ++k) {
     if (err == hipSuccess) err = hipEventSynchronize(g_piece_events[k]);
     ready[k].store(err == hipSuccess ? 1 : 2, std::memory_order_release);
   }
   drain();  // the calling thread copies whatever pieces are still unclaimed
   for (auto& t : th) t.join();
+  out.pieces.clear();
+  out.bytes = 0;
   if (err != hipSuccess) {
-    (void)hipStreamSynchronize(st);
+    (void)hipDeviceSynchronize();  // the pieces' streams may still write the pinned buffer
     return kans_fail(KANS_ERR_HIP, "hipEventSynchronize on a staged output piece failed: %s", hipGetErrorString(err));
   }
   return 0;
+}
+
+int stage_out(void* dst, const void* src, size_t bytes, void* pin, hipStream_t st) {
+  if (bytes == 0) return 0;
+  if (bytes < kThreadedBytes) {
+    HIP_TRY(hipMemcpyAsync(pin, src, bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    memcpy(dst, pin, bytes);
+    return 0;
+  }
+  StagedOut out;
+  int rc = stage_out_enqueue(out, dst, src, bytes, pin, st);
+  if (rc) return rc;
+  return stage_out_drain(out);
 }
 
 }  // namespace kans

@@ -689,12 +689,13 @@ def test_full_size_sampled_rows(gpu, kind, K):
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
 def test_host_staging_large_ragged(gpu, dtype):
     """Host arrays large enough for the pipelined, multi-threaded staging (several ~2 MB pieces, a short
-    last one) with D_in = 1001, so every staged row is padded to 1008 columns: the synchronous and the
-    async host call equal the device-array forward of the same layer and batch bit for bit, and sampled
-    rows match the float64 oracle."""
+    last one) and for the chunked synchronous forward (four row chunks of whole 256-row tiles, the last
+    one ragged: 3 x 2304 + 1283 rows) with D_in = 1001, so every staged row is padded to 1008 columns:
+    the synchronous and the async host call equal the device-array forward of the same layer and batch
+    bit for bit, and sampled rows match the float64 oracle."""
     import bench
     import metal_kans as mk
-    B, d_in, d_out = 4099, 1001, 515
+    B, d_in, d_out = 8195, 1001, 515
     L = make_layer(mk, "cheby", d_in, d_out, 4, seed=5)
     rng = np.random.default_rng(7)
     x = rng.uniform(-1.1, 1.1, (B, d_in)).astype(np.float32)
