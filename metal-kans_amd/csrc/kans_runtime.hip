@@ -511,8 +511,8 @@ static int layer_forward_locked(kans_layer* L, const void* X, long ldx, void* Y,
 // configurations without a feature split are chunked (no workspace is shared
 // by chunk kernels that may run at the same time).  Chunks are whole 256-row
 // tiles.  Measured on one MI355X, FastKAN fp16 16384 x 1024 -> 1024 from and
-// into host arrays: 2.11 -> 1.71 ms per call (the C entry point, output array
-// reused), 2.84 -> 1.94 ms through FastKAN.__call__ (a fresh output array).
+// into host arrays: 2.06 -> 1.54 ms per call (the C entry point, output array
+// reused), 2.87 -> 1.92 ms through FastKAN.__call__ (a fresh output array).
 constexpr size_t kChunkedBytes = size_t(16) << 20;  // x + y bytes from which a host forward is chunked
 constexpr int kHostChunks = 4;
 static std::vector<hipEvent_t> g_chunk_events;  // grow-only (library lock)
