@@ -347,11 +347,12 @@ long long kans_gated_stream_bytes(const kans_gated* block, int B);
  * identical results.  Returns the previous setting (no reference counterpart: a tuning and test
  * switch). */
 int kans_gated_set_fused_swiglu(int on);
-/* At B <= 2 with the fused SwiGLU epilogue, the gate|up GEMV computes the basis of x itself, each
- * wave for its own range of the reduction axis in LDS (on = 1, the default: 3 launches per block);
- * on = 0 runs the separate basis kernel first.  Both give identical results.  Returns the previous
- * setting (no reference counterpart: a tuning and test switch). */
-int kans_decode_set_pre_basis(int on);
+/* With the fused SwiGLU epilogue, the gate|up GEMV can compute the basis of x itself, each wave
+ * for its own range of the reduction axis in LDS (3 launches per block instead of 4): mode 1 (the
+ * default) does so at B = 1, mode 2 at B <= 2, mode 0 never (the separate basis kernel runs
+ * first).  All modes give identical results.  Returns the previous mode, or -1 for a mode outside
+ * 0..2 (no reference counterpart: a tuning and test switch). */
+int kans_decode_set_pre_basis(int mode);
 /* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
  * non-temporal.  Automatic loads INT4 and ternary records non-temporally and INT8 records with plain
  * loads, the faster form for each when a model's weights stream from HBM on every decode step.

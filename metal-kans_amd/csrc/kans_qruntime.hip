@@ -60,8 +60,13 @@ constexpr int kMaxDecodeB = 32;
 // GEMV's epilogue (QEPI_SWIGLU) at B <= 2, k_swiglu_basis above -- instead of
 // k_qswiglu + k_prep.
 bool g_fused_swiglu = true;
-// In-kernel basis of x in the B <= 2 gate|up GEMV (kans_decode_set_pre_basis).
-bool g_pre_basis = true;
+// In-kernel basis of x in the gate|up GEMV (kans_decode_set_pre_basis): 0 never,
+// 1 at B = 1, 2 at B <= 2.  At B = 2 the waves' longer basis phase (two rows)
+// outweighs the launch it saves: cfg5 block at B = 2, INT4 93.5 against
+// 87.2 us with k_prep, ternary 68.4 / 64.5, INT8 150.9 / 149.0; at B = 1 it
+// gains (INT4 82.1 / 82.8, ternary 60.1 / 61.6, INT8 141.8 / 144.8; one box,
+// three runs each).
+int g_pre_basis = 1;
 
 int mp_of(int B) { return B <= 16 ? 16 : 32; }
 
@@ -489,9 +494,9 @@ int gated_decode(kans_gated* G, const void* X, int x_dtype, long ldx, void* Y, i
   const int h = g->D_out;
   int rc;
   const int nt = use_nt(g->quant);
-  // B <= 2 with the fused epilogue: the gate|up GEMV computes the basis of x
-  // itself (no k_prep launch) when its LDS slices fit
-  if (g_fused_swiglu && g_pre_basis && B <= kSmallB && ks1 <= kMaxEpiSplit &&
+  // B = 1 (g_pre_basis) with the fused epilogue: the gate|up GEMV computes the
+  // basis of x itself (no k_prep launch) when its LDS slices fit
+  if (g_fused_swiglu && B <= (g_pre_basis == 2 ? kSmallB : g_pre_basis == 1 ? 1 : 0) && ks1 <= kMaxEpiSplit &&
       qgemv_pre_fits(g->quant, B, g->C_tot, ks1, QEPI_SWIGLU)) {
     QEpi e1;
     e1.kind = QEPI_SWIGLU;
@@ -851,8 +856,9 @@ int kans_gated_set_fused_swiglu(int on) {
 
 int kans_decode_set_pre_basis(int on) {
   std::lock_guard<std::mutex> lk(kans_mutex());
-  const int prev = g_pre_basis ? 1 : 0;
-  g_pre_basis = on != 0;
+  if (on < 0 || on > 2) return kans_fail(KANS_ERR_ARG, "pre-basis mode %d not in 0..2", on);
+  const int prev = g_pre_basis;
+  g_pre_basis = on;
   return prev;
 }
 

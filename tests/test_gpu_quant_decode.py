@@ -320,10 +320,11 @@ PRE_CFGS = [  # d, h, K and base branch of gate / up
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("cfg", PRE_CFGS, ids=lambda c: "d{}h{}K{}b{}".format(*c[:3], int(c[3])))
 def test_gated_pre_basis_matches_kprep(gpu, fmt, cfg):
-    """At B <= 2 the gate|up GEMV computes the basis of x itself, each wave for its own superchunk
-    range in LDS (kans_decode_set_pre_basis(1), the default).  It must equal the separate basis
-    kernel (k_prep) bit for bit, for every input dtype, with and without the base branch, K = 1 to
-    32 (a feature's basis values split across two waves' ranges), and on a repeated call."""
+    """The gate|up GEMV can compute the basis of x itself, each wave for its own superchunk range
+    in LDS (kans_decode_set_pre_basis: mode 1, the default, at B = 1; mode 2 at B <= 2).  It must
+    equal the separate basis kernel (k_prep, mode 0) bit for bit, for every input dtype, with and
+    without the base branch, K = 1 to 32 (a feature's basis values split across two waves'
+    ranges), and on a repeated call."""
     lib = gpu
     d, hdim, K, base = cfg
     layers = []
@@ -339,7 +340,7 @@ def test_gated_pre_basis_matches_kprep(gpu, fmt, cfg):
                   DT_BF16: (x32.view(np.uint32) >> 16).astype(np.uint16)}
             for xdt, x in xs.items():
                 outs = []
-                for pre in (1, 0, 1):
+                for pre in (2, 0, 1):
                     prev = lib.kans_decode_set_pre_basis(pre)
                     try:
                         y = np.full((B, d), np.nan, np.float32)
