@@ -299,9 +299,10 @@ int kans_qlayer_destroy(kans_qlayer* layer);
 int kans_qlayer_set_rbf(kans_qlayer* layer, const float* centers, float inv_denominator);
 int kans_qlayer_set_bspline(kans_qlayer* layer, int grid_size, float grid_min, float inv_h);
 /* 1 when a forward of B rows runs on the fused packed-weight kernels: B <= 32 always (decode GEMVs, every
- * basis and K); larger B when the prefill kernel is built for the layer's K and basis (Chebyshev K in
- * {1, 2, 4, 8}; RBF on uniform centres and B-spline K in {4, 8}, except INT8 B-spline at K = 8); 0 when
- * such a forward returns KANS_ERR_UNSUPPORTED. */
+ * basis and K); larger B when the prefill kernel is built for the layer's K and basis (Chebyshev K <= 9;
+ * RBF on uniform centres 2 <= K <= 9 within the recurrence's span guard; B-spline K in {4, 8}; not INT8
+ * with the base branch at K = 7, nor INT8 B-spline at K = 8); 0 when such a forward returns
+ * KANS_ERR_UNSUPPORTED. */
 int kans_qlayer_fused(const kans_qlayer* layer, int B);
 /* device pointers; x_dtype / y_dtype any of KANS_DT_* (the prefill path reads fp16 / fp32 X, 16-byte aligned,
  * ldx % 8 == 0 and ldx >= round_up(D_in, 8)) */
@@ -313,8 +314,8 @@ int kans_qlayer_forward_host(kans_qlayer* layer, const void* X, int x_dtype, voi
  * must outlive the block.  round16: 1 (fp16) / 2 (bf16) rounds the gate, up and hidden activations as a
  * 16-bit model does, 0 keeps them fp32.  Chebyshev layers only (the reference's GatedKAN is built of
  * ChebyKAN layers).  Decode (B <= 32, every format): the gate|up GEMV with SwiGLU into the down layer's
- * basis (computing the basis of x itself at B <= 2, after one prep kernel above), the down GEMV and its
- * reduce.  Prefill (larger B, K in {1, 2, 4, 8}): one fused launch for gate|up with the SwiGLU epilogue
+ * basis (computing the basis of x itself at B = 1, after one prep kernel above), the down GEMV and its
+ * reduce.  Prefill (larger B, K <= 9; not INT8 at K = 7): one fused launch for gate|up with the SwiGLU epilogue
  * (gate and up columns paired in one tile) writing the hidden activations, one for down. */
 typedef struct kans_gated kans_gated;
 int kans_gated_create(kans_qlayer* gate, kans_qlayer* up, kans_qlayer* down, kans_gated** out);

@@ -1,0 +1,10 @@
+// Fused prefill kernels of one weight format (int4) with the base
+// branch: the instantiations of kan_qfused_block (kans_qprefill_kernel.h)
+// that qp_supported lists.
+#include "kans_qprefill_kernel.h"
+
+namespace kans {
+
+hipError_t qp_run_int4_b1(const QPLaunch& L, const QPGrid& G, hipStream_t st) { return qp_run<Q_INT4, 1>(L, G, st); }
+
+}  // namespace kans

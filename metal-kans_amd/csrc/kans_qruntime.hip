@@ -158,8 +158,13 @@ int build_ptiles(kans_qlayer* L, int seg, const void* codes, long rowbytes, cons
                  const float* biases, int gpr, hipStream_t st) {
   const int Kseg = seg ? 1 : L->K;
   const int CB = qp_chunk_bytes(L->quant), GS = qp_group(L->quant), PF = qp_param_floats(L->quant);
-  const size_t cbytes = (size_t)L->p_nfb * L->p_nob_pad * 64 * Kseg * CB;
-  const int G_alloc = (16 * L->p_nfb * Kseg + GS - 1) / GS;
+  // ternary pads an odd Kseg > 1 to whole slot pairs
+  const int Kpad = L->quant == Q_TERN && Kseg > 1 ? (Kseg + 1) / 2 * 2 : Kseg;
+  const size_t cbytes = (size_t)L->p_nfb * L->p_nob_pad * 64 * Kpad * CB;
+  // groups of every index, plus zero rows for the kernel's loads of a
+  // half-block's later groups (up to 3 past the first) and of its first group
+  // (qp_gl, up to 2 past the block's)
+  const int G_alloc = (16 * L->p_nfb * Kseg + GS - 1) / GS + 6;
   const long ldp = (long)L->p_nob_pad * 32;
   DevBuf& C = seg ? L->PCw : L->PCb;
   DevBuf& P = seg ? L->PPw : L->PPb;
@@ -178,7 +183,7 @@ int build_ptiles(kans_qlayer* L, int seg, const void* codes, long rowbytes, cons
 }
 
 void prefill_geometry(kans_qlayer* L) {
-  L->prefill = qp_supported(L->quant, L->K);
+  L->prefill = qp_supported(L->quant, L->K, L->has_base);
   L->p_nfb = (L->D_in + 15) / 16;
   L->p_nob_pad = round_up((L->D_out + 31) / 32, 8);
 }
@@ -268,7 +273,7 @@ int prep_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, int B, _Fl
 
 // Whether the fused prefill kernel covers this layer (tiles built, K and basis instantiated).
 bool prefill_ok(const kans_qlayer* L) {
-  return L->prefill && qp_supported(L->quant, L->K, L->basis, L->bp.rbf_rec);
+  return L->prefill && qp_supported(L->quant, L->K, L->has_base, L->basis, L->bp.rbf_rec);
 }
 
 // GEMV of layer a (and b, sharing a's activations phi / S): split-K partial sums
@@ -348,8 +353,9 @@ int prefill_layer_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, v
                          hipStream_t st) {
   if (!prefill_ok(L))
     return kans_fail(KANS_ERR_UNSUPPORTED,
-                     "the fused quantized prefill path takes K in {1, 2, 4, 8} (Chebyshev) or {4, 8} (RBF on uniform "
-                     "centres, B-spline); this layer has K = %d, basis %d", L->K, L->basis);
+                     "the fused quantized prefill path takes Chebyshev K <= 9, RBF on uniform centres 2 <= K <= 9 and "
+                     "B-spline K in {4, 8} (not INT8 with the base branch at K = 7, nor INT8 B-spline at K = 8); this "
+                     "layer has K = %d, basis %d", L->K, L->basis);
   int rc = check_prefill_x(X, x_dtype, ldx, L->D_in);
   if (rc) return rc;
   QPLaunch P{};
@@ -409,7 +415,8 @@ int plan_gated_prefill(kans_gated* G, const void* X, int x_dtype, long ldx, void
                        int round16, GatedPrefill& GP) {
   kans_qlayer *g = G->gate, *u = G->up, *d = G->down;
   if (!prefill_ok(g) || !prefill_ok(u) || !prefill_ok(d))
-    return kans_fail(KANS_ERR_UNSUPPORTED, "the fused quantized prefill path takes K in {1, 2, 4, 8} (K = %d, %d)",
+    return kans_fail(KANS_ERR_UNSUPPORTED,
+                     "the fused quantized prefill path takes K <= 9 (not INT8 with the base branch at K = 7): K = %d, %d",
                      g->K, d->K);
   if (g->has_bias && u->has_bias && g->bias_dtype != u->bias_dtype)
     return kans_fail(KANS_ERR_UNSUPPORTED, "gate and up biases of different dtypes");

@@ -23,8 +23,9 @@ from . import device
 from ._engine import DT_BF16, DT_F16, DT_F32
 
 MAX_DECODE_B = 32
-# Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for (the GatedKAN block)
-PREFILL_K = (1, 2, 4, 8)
+# Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for (the GatedKAN block;
+# INT8 with the base branch is not built at K = 7)
+PREFILL_K = (1, 2, 3, 4, 5, 6, 7, 8, 9)
 KANS_ERR_UNSUPPORTED = -5
 
 
@@ -36,7 +37,7 @@ def fused_batch_ok(fmt: str, K: int, B: int) -> bool:
         return False
     if B <= MAX_DECODE_B:
         return True
-    return K in PREFILL_K
+    return K in PREFILL_K and not (fmt == "int8" and K == 7)
 
 
 def packed_format(layer) -> Optional[str]:

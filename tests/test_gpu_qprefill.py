@@ -13,10 +13,13 @@ oracle on the oracle-dequantized weights:
 
 Shapes cover ragged D_in (the last feature block is partly padding, inside an
 affine group), ragged D_out (N-tile padding), several feature blocks per
-split, feature splits (few row tiles), K in {1, 2, 4, 8} (Chebyshev) and {4, 8}
-(Gaussian RBF on uniform centres, cubic B-spline), with and without the base /
-bias branches, fp16 and fp32 inputs and fp32 / fp16 / bf16 outputs.  The same
-RBF / B-spline layers are checked through the decode GEMVs (B <= 32, every K).
+split, feature splits (few row tiles, a split size rounded up to the kernel's
+phase period), K = 1 .. 9 (Chebyshev: at K in {3, 5, 6, 7, 9} the 8 codes of a
+chunk straddle quantization groups, and where they straddle depends on the
+feature block and lane half), {3, 4, 5, 7, 8} (Gaussian RBF on uniform centres)
+and {4, 8} (cubic B-spline), with and without the base / bias branches, fp16
+and fp32 inputs and fp32 / fp16 / bf16 outputs.  The same RBF / B-spline layers
+are checked through the decode GEMVs (B <= 32, every K).
 """
 import ctypes
 
@@ -122,6 +125,12 @@ def _oracle_rounded(L, x, weights16=True):
     return y
 
 
+def prefill_built(fmt, kind, K, base):
+    """Whether the fused prefill kernel is built for a layer (the rest runs the dense kernels on the dequantized
+    weights above 32 rows): not INT8 with the base branch at K = 7, nor INT8 B-spline at K = 8 (both spill)."""
+    return not ((fmt == "int8" and K == 7 and base) or (fmt, kind, K) == ("int8", "bspline", 8))
+
+
 def run(lib, h, x, d_out, y_dt="float32"):
     B = x.shape[0]
     xdt = DT["float16"] if x.dtype == np.float16 else DT["float32"]
@@ -136,15 +145,21 @@ def run(lib, h, x, d_out, y_dt="float32"):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
-@pytest.mark.parametrize("K", [1, 2, 4, 8])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("base,bias", [(True, False), (False, True), (True, True)])
-@pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300), (600, 48, 33)])
+@pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300), (600, 48, 33), (64, 328, 40)])
 def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
     lib = gpu
     print(f"case {fmt} K={K} base={base} bias={bias} B={B} {d_in}->{d_out}", flush=True)
     h, L = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=B + d_in + K)
     try:
         x = np.random.default_rng(K * 7 + d_out).uniform(-1.3, 1.3, (B, d_in)).astype(np.float32)
+        if not prefill_built(fmt, "cheby", K, base):
+            assert lib.kans_qlayer_fused(h, B) == 0
+            y = np.zeros((B, d_out), np.float32)
+            assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 0, y.ctypes.data, 0, B) == -5
+            return
+        assert lib.kans_qlayer_fused(h, B) == 1
         y = run(lib, h, x, d_out)
         e16 = O.rel_err(y, oracle(L, x))
         eop = O.rel_err(y, _oracle_rounded(L, x))
@@ -157,7 +172,8 @@ def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
-@pytest.mark.parametrize("kind,K", [("rbf", 8), ("rbf", 4), ("bspline", 8), ("bspline", 4)])
+@pytest.mark.parametrize("kind,K", [("rbf", 8), ("rbf", 4), ("rbf", 3), ("rbf", 5), ("rbf", 7), ("bspline", 8),
+                                    ("bspline", 4)])
 @pytest.mark.parametrize("base,bias", [(True, True), (False, False)])
 @pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300)])
 def test_qlayer_prefill_bases(gpu, fmt, kind, K, base, bias, B, d_in, d_out):
@@ -168,7 +184,7 @@ def test_qlayer_prefill_bases(gpu, fmt, kind, K, base, bias, B, d_in, d_out):
     h, L = make_qlayer(lib, fmt, d_in, d_out, K, base, bias, seed=B + d_in + 3 * K, kind=kind)
     try:
         x = np.random.default_rng(K + d_out).uniform(-2.0, 2.0, (B, d_in)).astype(np.float32)
-        if (fmt, kind, K) == ("int8", "bspline", 8):   # not built: the dense path on dequantized weights
+        if not prefill_built(fmt, kind, K, base):
             assert lib.kans_qlayer_fused(h, B) == 0
             y = np.zeros((B, d_out), np.float32)
             assert lib.kans_qlayer_forward_host(h, x.ctypes.data, 0, y.ctypes.data, 0, B) == -5
@@ -207,10 +223,12 @@ def test_qlayer_decode_bases(gpu, fmt, kind, K, uniform):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "ternary"])
-@pytest.mark.parametrize("kind,K,uniform", [("rbf", 8, False), ("rbf", 6, True), ("bspline", 6, True)])
+@pytest.mark.parametrize("kind,K,uniform", [("rbf", 8, False), ("rbf", 9, True), ("bspline", 5, True),
+                                            ("bspline", 6, True)])
 def test_qlayer_prefill_bases_unsupported(gpu, fmt, kind, K, uniform):
-    """RBF on non-uniform centres and K outside {4, 8}: decode batches run, larger ones report
-    KANS_ERR_UNSUPPORTED (-5) and kans_qlayer_fused says so."""
+    """RBF on non-uniform centres, RBF whose centres span more than the recurrence's guard (9 centres at
+    the reference's inv_den = 1 / (2 h^2): scaled span 6.8 > 6) and B-spline K outside {4, 8}: decode
+    batches run, larger ones report KANS_ERR_UNSUPPORTED (-5) and kans_qlayer_fused says so."""
     lib = gpu
     h, L = make_qlayer(lib, fmt, 40, 24, K, True, False, seed=2, kind=kind, uniform=uniform)
     try:
@@ -245,11 +263,11 @@ def test_qlayer_prefill_io_dtypes(gpu, fmt):
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 def test_qlayer_prefill_rejects_unsupported_K(gpu, fmt):
-    """K outside {1, 2, 4, 8}: the layer decodes small batches (any K) and reports KANS_ERR_UNSUPPORTED (-5)
-    for batches the prefill kernel would take."""
+    """K = 10 (past the prefill kernel's 9): the layer decodes small batches (any K) and reports
+    KANS_ERR_UNSUPPORTED (-5) for batches the prefill kernel would take."""
     lib = gpu
     rng = np.random.default_rng(0)
-    h, L = make_qlayer(lib, fmt, 24, 40, 3, True, False, seed=1)
+    h, L = make_qlayer(lib, fmt, 24, 40, 10, True, False, seed=1)
     try:
         x = rng.uniform(-1, 1, (33, 24)).astype(np.float32)
         y = np.zeros((33, 40), np.float32)
@@ -285,7 +303,7 @@ def gated_oracle(specs, x, round16):
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 @pytest.mark.parametrize("B", [33, 300])
 @pytest.mark.parametrize("d,hdim,bias,K", [(64, 160, False, 4), (96, 150, True, 4), (256, 520, False, 4),
-                                           (96, 200, True, 8)])
+                                           (96, 200, True, 8), (80, 200, False, 3), (96, 136, True, 9)])
 @pytest.mark.parametrize("round16", [1, 0])
 def test_gated_prefill(gpu, fmt, B, d, hdim, bias, K, round16):
     """gate|up in one launch (column-paired tile, SwiGLU epilogue), then down: against the oracle block."""
@@ -369,18 +387,18 @@ def test_python_gatedkan_prefill(gpu, quant):
 
 
 @pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
-@pytest.mark.parametrize("kind", ["rbf", "bspline", "rbf5"])
+@pytest.mark.parametrize("kind", ["rbf", "bspline", "rbf5", "rbf9"])
 def test_python_quantized_fastkan_bsplinekan(gpu, quant, kind):
     """FastKAN(...).half().to_<quant>() and BSplineKAN(...).half().to_<quant>() keep fp16 compute and run on
-    their packed weights: the decode GEMVs at B = 5 and the prefill kernel at B = 300 (K = 8); a 5-centre
-    FastKAN (no prefill kernel for K = 5) takes the packed path at B = 5 and the dequantized weights at
-    B = 300, equally correct."""
+    their packed weights: the decode GEMVs at B = 5 and the prefill kernel at B = 300 (K = 8, and 5 centres);
+    a 9-centre FastKAN (its centres span more than the RBF recurrence allows at the default width) takes
+    the packed path at B = 5 and the dequantized weights at B = 300, equally correct."""
     import metal_kans as mk
     np.random.seed(8)
     if kind == "bspline":
         L = mk.BSplineKAN(72, 40, grid_size=5)
     else:
-        L = mk.FastKAN(72, 40, num_centers=5 if kind == "rbf5" else 8, grid_range=(-2.0, 2.0))
+        L = mk.FastKAN(72, 40, num_centers={"rbf5": 5, "rbf9": 9}.get(kind, 8), grid_range=(-2.0, 2.0))
     L.bias = np.random.normal(0, 0.1, 40).astype(np.float32)
     L.half()
     getattr(mk, f"to_{quant}")(L)
@@ -394,7 +412,7 @@ def test_python_quantized_fastkan_bsplinekan(gpu, quant, kind):
         assert y.dtype == np.float16 and y.shape == (B, 40)
         eng = L.__dict__.get("_qlayer_engine")
         assert eng is not None
-        assert eng.fused(B) == (B <= 32 or (kind != "rbf5" and (kind, quant) != ("bspline", "int8")))
+        assert eng.fused(B) == (B <= 32 or (kind != "rbf9" and (kind, quant) != ("bspline", "int8")))
         assert O.rel_err(y.astype(np.float32), oracle(spec, x)) <= 2e-2
         if eng.fused(B):
             # fp16 output: its own rounding is up to 2^-12 of |y| (the C-level tests above check fp32 outputs)
