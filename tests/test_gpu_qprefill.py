@@ -350,21 +350,24 @@ def test_gated_decode_and_prefill_agree(gpu, fmt):
 
 # ---------------------------------------------------------------- Python layer API
 @pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
-def test_python_quantized_fp16_layer_uses_packed_weights(gpu, quant):
+@pytest.mark.parametrize("degree", [4, 9, 3])
+def test_python_quantized_fp16_layer_uses_packed_weights(gpu, quant, degree):
     """ChebyKAN(...).half().to_<quant>() keeps fp16 compute and runs on its packed weights at every batch
-    (decode GEMV up to 32 rows, the prefill kernel above)."""
+    (decode GEMV up to 32 rows, the prefill kernel above), including degrees whose code chunks straddle
+    quantization groups (3, and the north star's 9)."""
     import metal_kans as mk
     np.random.seed(7)
-    L = mk.ChebyKAN(80, 50, degree=4)
+    L = mk.ChebyKAN(80, 50, degree=degree)
     L.bias = np.random.normal(0, 0.1, 50).astype(np.float32)
     L.half()
     getattr(mk, f"to_{quant}")(L)
-    spec = {"W": L.w_cheby, "W_base": L.w_base, "bias": L.bias.astype(np.float32), "K": 4}
+    spec = {"W": L.w_cheby, "W_base": L.w_base, "bias": L.bias.astype(np.float32), "K": degree}
     for B in (5, 300):
         x = np.random.default_rng(B).uniform(-1.1, 1.1, (B, 80)).astype(np.float32)
         y = L(x)
         assert y.dtype == np.float16 and y.shape == (B, 50)
-        assert L.__dict__.get("_qlayer_engine") is not None
+        eng = L.__dict__.get("_qlayer_engine")
+        assert eng is not None and eng.fused(B)
         assert O.rel_err(y.astype(np.float32), _oracle_rounded(spec, x)) <= 2e-3
         assert O.rel_err(y.astype(np.float32), oracle(spec, x)) <= 2e-2
 
