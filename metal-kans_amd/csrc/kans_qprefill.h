@@ -1,5 +1,6 @@
-// Quantized prefill kernels (kans_qprefill.hip): tile format and launch
-// descriptors shared with the runtime.
+// Quantized prefill kernels (kans_qprefill_kernel.h, launched by
+// kans_qprefill.hip): tile format and launch descriptors shared with the
+// runtime.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "kans_common.h"

@@ -1,9 +1,9 @@
-// Runtime objects of the quantized paths: a Chebyshev KAN layer held in the
-// reference's packed INT8 / INT4 / ternary formats (kans_qlayer) and the
-// GatedKAN block of three such layers (kans_gated), plus the reference-named
-// fused ternary entry point.  Batches of at most 32 rows take the decode GEMVs
-// (kans_qgemv.hip, INT4 and ternary); larger batches, and every INT8 batch,
-// the fused prefill kernel (kans_qprefill.hip).
+// Runtime objects of the quantized paths: a KAN layer (Chebyshev, RBF or
+// B-spline basis) held in the reference's packed INT8 / INT4 / ternary formats
+// (kans_qlayer) and the GatedKAN block of three such layers (kans_gated), plus
+// the reference-named fused ternary entry point.  Batches of at most 32 rows
+// take the decode GEMVs (kans_qgemv.hip, every format); larger batches the
+// fused prefill kernel (kans_qprefill_kernel.h).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -348,7 +348,7 @@ int check_y(const void* Y, int y_dtype, long ldy, int D_out) {
   return 0;
 }
 
-// Fused prefill forward of one layer (kans_qprefill.hip), any batch.
+// Fused prefill forward of one layer (kans_qprefill_kernel.h), any batch.
 int prefill_layer_locked(kans_qlayer* L, const void* X, int x_dtype, long ldx, void* Y, int y_dtype, long ldy, int B,
                          hipStream_t st) {
   if (!prefill_ok(L))

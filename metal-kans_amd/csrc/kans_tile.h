@@ -1,5 +1,5 @@
 // Tile helpers shared by the fused dense kernels (kans_dense.hip) and the
-// fused quantized-weight kernels (kans_qprefill.hip): the 16-bit MFMA
+// fused quantized-weight kernels (kans_qprefill_kernel.h): the 16-bit MFMA
 // wrappers, the XCD-aware workgroup -> tile mapping and compile-time loops.
 #pragma once
 #include "kans_common.h"
