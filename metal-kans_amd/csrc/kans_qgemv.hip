@@ -733,6 +733,68 @@ __device__ __forceinline__ int unpack_pos(int rp) {
   return rp;
 }
 
+// In-kernel basis of x, Chebyshev with K = 4 or 8 coefficients: the 8-blocks
+// b < nblocks of a wave's range (reduction indices P_lo + 8 b .. + 7, all in
+// the basis segment), one per lane and step.  A block covers 8 / K whole
+// features; the lane evaluates T_0 .. T_{K-1} of them with k_prep's
+// recurrence (cheb_k: the same fma chain, so the same values), converts them
+// with half_of, places them in the weight format's unpack order and writes the
+// block with one 16-byte LDS store.  The input loads of a step are issued
+// together, then kick() (the ring's first weight loads), then the arithmetic.
+// The per-value form (below) spent ~8 us per wave at cfg5 in its 64-bit index
+// arithmetic and 2-byte LDS stores; this form writes whole blocks.
+constexpr int kPreBlocks = 8;  // 8-blocks per lane and step
+template <int QT, int KC, typename Kick>
+__device__ __forceinline__ void pre_cheb_blocks(const QPreDev& P, int m, long P_lo, int nblocks, _Float16* dst,
+                                                int lane, Kick&& kick) {
+  constexpr int NF = 8 / KC;  // features per block
+  const int es = P.x_dtype == DT_F32 ? 4 : 2;
+  const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
+  const unsigned f_base = (unsigned)(P_lo / KC);  // feature of block 0's first index (P_lo is a multiple of 128)
+  for (int b0 = 0; b0 < nblocks; b0 += 64 * kPreBlocks) {
+    unsigned xr[kPreBlocks][NF];
+    if (es == 4) {
+#pragma unroll
+      for (int it = 0; it < kPreBlocks; ++it) {
+        const unsigned f = f_base + (unsigned)min(b0 + lane + 64 * it, nblocks - 1) * NF;
+#pragma unroll
+        for (int q = 0; q < NF; ++q) xr[it][q] = *reinterpret_cast<const unsigned*>(row + 4u * (f + q));
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kPreBlocks; ++it) {
+        const unsigned f = f_base + (unsigned)min(b0 + lane + 64 * it, nblocks - 1) * NF;
+#pragma unroll
+        for (int q = 0; q < NF; ++q) xr[it][q] = *reinterpret_cast<const unsigned short*>(row + 2u * (f + q));
+      }
+    }
+    kick();
+#pragma unroll
+    for (int it = 0; it < kPreBlocks; ++it) {
+      const int b = b0 + lane + 64 * it;
+      if (b < nblocks) {
+        float T[NF][KC];
+#pragma unroll
+        for (int q = 0; q < NF; ++q) {
+          const float t = fminf(fmaxf(x_of_raw(xr[it][q], P.x_dtype), -1.0f), 1.0f);
+          T[q][0] = 1.0f;
+          T[q][1] = t;
+#pragma unroll
+          for (int k = 2; k < KC; ++k) T[q][k] = __builtin_fmaf(2.0f * t, T[q][k - 1], -T[q][k - 2]);
+        }
+        // position e holds index unpack_order(e) of the block: feature u / KC, coefficient u % KC
+        _Float16 hv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int u = unpack_order<QT>(e);
+          hv[e] = half_of(T[u / KC][u % KC]);
+        }
+        reinterpret_cast<uint4*>(dst)[b] = *reinterpret_cast<const uint4*>(hv);
+      }
+    }
+  }
+}
+
 // Small-batch decode GEMV (B = SR <= kSmallB).  One wave = kQNW row blocks
 // (64 output rows) x one contiguous superchunk range (split-K over waves for
 // memory-level parallelism); 4 independent waves per workgroup.
@@ -916,8 +978,18 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
           reinterpret_cast<uint4*>(phl + m * lrow)[i] = make_uint4(0u, 0u, 0u, 0u);
       // basis segment: T_k(clamp(x_i)) at index i K + k (k_prep / cheb_k)
       const long Pb_end = min(P_hi, min((long)P.Cb * 128, (long)P.D_in * P.K));
-      if (P_lo < Pb_end) {
-        const int f0 = (int)(P_lo / P.K), f1 = (int)((Pb_end - 1) / P.K) + 1;
+      // K = 4 and 8: whole 8-blocks per lane (pre_cheb_blocks), the rest per feature below
+      long Pg_lo = P_lo;
+      if (P_lo < Pb_end && (P.K == 4 || P.K == 8)) {
+        const int nfull = (int)((Pb_end - P_lo) / 8);
+        for (int m = 0; m < SR; ++m) {
+          if (P.K == 4) pre_cheb_blocks<QT, 4>(P, m, P_lo, nfull, phl + m * lrow, lane, kick);
+          else pre_cheb_blocks<QT, 8>(P, m, P_lo, nfull, phl + m * lrow, lane, kick);
+        }
+        Pg_lo = P_lo + 8L * nfull;
+      }
+      if (Pg_lo < Pb_end) {
+        const int f0 = (int)(Pg_lo / P.K), f1 = (int)((Pb_end - 1) / P.K) + 1;
         for (int m = 0; m < SR; ++m)
           for (int fb = f0; fb < f1; fb += 64 * kPreBatch) {
             unsigned xr[kPreBatch];
@@ -938,7 +1010,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
                     v = cn;
                   }
                   const long j = (long)f * P.K + k;
-                  if (j >= P_lo && j < Pb_end) phl[m * lrow + unpack_pos<QT>((int)(j - P_lo))] = half_of(v);
+                  if (j >= Pg_lo && j < Pb_end) phl[m * lrow + unpack_pos<QT>((int)(j - P_lo))] = half_of(v);
                 }
               }
             }

@@ -313,8 +313,9 @@ def test_gated_fused_epilogue_matches_unfused(gpu, fmt, cfg):
             lib.kans_qlayer_destroy(h)
 
 
-PRE_CFGS = [  # d, h, K and base branch of gate / up
-    (96, 200, 1, True), (100, 70, 5, False), (130, 64, 32, True), (2048, 256, 4, True), (33, 17, 3, True)]
+PRE_CFGS = [  # d, h, K and base branch of gate / up (K = 4 and 8 take the whole-block basis path)
+    (96, 200, 1, True), (100, 70, 5, False), (130, 64, 32, True), (2048, 256, 4, True), (33, 17, 3, True),
+    (1000, 96, 8, True), (333, 80, 4, False), (3001, 64, 4, True)]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
