@@ -682,38 +682,40 @@ __device__ __forceinline__ void load_codes(const char* rec, int lane, QW (&qw)[k
 }
 
 // In-kernel activation basis of k_qgemv (PRE): the layer input and the basis
-// geometry, and each wave's LDS slice: Phi rows [SR][span * 128] (fp16, in the
-// weight format's unpack order) then the group sums [span][SR] (INT4 / INT8).
+// geometry, and the workgroup's LDS slice: Phi rows [SR][span * 128] (fp16, in
+// the weight format's unpack order) then the group sums [span][SR] (INT4 / INT8).
 struct QPreDev {
   const void* X;
   int x_dtype;
   long ldx;
   int D_in, K, has_base, Cb;
-  int span;   // superchunks per slice, >= every wave's range
-  int slice;  // bytes of LDS per wave (also holds the SwiGLU epilogue's stage)
+  int span;   // superchunks per slice, >= every workgroup's range
+  int slice;  // bytes of the workgroup's LDS slice (the waves' epilogue stages follow it)
 };
-constexpr int kPreBatch = 16;           // input loads in flight per lane
-constexpr int kPreVec = 8;              // 16-byte input loads in flight per lane (base segment)
+constexpr int kPreThreads = 256;       // threads of a workgroup computing one range's basis together
+constexpr int kEpiStageBytes = 64 * (kMaxK + 1) * 2;  // a wave's SwiGLU epilogue stage (fp16)
+constexpr int kPreBatch = 4;            // input loads in flight per thread
+constexpr int kPreVec = 2;              // 16-byte input loads in flight per thread (base segment)
 constexpr int kPreLdsMax = 80 * 1024;   // dynamic LDS per workgroup (two per CU)
 
-// One batch of layer inputs, x[m][min(fb + lane + 64 it, f1 - 1)] for
+// One batch of layer inputs, x[m][min(fb + pt + kPreThreads it, f1 - 1)] for
 // it < kPreBatch, as raw bits (4- or 2-byte loads under one uniform branch):
 // no value is used before the batch's last load is issued, so the loads stay
 // in flight together (converted in the branch, each load was waited for in
 // turn).  x_of_raw converts as load_any does (all three conversions exact).
 __device__ __forceinline__ void load_x_raw(unsigned (&xr)[kPreBatch], const QPreDev& P, int m, int fb, int f1,
-                                           int lane) {
+                                           int pt) {
   // a uniform row pointer and 32-bit lane offsets: one VGPR per address
   const int es = P.x_dtype == DT_F32 ? 4 : 2;
   const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
   if (es == 4) {
 #pragma unroll
     for (int it = 0; it < kPreBatch; ++it)
-      xr[it] = *reinterpret_cast<const unsigned*>(row + 4u * (unsigned)min(fb + lane + 64 * it, f1 - 1));
+      xr[it] = *reinterpret_cast<const unsigned*>(row + 4u * (unsigned)min(fb + pt + kPreThreads * it, f1 - 1));
   } else {
 #pragma unroll
     for (int it = 0; it < kPreBatch; ++it)
-      xr[it] = *reinterpret_cast<const unsigned short*>(row + 2u * (unsigned)min(fb + lane + 64 * it, f1 - 1));
+      xr[it] = *reinterpret_cast<const unsigned short*>(row + 2u * (unsigned)min(fb + pt + kPreThreads * it, f1 - 1));
   }
 }
 __device__ __forceinline__ float x_of_raw(unsigned r, int dt) {
@@ -734,36 +736,36 @@ __device__ __forceinline__ int unpack_pos(int rp) {
 }
 
 // In-kernel basis of x, Chebyshev with K = 4 or 8 coefficients: the 8-blocks
-// b < nblocks of a wave's range (reduction indices P_lo + 8 b .. + 7, all in
-// the basis segment), one per lane and step.  A block covers 8 / K whole
-// features; the lane evaluates T_0 .. T_{K-1} of them with k_prep's
+// b < nblocks of a workgroup's range (reduction indices P_lo + 8 b .. + 7, all
+// in the basis segment), one per thread pt and step.  A block covers 8 / K
+// whole features; the thread evaluates T_0 .. T_{K-1} of them with k_prep's
 // recurrence (cheb_k: the same fma chain, so the same values), converts them
 // with half_of, places them in the weight format's unpack order and writes the
 // block with one 16-byte LDS store.  The input loads of a step are issued
-// together, then kick() (the ring's first weight loads), then the arithmetic.
+// together, then kick() (the wave's first weight loads), then the arithmetic.
 // The per-value form (below) spent ~8 us per wave at cfg5 in its 64-bit index
 // arithmetic and 2-byte LDS stores; this form writes whole blocks.
-constexpr int kPreBlocks = 8;  // 8-blocks per lane and step
+constexpr int kPreBlocks = 2;    // 8-blocks per thread and step
 template <int QT, int KC, typename Kick>
 __device__ __forceinline__ void pre_cheb_blocks(const QPreDev& P, int m, long P_lo, int nblocks, _Float16* dst,
-                                                int lane, Kick&& kick) {
+                                                int pt, Kick&& kick) {
   constexpr int NF = 8 / KC;  // features per block
   const int es = P.x_dtype == DT_F32 ? 4 : 2;
   const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
   const unsigned f_base = (unsigned)(P_lo / KC);  // feature of block 0's first index (P_lo is a multiple of 128)
-  for (int b0 = 0; b0 < nblocks; b0 += 64 * kPreBlocks) {
+  for (int b0 = 0; b0 < nblocks; b0 += kPreThreads * kPreBlocks) {
     unsigned xr[kPreBlocks][NF];
     if (es == 4) {
 #pragma unroll
       for (int it = 0; it < kPreBlocks; ++it) {
-        const unsigned f = f_base + (unsigned)min(b0 + lane + 64 * it, nblocks - 1) * NF;
+        const unsigned f = f_base + (unsigned)min(b0 + pt + kPreThreads * it, nblocks - 1) * NF;
 #pragma unroll
         for (int q = 0; q < NF; ++q) xr[it][q] = *reinterpret_cast<const unsigned*>(row + 4u * (f + q));
       }
     } else {
 #pragma unroll
       for (int it = 0; it < kPreBlocks; ++it) {
-        const unsigned f = f_base + (unsigned)min(b0 + lane + 64 * it, nblocks - 1) * NF;
+        const unsigned f = f_base + (unsigned)min(b0 + pt + kPreThreads * it, nblocks - 1) * NF;
 #pragma unroll
         for (int q = 0; q < NF; ++q) xr[it][q] = *reinterpret_cast<const unsigned short*>(row + 2u * (f + q));
       }
@@ -771,7 +773,7 @@ __device__ __forceinline__ void pre_cheb_blocks(const QPreDev& P, int m, long P_
     kick();
 #pragma unroll
     for (int it = 0; it < kPreBlocks; ++it) {
-      const int b = b0 + lane + 64 * it;
+      const int b = b0 + pt + kPreThreads * it;
       if (b < nblocks) {
         float T[NF][KC];
 #pragma unroll
@@ -814,12 +816,16 @@ __device__ __forceinline__ void pre_cheb_blocks(const QPreDev& P, int m, long P_
 // counts merged across it and it drained the ring at every round; it also
 // held ~90 more registers).  NT: non-temporal weight loads (load_rec).
 //
-// PRE: the wave computes Phi / S of its own superchunk range from the layer
-// input into its LDS slice first (QPreDev), with the values, rounding and sum
-// order of k_prep, so the results equal the k_prep path bit for bit.  The
-// input loads of the first batch are issued before the ring's first weight
-// loads, so they return first; the weights stream while the basis is
-// computed, and the k_prep launch and its wait disappear.
+// PRE: the four waves of a workgroup take four consecutive row groups over
+// one superchunk range, and its 256 threads compute Phi / S of that range from
+// the layer input into the workgroup's LDS slice first (QPreDev), with the
+// values, rounding and sum order of k_prep, so the results equal the k_prep
+// path bit for bit; two barriers order the basis values, the sums and the
+// reads.  Each wave's first weight loads are issued right after the first
+// batch of input loads, so the inputs return first and the weights stream
+// while the basis is computed; the k_prep launch and its wait disappear.
+// (Each wave computing its own range's basis alone spent 5-16 us per wave on
+// it at cfg5, a quarter of the gate|up GEMV's time.)
 template <int QT, int SR, int EPI, bool NT, bool PRE>
 __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_split, int n_rg, int ksplit,
                                                int C_tot, const _Float16* __restrict__ Phi,
@@ -828,10 +834,17 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   static_assert(SR >= 1 && SR <= kSmallB, "small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int rg = item / ksplit;
-  const int ks = item - rg * ksplit;
-  if (rg >= n_rg) return;  // uniform per wave
+  const int wave = threadIdx.x >> 6;
+  // PRE: the four waves of a workgroup take four consecutive row groups over
+  // ONE superchunk range and compute its basis together (a workgroup past the
+  // last row group still takes part in that, then stops); otherwise four
+  // consecutive (row group, split) items
+  const int item = blockIdx.x * 4 + wave;
+  const int rg_all = PRE ? (int)(blockIdx.x / ksplit) * 4 + wave : item / ksplit;
+  const int ks = PRE ? (int)(blockIdx.x % ksplit) : item - rg_all * ksplit;
+  const bool live_rg = rg_all < n_rg;
+  if (!PRE && !live_rg) return;  // uniform per wave
+  const int rg = live_rg ? rg_all : n_rg - 1;
   const QMatDev& M = rg < rg_split ? m0 : m1;
   const int rg_loc = rg < rg_split ? rg : rg - rg_split;
   const int rb0 = rg_loc * NW;
@@ -849,11 +862,12 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   const int arow = r & 3;  // batch row of this lane's MFMA row (replicated every 4 rows)
   const bool alive = arow < B;
   const _Float16* arow_p = Phi + (long)(alive ? arow : 0) * ldphi + 8 * q;
-  // PRE: this wave's LDS slice
+  // PRE: the workgroup's LDS slice (basis values, then group sums), then one
+  // epilogue stage per wave
   extern __shared__ __attribute__((aligned(16))) char qg_dyn[];
-  char* const myl = qg_dyn + (threadIdx.x >> 6) * P.slice;
-  _Float16* const phl = reinterpret_cast<_Float16*>(myl);
-  float2* const sl = reinterpret_cast<float2*>(myl + P.span * SR * 256);
+  const int pt = threadIdx.x;  // thread of the workgroup in the basis work
+  _Float16* const phl = reinterpret_cast<_Float16*>(qg_dyn);
+  float2* const sl = reinterpret_cast<float2*>(qg_dyn + P.span * SR * 256);
   const int lrow = P.span * 128;
   const _Float16* const arow_l = phl + (alive ? arow : 0) * lrow + 8 * q;
 
@@ -961,7 +975,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       // the ring's first weight loads, issued once, right after the first
       // batch of input loads
       auto kick = [&] {
-        if (started) return;
+        if (started || !live_rg) return;
         started = true;
         fence();
         issue_w(c_lo, o0);
@@ -974,7 +988,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       // zero the slice: indices past the segments' values read 0
 #pragma unroll
       for (int m = 0; m < SR; ++m)
-        for (int i = lane; i < nblk; i += 64)
+        for (int i = pt; i < nblk; i += kPreThreads)
           reinterpret_cast<uint4*>(phl + m * lrow)[i] = make_uint4(0u, 0u, 0u, 0u);
       // basis segment: T_k(clamp(x_i)) at index i K + k (k_prep / cheb_k)
       const long Pb_end = min(P_hi, min((long)P.Cb * 128, (long)P.D_in * P.K));
@@ -983,21 +997,21 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       if (P_lo < Pb_end && (P.K == 4 || P.K == 8)) {
         const int nfull = (int)((Pb_end - P_lo) / 8);
         for (int m = 0; m < SR; ++m) {
-          if (P.K == 4) pre_cheb_blocks<QT, 4>(P, m, P_lo, nfull, phl + m * lrow, lane, kick);
-          else pre_cheb_blocks<QT, 8>(P, m, P_lo, nfull, phl + m * lrow, lane, kick);
+          if (P.K == 4) pre_cheb_blocks<QT, 4>(P, m, P_lo, nfull, phl + m * lrow, pt, kick);
+          else pre_cheb_blocks<QT, 8>(P, m, P_lo, nfull, phl + m * lrow, pt, kick);
         }
         Pg_lo = P_lo + 8L * nfull;
       }
       if (Pg_lo < Pb_end) {
         const int f0 = (int)(Pg_lo / P.K), f1 = (int)((Pb_end - 1) / P.K) + 1;
         for (int m = 0; m < SR; ++m)
-          for (int fb = f0; fb < f1; fb += 64 * kPreBatch) {
+          for (int fb = f0; fb < f1; fb += kPreThreads * kPreBatch) {
             unsigned xr[kPreBatch];
-            load_x_raw(xr, P, m, fb, f1, lane);
+            load_x_raw(xr, P, m, fb, f1, pt);
             kick();
 #pragma unroll
             for (int it = 0; it < kPreBatch; ++it) {
-              const int f = fb + lane + 64 * it;
+              const int f = fb + pt + kPreThreads * it;
               if (f < f1) {
                 const float t = fminf(fmaxf(x_of_raw(xr[it], P.x_dtype), -1.0f), 1.0f);
                 float a = 1.0f, b = t;
@@ -1029,22 +1043,26 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
           const int ch0 = (int)(Pw0 - w0) / 8, ch1 = (int)(Pw1 - w0) / 8;  // 8-input chunks
           for (int m = 0; m < SR; ++m) {
             const char* row = reinterpret_cast<const char*>(P.X) + (long)m * P.ldx * es;
-            for (int cb = ch0; cb < ch1; cb += 64 * kPreVec) {
+            // chunks per thread and step: kPreVec (16-bit x, one load each) or
+            // kPreVec / 2 (fp32 x, two loads each)
+            const int cstep = kPreThreads * (es == 2 ? kPreVec : kPreVec / 2);
+            for (int cb = ch0; cb < ch1; cb += cstep) {
               uint4 xr[kPreVec];  // es = 2: one chunk each; es = 4: half a chunk each
               if (es == 2) {
 #pragma unroll
                 for (int it = 0; it < kPreVec; ++it)
-                  xr[it] = *reinterpret_cast<const uint4*>(row + 16u * (unsigned)min(cb + lane + 64 * it, ch1 - 1));
+                  xr[it] = *reinterpret_cast<const uint4*>(
+                      row + 16u * (unsigned)min(cb + pt + kPreThreads * it, ch1 - 1));
               } else {
 #pragma unroll
                 for (int it = 0; it < kPreVec; ++it)
                   xr[it] = *reinterpret_cast<const uint4*>(
-                      row + 32u * (unsigned)min(cb + lane + 64 * (it >> 1), ch1 - 1) + 16u * (unsigned)(it & 1));
+                      row + 32u * (unsigned)min(cb + pt + kPreThreads * (it >> 1), ch1 - 1) + 16u * (unsigned)(it & 1));
               }
               kick();
-              // chunk `it` of this lane: SiLU of its 8 inputs into one 8-block
+              // chunk `it` of this thread: SiLU of its 8 inputs into one 8-block
               auto put = [&](int it, const float (&v)[8]) {
-                const int ch = cb + lane + 64 * it;
+                const int ch = cb + pt + kPreThreads * it;
                 if (ch < ch1) {
                   _Float16 hv[8];
 #pragma unroll
@@ -1080,13 +1098,13 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         } else if (Pw0 < Pw1) {
           const int f0 = (int)(Pw0 - w0), f1 = (int)(Pw1 - w0);
           for (int m = 0; m < SR; ++m)
-            for (int fb = f0; fb < f1; fb += 64 * kPreBatch) {
+            for (int fb = f0; fb < f1; fb += kPreThreads * kPreBatch) {
               unsigned xr[kPreBatch];
-              load_x_raw(xr, P, m, fb, f1, lane);
+              load_x_raw(xr, P, m, fb, f1, pt);
               kick();
 #pragma unroll
               for (int it = 0; it < kPreBatch; ++it) {
-                const int f = fb + lane + 64 * it;
+                const int f = fb + pt + kPreThreads * it;
                 if (f < f1)
                   phl[m * lrow + unpack_pos<QT>((int)(w0 + f - P_lo))] = half_of(silu_f32(x_of_raw(xr[it], P.x_dtype)));
               }
@@ -1094,14 +1112,14 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         }
       }
       kick();
-      asm volatile("" ::: "memory");  // LDS writes before the reads below (one wave, in order)
+      __syncthreads();  // every thread's basis values are in LDS before the sums read them
       // group sums as k_prep: each 8-block's fp16 values in order, then the
       // 8-block sums of a 64-group by xor steps 1, 2, 4 over its 8 lanes
       if constexpr (q_affine(QT)) {
 #pragma unroll
         for (int m = 0; m < SR; ++m)
-          for (int b0 = 0; b0 < nblk; b0 += 64) {
-            const int blk = b0 + lane;
+          for (int b0 = 0; b0 < nblk; b0 += kPreThreads) {
+            const int blk = b0 + pt;
             const bool live = blk < nblk;
             uint4 u = make_uint4(0u, 0u, 0u, 0u);
             if (live) u = reinterpret_cast<const uint4*>(phl + m * lrow)[blk];
@@ -1115,8 +1133,9 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
             const float other = __shfl_xor(sum, 8);
             if (live && (lane & 15) == 0) sl[(blk >> 4) * SR + m] = make_float2(sum, other);
           }
-        asm volatile("" ::: "memory");
+        __syncthreads();  // the group sums are in LDS before any wave reads them
       }
+      if (!live_rg) return;  // a padding row group: its share of the basis is done
       issue_a(c_lo, o0);
       issue_a(c_lo + 1, o1);
     } else {
@@ -1143,6 +1162,7 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     }
   }
 
+  if (PRE && !live_rg) return;  // padding row group (an empty range skipped the basis work)
   // lane (q, r): row block q, column 16*(rb0 + q) + r, rows i < B from acc[q][i]
   const int n = (rb0 + q) * 16 + r;
   if (n < M.D_out) {
@@ -1160,7 +1180,8 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   if constexpr (EPI == QEPI_SWIGLU) {
     _Float16* stg;
     if constexpr (PRE) {
-      stg = phl;  // the slice is free again
+      // this wave's stage after the shared slice (other waves may still read the slice)
+      stg = reinterpret_cast<_Float16*>(qg_dyn + P.slice + wave * kEpiStageBytes);
     } else {
       __shared__ _Float16 stage[4][64 * (kMaxK + 1)];
       stg = stage[threadIdx.x >> 6];
@@ -1588,11 +1609,16 @@ hipError_t qprep(int qt, const QPrep& P, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Bytes of one wave's LDS slice for the in-kernel basis (QPreDev).
-static int pre_slice_bytes(int qt, int B, int span, int epi_kind) {
-  int b = span * B * 256 + (q_affine(qt) ? span * B * 8 : 0);
-  if (epi_kind == QEPI_SWIGLU) b = std::max(b, 64 * (kMaxK + 1) * 2);
+// Bytes of a workgroup's LDS slice for the in-kernel basis (QPreDev): the
+// basis values and group sums of its superchunk range.
+static int pre_slice_bytes(int qt, int B, int span) {
+  const int b = span * B * 256 + (q_affine(qt) ? span * B * 8 : 0);
   return (b + 15) & ~15;
+}
+// Dynamic LDS of a k_qgemv<PRE> workgroup: the slice, then one epilogue stage
+// per wave (QEPI_SWIGLU).
+static int pre_lds_bytes(int qt, int B, int span, int epi_kind) {
+  return pre_slice_bytes(qt, B, span) + (epi_kind == QEPI_SWIGLU ? 4 * kEpiStageBytes : 0);
 }
 
 bool qgemv_pre_fits(int qt, int B, int C_tot, int ksplit, int epi_kind) {
@@ -1606,7 +1632,7 @@ bool qgemv_pre_fits(int qt, int B, int C_tot, int ksplit, int epi_kind) {
   }
   if (B < 1 || B > kSmallB || ksplit < 1) return false;
   const int span = (C_tot + ksplit - 1) / ksplit;
-  return 4 * pre_slice_bytes(qt, B, span, epi_kind) <= std::min(kPreLdsMax, lds_max);
+  return pre_lds_bytes(qt, B, span, epi_kind) <= std::min(kPreLdsMax, lds_max);
 }
 
 // Launch of the decode GEMV kernel for G (arguments checked by qgemv).
@@ -1615,14 +1641,15 @@ static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
   QMatDev a{(const char*)G.rec0, G.D_out0, 0};
   QMatDev b{(const char*)(G.rec1 ? G.rec1 : G.rec0), G.D_out1, G.D_out0};
   const int items = G.n_rg * G.ksplit;
-  dim3 grid((unsigned)((items + 3) / 4));
   QPreDev P{G.X, G.x_dtype, G.ldx, G.D_in, G.K, G.has_base, G.Cb, 0, 0};
   const bool pre = G.X != nullptr;
   if (pre) {
     P.span = (G.C_tot + G.ksplit - 1) / G.ksplit;
-    P.slice = pre_slice_bytes(qt, G.B, P.span, G.epi.kind);
+    P.slice = pre_slice_bytes(qt, G.B, P.span);
   }
-  const size_t dyn = pre ? (size_t)4 * P.slice : 0;
+  // PRE: a workgroup per (four row groups, split); otherwise per four items
+  dim3 grid((unsigned)(pre ? (G.n_rg + 3) / 4 * G.ksplit : (items + 3) / 4));
+  const size_t dyn = pre ? (size_t)pre_lds_bytes(qt, G.B, P.span, G.epi.kind) : 0;
 #define KQ_GEMV(QTV, SR, EP)                                                                                      \
   do {                                                                                                           \
     if (pre)                                                                                                     \

@@ -226,6 +226,22 @@ def test_cfg5_gatedkan_full_shape(gpu, cfg5_weights, fmt):
             print(f"cfg5 {fmt} B={B}: rel err {e:.3e}")
             assert np.isfinite(ys.astype(np.float32)).all()
             assert e <= TOL["float16"]
+        # fp32 x at B = 1 and 2: the in-kernel basis (each workgroup's range holds 4096 base inputs here)
+        # equals the separate basis kernel bit for bit
+        for B in (1, 2):
+            x32 = xs[32][:B].astype(np.float32)
+            outs = []
+            for mode in (2, 0):
+                prev = lib.kans_decode_set_pre_basis(mode)
+                try:
+                    y = np.empty((B, D_MODEL), np.float16)
+                    assert lib.kans_gated_forward_host(blk, x32.ctypes.data, 0, y.ctypes.data, 1, B, 1) == 0, \
+                        lib.kans_last_error()
+                finally:
+                    lib.kans_decode_set_pre_basis(prev)
+                outs.append(y)
+            print(f"cfg5 {fmt} fp32 x B={B}: in-kernel basis vs separate kernel", flush=True)
+            np.testing.assert_array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
     finally:
         lib.kans_gated_destroy(blk)
         for h in layers:
