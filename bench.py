@@ -520,11 +520,13 @@ COPIES = 3
 def run_cfg5(lib, warmup, iters, cpu=True):
     """GatedKAN d=4096, h=11008, K=4 (base on, no bias), all six weight matrices
     ~N(0, 0.02) then INT4 (group 64) or ternary (group 32), plus the north star's INT8 (group 64); x ~ N(0,1)
-    fp16.  Every line is one whole block forward (gate, up, SwiGLU, down) replayed as one HIP graph on
-    device-resident x / y, timed with HIP events.  Decode B in {1, 32} (INT4 / ternary GEMVs over the packed
-    weights): COPIES blocks with separate device weights, calls cycling through them (weights from HBM, not
-    the MALL); GB/s = algorithmic bytes (packed codes + group parameters + x + y) / time; the same block
-    replayed alone is reported beside it as the MALL-warm rate.  Prefill B = 8192 (fused kernels decoding
+    fp16.  Every line times whole block forwards (gate, up, SwiGLU, down) captured in HIP graphs on
+    device-resident x / y, with HIP events.  Decode B in {1, 32} (INT4 / ternary GEMVs over the packed
+    weights): COPIES blocks with separate device weights (weights from HBM, not the MALL) chained x -> y -> x
+    as one decode step captured in ONE graph, time per block; GB/s = algorithmic bytes (packed codes + group
+    parameters + x + y) / time.  Beside it: each block as its own graph, calls cycling through the copies
+    (ms_graph_per_block, which also carries one graph launch per block), and the same block replayed alone
+    (the MALL-warm rate).  Prefill B = 8192 (fused kernels decoding
     the packed weights into fp16 MFMA tiles, gate|up in one launch with the SwiGLU epilogue): TFLOP/s of
     2*B*(2*h*d + d*h)*(K + 1), and the packed bytes per forward."""
     d, hdim, K = 4096, 11008, 4
@@ -574,6 +576,11 @@ def run_cfg5(lib, warmup, iters, cpu=True):
                                                 ctypes.byref(ms))
                 if rc:
                     raise RuntimeError(lib.kans_last_error().decode())
+                per_graph = ms.value
+                # the decode step a serving loop replays: the ncopy blocks chained (x -> y -> x ...) in ONE graph
+                rc = lib.kans_gated_time_step(arr, ncopy, xd.p, yd.p, 1, B, min(warmup, it), it, ctypes.byref(ms))
+                if rc:
+                    raise RuntimeError(lib.kans_last_error().decode())
                 gbs = nbytes / ms.value / 1e6
                 if fmt not in stream_ceiling:
                     # one read-only streaming kernel (kans_stream_ceiling) over ncopy times the block's bytes, so
@@ -590,7 +597,11 @@ def run_cfg5(lib, warmup, iters, cpu=True):
                                                   "stream_ceiling_GB_per_s": stream_ceiling[fmt],
                                                   "frac_of_stream_ceiling": round(gbs / stream_ceiling[fmt], 4),
                                                   "bytes": int(nbytes), "batch": B,
-                                                  "timing": f"{ncopy} weight copies, calls rotating (from HBM)",
+                                                  "timing": f"decode step of {ncopy} blocks with separate weights "
+                                                            "(from HBM), chained and captured as one HIP graph; "
+                                                            "time per block",
+                                                  "ms_graph_per_block": round(per_graph, 5),
+                                                  "GB_per_s_graph_per_block": round(nbytes / per_graph / 1e6, 1),
                                                   "ms_mall_warm": round(warm, 5),
                                                   "GB_per_s_mall_warm": round(nbytes / warm / 1e6, 1)}
             xd.free()

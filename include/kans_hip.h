@@ -340,6 +340,12 @@ int kans_gated_time(kans_gated* block, const void* X, int x_dtype, void* Y, int 
  * its weights from HBM (measurement only; no reference counterpart) */
 int kans_gated_time_rotate(kans_gated* const* blocks, int n, const void* X, int x_dtype, void* Y, int y_dtype,
                            int B, int warmup, int iters, float* ms);
+/* mean ms per block forward of a decode step of the n blocks (d -> d each) captured as one HIP graph, the
+ * way a model runs its layers per step: block b reads block b-1's output (X and Y alternate; both device
+ * arrays [B][d] of `dtype`), each block streams its own weights (measurement only; no reference
+ * counterpart) */
+int kans_gated_time_step(kans_gated* const* blocks, int n, void* X, void* Y, int dtype, int B, int warmup, int iters,
+                         float* ms);
 /* algorithmic bytes of one block forward: packed weights + group parameters + x and y (fp16) */
 long long kans_gated_stream_bytes(const kans_gated* block, int B);
 /* The GatedKAN block computes SwiGLU(gate, up) and the down layer's basis in one step (on = 1, the

@@ -778,6 +778,57 @@ int time_blocks_locked(kans_gated* const* Gs, int n, const void* X, int x_dtype,
   return rc;
 }
 
+// Mean ms per block forward of a decode step of n blocks captured as ONE HIP
+// graph, as a model's step over its layers runs: block b reads the previous
+// block's output (X -> Y -> X ..., so x_dtype == y_dtype), each block streams
+// its own weights.  Lock held.
+static int time_step_locked(kans_gated* const* Gs, int n, void* X, int dtype, void* Y, int B, int warmup, int iters,
+                            float* ms) {
+  hipStream_t st = kans_default_stream();
+  const int d = Gs[0]->gate->D_in;
+  for (int b = 0; b < n; ++b)
+    if (Gs[b]->gate->D_in != d || Gs[b]->down->D_out != d)
+      return kans_fail(KANS_ERR_ARG, "a decode step chains blocks of one width d -> d");
+  auto step = [&]() -> int {
+    for (int b = 0; b < n; ++b) {
+      const void* in = (b & 1) ? Y : X;
+      void* out = (b & 1) ? X : Y;
+      int rc = gated_forward_locked(Gs[b], in, dtype, d, out, dtype, d, B, 1, st);
+      if (rc) return rc;
+    }
+    return 0;
+  };
+  int rc = step();  // sizes every workspace before the capture
+  if (rc) return rc;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  rc = step();
+  hipError_t e = hipStreamEndCapture(st, &graph);
+  if (!rc && e != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  if (!rc && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+    rc = kans_fail(KANS_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float t = 0.f;
+  for (int i = 0; i < warmup && !rc; ++i)
+    if (hipGraphLaunch(exec, st) != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipGraphLaunch failed");
+  if (!rc && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+    rc = kans_fail(KANS_ERR_HIP, "hipEventCreate failed");
+  if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipEventRecord failed");
+  for (int i = 0; i < iters && !rc; ++i)
+    if (hipGraphLaunch(exec, st) != hipSuccess) rc = kans_fail(KANS_ERR_HIP, "hipGraphLaunch failed");
+  if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+              hipEventElapsedTime(&t, e0, e1) != hipSuccess))
+    rc = kans_fail(KANS_ERR_HIP, "event timing failed");
+  if (rc) (void)hipStreamSynchronize(st);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  if (!rc) *ms = t / ((float)iters * n);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1047,6 +1098,17 @@ int kans_gated_time(kans_gated* G, const void* X, int x_dtype, void* Y, int y_dt
   int rc = kans_ensure_init();
   if (rc) return rc;
   return time_blocks_locked(&G, 1, X, x_dtype, Y, y_dtype, B, warmup, iters, use_graph, ms);
+}
+
+int kans_gated_time_step(kans_gated* const* blocks, int n, void* X, void* Y, int dtype, int B, int warmup, int iters,
+                         float* ms) {
+  if (!blocks || n <= 0 || !X || !Y || !ms || iters <= 0 || B <= 0) return kans_fail(KANS_ERR_ARG, "bad argument");
+  for (int b = 0; b < n; ++b)
+    if (!blocks[b]) return kans_fail(KANS_ERR_ARG, "null block");
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  int rc = kans_ensure_init();
+  if (rc) return rc;
+  return time_step_locked(blocks, n, X, dtype, Y, B, warmup, iters, ms);
 }
 
 int kans_gated_time_rotate(kans_gated* const* blocks, int n, const void* X, int x_dtype, void* Y, int y_dtype, int B,

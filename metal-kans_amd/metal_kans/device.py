@@ -123,6 +123,7 @@ SIGNATURES = {
     "kans_gated_forward_host": (c_int, [P, P, c_int, P, c_int, c_int, c_int]),
     "kans_gated_time": (c_int, [P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, P]),
     "kans_gated_time_rotate": (c_int, [P, c_int, P, c_int, P, c_int, c_int, c_int, c_int, P]),
+    "kans_gated_time_step": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, P]),
     "kans_gated_stream_bytes": (c_longlong, [P, c_int]),
     "kans_gated_set_fused_swiglu": (c_int, [c_int]),
     "kans_decode_set_pre_basis": (c_int, [c_int]),

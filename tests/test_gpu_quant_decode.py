@@ -249,6 +249,15 @@ def test_gated_block_decode(gpu, fmt, B, biased):
                 assert O.rel_err(y16.astype(np.float32), ref) <= 2e-2
                 outs.append(y16)
             assert np.array_equal(outs[0], outs[1])  # graph replays give the eager result
+            # a decode step of one block captured as one graph (kans_gated_time_step): X -> Y
+            arr = (ctypes.c_void_p * 1)(blk.value)
+            assert lib.kans_gated_time_step(arr, 1, xd, yd, DT_F16, B, 1, 3, ctypes.byref(ms)) == 0, \
+                lib.kans_last_error()
+            assert ms.value > 0
+            y16 = np.empty((B, d), np.float16)
+            assert lib.kans_memcpy_d2h(y16.ctypes.data, yd, y16.nbytes) == 0
+            assert np.array_equal(y16, outs[0])
+            assert lib.kans_gated_time_step(arr, 1, xd, yd, DT_F16, 0, 1, 3, ctypes.byref(ms)) == -1  # bad B
         finally:
             lib.kans_dev_free(xd)
             lib.kans_dev_free(yd)
