@@ -515,6 +515,7 @@ def cpu_cfg5(lib, fmt, packed, shapes, K, xs, out, batches):
 # so even the ternary block (254 MB, within the 256 MB MALL) streams from HBM, as in a model whose layers
 # together exceed the MALL.
 COPIES = 3
+DECODE_ITERS, DECODE_REPS = 40, 5
 
 
 def run_cfg5(lib, warmup, iters, cpu=True):
@@ -523,7 +524,7 @@ def run_cfg5(lib, warmup, iters, cpu=True):
     fp16.  Every line times whole block forwards (gate, up, SwiGLU, down) captured in HIP graphs on
     device-resident x / y, with HIP events.  Decode B in {1, 32} (INT4 / ternary GEMVs over the packed
     weights): COPIES blocks with separate device weights (weights from HBM, not the MALL) chained x -> y -> x
-    as one decode step captured in ONE graph, time per block; GB/s = algorithmic bytes (packed codes + group
+    as one decode step captured in ONE graph, time per block (median of DECODE_REPS timings); GB/s = algorithmic bytes (packed codes + group
     parameters + x + y) / time.  Beside it: each block as its own graph, calls cycling through the copies
     (ms_graph_per_block, which also carries one graph launch per block), and the same block replayed alone
     (the MALL-warm rate).  Prefill B = 8192 (fused kernels decoding
@@ -572,15 +573,24 @@ def run_cfg5(lib, warmup, iters, cpu=True):
             else:
                 warm = ms.value
                 arr = (ctypes.c_void_p * ncopy)(*[b.value for b in blocks])
-                rc = lib.kans_gated_time_rotate(arr, ncopy, xd.p, 1, yd.p, 1, B, max(ncopy, min(warmup, it)), it,
-                                                ctypes.byref(ms))
-                if rc:
-                    raise RuntimeError(lib.kans_last_error().decode())
-                per_graph = ms.value
+                # decode lines are tens of microseconds: median of DECODE_REPS timings of >= DECODE_ITERS
+                # replays each, so that one slow stretch (clock, another engine) does not set the line
+                dit = max(it, DECODE_ITERS)
+
+                def median_ms(call):
+                    vals = []
+                    for _ in range(DECODE_REPS):
+                        if call():
+                            raise RuntimeError(lib.kans_last_error().decode())
+                        vals.append(ms.value)
+                    return float(np.median(vals))
+
+                per_graph = median_ms(lambda: lib.kans_gated_time_rotate(
+                    arr, ncopy, xd.p, 1, yd.p, 1, B, max(ncopy, min(warmup, dit)), dit, ctypes.byref(ms)))
                 # the decode step a serving loop replays: the ncopy blocks chained (x -> y -> x ...) in ONE graph
-                rc = lib.kans_gated_time_step(arr, ncopy, xd.p, yd.p, 1, B, min(warmup, it), it, ctypes.byref(ms))
-                if rc:
-                    raise RuntimeError(lib.kans_last_error().decode())
+                step = median_ms(lambda: lib.kans_gated_time_step(
+                    arr, ncopy, xd.p, yd.p, 1, B, max(2, min(warmup, dit)), dit, ctypes.byref(ms)))
+                ms.value = step
                 gbs = nbytes / ms.value / 1e6
                 if fmt not in stream_ceiling:
                     # one read-only streaming kernel (kans_stream_ceiling) over ncopy times the block's bytes, so
