@@ -268,6 +268,67 @@ def test_gated_block_decode(gpu, fmt, B, biased):
             lib.kans_qlayer_destroy(h)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("B", [1, 2, 32])
+def test_gated_decode_step_graph(gpu, fmt, B):
+    """kans_gated_time_step: three blocks chained x -> y -> x -> y (x = X's buffer, y = Y's).  The
+    uncaptured step leaves x2 = f2(f1(x)) in X; one graph replay then leaves f2(f1(x2)) in X and
+    f3(f2(f1(x2))) in Y, bit for bit the eager block forwards (round16 on, fp16 activations, as the
+    step runs them)."""
+    lib = gpu
+    d, hdim, K = 96, 200, 4
+    layers, blocks = [], []
+    for bi in range(3):
+        ls = []
+        for i, (di, do) in enumerate(((d, hdim), (d, hdim), (hdim, d))):
+            h, _ = make_qlayer(lib, fmt, di, do, K, True, bi == 1, seed=300 + 10 * bi + i)
+            ls.append(h)
+        blk = ctypes.c_void_p()
+        assert lib.kans_gated_create(*ls, ctypes.byref(blk)) == 0, lib.kans_last_error()
+        layers += ls
+        blocks.append(blk)
+    xd, yd = ctypes.c_void_p(), ctypes.c_void_p()
+    try:
+        x = np.random.default_rng(40 + B).normal(0, 1, (B, d)).astype(np.float16)
+        chain = [x]
+        for blk in blocks:
+            y = np.empty((B, d), np.float16)
+            assert lib.kans_gated_forward_host(blk, chain[-1].ctypes.data, DT_F16, y.ctypes.data, DT_F16, B, 1) == 0, \
+                lib.kans_last_error()
+            chain.append(y)
+        assert lib.kans_dev_malloc(ctypes.byref(xd), x.nbytes) == 0
+        assert lib.kans_dev_malloc(ctypes.byref(yd), x.nbytes) == 0
+        assert lib.kans_memcpy_h2d(xd, x.ctypes.data, x.nbytes) == 0
+        arr = (ctypes.c_void_p * 3)(*[b.value for b in blocks])
+        ms = ctypes.c_float()
+        # no warm-up, one timed replay
+        assert lib.kans_gated_time_step(arr, 3, xd, yd, DT_F16, B, 0, 1, ctypes.byref(ms)) == 0, \
+            lib.kans_last_error()
+        assert ms.value > 0
+        got_x, got_y = np.empty_like(x), np.empty_like(x)
+        assert lib.kans_memcpy_d2h(got_x.ctypes.data, xd, x.nbytes) == 0
+        assert lib.kans_memcpy_d2h(got_y.ctypes.data, yd, x.nbytes) == 0
+        print(f"step {fmt} B={B}: {ms.value * 1e3:.1f} us per block")
+        assert np.isfinite(chain[3].astype(np.float32)).all()
+        x2 = chain[2]
+        ref = [x2]
+        for blk in blocks:
+            y = np.empty((B, d), np.float16)
+            assert lib.kans_gated_forward_host(blk, ref[-1].ctypes.data, DT_F16, y.ctypes.data, DT_F16, B, 1) == 0
+            ref.append(y)
+        assert np.array_equal(got_x, ref[2])
+        assert np.array_equal(got_y, ref[3])
+        assert lib.kans_gated_time_step(arr, 3, xd, yd, 9, B, 0, 1, ctypes.byref(ms)) < 0  # bad dtype
+    finally:
+        for p_ in (xd, yd):
+            if p_.value:
+                lib.kans_dev_free(p_)
+        for blk in blocks:
+            lib.kans_gated_destroy(blk)
+        for h in layers:
+            lib.kans_qlayer_destroy(h)
+
+
 GATED_EDGE = [  # d, h, K of gate/up, K of down, down has base, biased
     (96, 200, 4, 4, True, True), (40, 65, 3, 5, False, False), (128, 64, 4, 1, True, True),
     (72, 130, 2, 32, True, False), (512, 1000, 4, 4, True, True), (2048, 256, 4, 4, True, True)]
