@@ -131,11 +131,11 @@ class KANLayerBase:
         if D_in != self.in_features:
             raise ValueError(f"Expected in_features={self.in_features}, got {D_in}")
 
-        # a layer quantized from fp16 runs on its packed weights (fused quantized kernels)
+        # a layer quantized from fp16 / bf16 runs on its packed weights (fused quantized kernels)
         from ._qengine import layer_engine
         qeng = layer_engine(self) if B > 0 else None
         if qeng is not None and qeng.fused(B):
-            y = qeng.forward_host(x, np.float16)
+            y = qeng.forward_host(x, np.float16 if compute == "float16" else "bfloat16")
             if len(orig_shape) > 2:
                 return y.reshape(*orig_shape[:-1], self.out_features)
             return y

@@ -20,7 +20,7 @@ from typing import Optional
 import numpy as np
 
 from . import device
-from ._engine import DT_BF16, DT_F16, DT_F32
+from ._engine import DT_BF16, DT_F16, DT_F32, from_bf16_bits
 
 MAX_DECODE_B = 32
 # Chebyshev degrees (coefficients per feature) the fused prefill kernel is built for (the GatedKAN block;
@@ -140,24 +140,30 @@ class QLayerEngine:
         return B > 0 and device.get_metal_bridge().kans_qlayer_fused(self.handle, int(B)) == 1
 
     def forward_host(self, x: np.ndarray, out_dtype) -> np.ndarray:
+        """y = layer(x) on the packed weights; out_dtype np.float16, np.float32 or "bfloat16" (the
+        result rounded to bf16, returned as float32 values)."""
         x = np.ascontiguousarray(x)
         B = x.shape[0]
         xdt = DT_F16 if x.dtype == np.float16 else DT_F32
         if xdt == DT_F32 and x.dtype != np.float32:
             x = x.astype(np.float32)
-        y = np.empty((B, self.d_out), dtype=out_dtype)
-        ydt = DT_F16 if out_dtype == np.float16 else DT_F32
+        bf16 = isinstance(out_dtype, str) and out_dtype == "bfloat16"
+        y = np.empty((B, self.d_out), dtype=np.uint16 if bf16 else out_dtype)
+        ydt = DT_BF16 if bf16 else DT_F16 if out_dtype == np.float16 else DT_F32
         device.check(device.get_metal_bridge().kans_qlayer_forward_host(self.handle, x.ctypes.data, xdt, y.ctypes.data,
                                                                           ydt, B), "kans_qlayer_forward_host")
-        return y
+        return from_bf16_bits(y).reshape(B, self.d_out) if bf16 else y
 
 
 def layer_engine(layer) -> Optional["QLayerEngine"]:
-    """The fused quantized engine of a KAN layer (Chebyshev, RBF, B-spline) that computes in fp16 after
-    ``to_int8`` / ``to_int4`` / ``to_ternary`` (cached on the layer, rebuilt when its packed weights or basis
-    parameters change), else None."""
+    """The fused quantized engine of a KAN layer (Chebyshev, RBF, B-spline) that computes in fp16 or bf16
+    after ``to_int8`` / ``to_int4`` / ``to_ternary`` (cached on the layer, rebuilt when its packed weights or
+    basis parameters change), else None.  A bf16 layer runs the same kernels: fp16 basis values and decoded
+    weights (each at least as precise as its bf16 rounding in the value ranges these take), fp32
+    accumulation, the result rounded to bf16."""
+    q = getattr(layer, "_quantized_from", None)
     if getattr(layer, "_basis", "") not in ("cheby", "rbf", "bspline") \
-            or getattr(layer, "_quantized_from", None) != "float16" or layer._resolve_compute() != "float16":
+            or q not in ("float16", "bfloat16") or layer._resolve_compute() != q:
         return None
     fmt = packed_format(layer)
     if fmt is None:

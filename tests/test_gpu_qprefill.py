@@ -373,6 +373,47 @@ def test_python_quantized_fp16_layer_uses_packed_weights(gpu, quant, degree):
 
 
 @pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+@pytest.mark.parametrize("kind", ["cheby4", "cheby3", "rbf", "bspline"])
+def test_python_quantized_bf16_layer_uses_packed_weights(gpu, quant, kind):
+    """A bf16 layer quantized with to_<quant>() keeps bf16 compute and runs on its packed weights: the
+    same kernels as the fp16 layer (fp16 basis values and decoded weights, fp32 accumulation) with the
+    result rounded to bf16, at the decode (B = 5) and prefill (B = 300) sizes."""
+    import metal_kans as mk
+    from metal_kans._engine import from_bf16_bits, to_bf16_bits
+    np.random.seed(11)
+    if kind.startswith("cheby"):
+        L = mk.ChebyKAN(80, 48, degree=int(kind[-1]))
+    elif kind == "rbf":
+        L = mk.FastKAN(80, 48, num_centers=8, grid_range=(-2.0, 2.0))
+    else:
+        L = mk.BSplineKAN(80, 48, grid_size=5)
+    L.bias = np.random.normal(0, 0.1, 48).astype(np.float32)
+    L.bfloat16()
+    getattr(mk, f"to_{quant}")(L)
+    if kind.startswith("cheby"):
+        spec = {"W": L.w_cheby, "W_base": L.w_base, "bias": L.bias.astype(np.float32), "K": L.degree}
+    else:
+        params = ({"G": L.grid_size, "grid_min": float(L.grid_params[0]), "inv_h": float(L.grid_params[1])}
+                  if kind == "bspline" else {"grid": np.asarray(L.grid, np.float64), "inv_den": L.inv_denominator})
+        spec = {"W": getattr(L, L._weight_attr), "W_base": L.w_base, "bias": L.bias.astype(np.float32),
+                "K": L._num_basis(), "kind": L._basis, "params": params}
+    for B in (5, 300):
+        x = np.random.default_rng(B).normal(0, 1, (B, 80)).astype(np.float32)
+        y = L(x)
+        assert y.shape == (B, 48)
+        eng = L.__dict__.get("_qlayer_engine")
+        assert eng is not None
+        if not eng.fused(B):
+            assert B > 32 and (kind, quant) == ("bspline", "int8")  # not built: dequantized weights
+        y32 = np.asarray(y, np.float32)
+        assert np.array_equal(from_bf16_bits(to_bf16_bits(y32)).reshape(y32.shape), y32)  # bf16 values
+        assert O.rel_err(y32, oracle(spec, x)) <= 2e-2
+        if eng.fused(B):
+            # against the fp16-operand forward: only the bf16 rounding of the output (2^-9 of |y|) apart
+            assert O.rel_err(y32, _oracle_rounded(spec, x, weights16=B > 32)) <= 5e-3
+
+
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
 def test_python_gatedkan_prefill(gpu, quant):
     """GatedKAN(dtype=float16).to_<quant>() at B > 32 runs the fused prefill block."""
     import metal_kans as mk
