@@ -199,13 +199,16 @@ class GatedEngine:
         return all(e.current(k) for e, k in zip(self.layers, (block.gate_kan, block.up_kan, block.down_kan)))
 
     def forward_host(self, x: np.ndarray, out_dtype, round16: int) -> np.ndarray:
+        """The block on the packed weights; out_dtype np.float16, np.float32 or "bfloat16" (returned as
+        float32 values); round16 1 / 2 rounds gate, up and hidden to fp16 / bf16."""
         x = np.ascontiguousarray(x)
         B = x.shape[0]
         xdt = DT_F16 if x.dtype == np.float16 else DT_F32
         if xdt == DT_F32 and x.dtype != np.float32:
             x = x.astype(np.float32)
-        y = np.empty((B, self.d_model), dtype=out_dtype)
-        ydt = DT_F16 if out_dtype == np.float16 else DT_F32
+        bf16 = isinstance(out_dtype, str) and out_dtype == "bfloat16"
+        y = np.empty((B, self.d_model), dtype=np.uint16 if bf16 else out_dtype)
+        ydt = DT_BF16 if bf16 else DT_F16 if out_dtype == np.float16 else DT_F32
         device.check(device.get_metal_bridge().kans_gated_forward_host(self.handle, x.ctypes.data, xdt, y.ctypes.data,
                                                                          ydt, B, round16), "kans_gated_forward_host")
-        return y
+        return from_bf16_bits(y).reshape(B, self.d_model) if bf16 else y

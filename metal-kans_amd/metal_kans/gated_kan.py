@@ -17,8 +17,9 @@ Quantized path: a float16 block quantized with ``to_int8()`` / ``to_int4()``
 (``_qengine.GatedEngine``): the packed weights are read from HBM once per
 forward instead of being dequantized, and gate/up, SwiGLU and down run back to
 back on the device (decode GEMVs up to 32 rows, the fused prefill kernels -- one
-launch for gate|up with the SwiGLU epilogue, one for down -- above).  Other
-cases use the three layers.
+launch for gate|up with the SwiGLU epilogue, one for down -- above).  A block
+whose three layers were bf16 when quantized takes the same kernels with gate,
+up, hidden and the result rounded to bf16.  Other cases use the three layers.
 """
 from __future__ import annotations
 
@@ -61,9 +62,20 @@ class GatedKAN:
         self._saved_up = None
         self._saved_hidden = None
 
+    def _packed_compute(self) -> Optional[str]:
+        """"float16" for a float16 block, "bfloat16" when its three layers were bf16 when quantized and
+        still compute in bf16, else None (no packed-weight path)."""
+        if self.dtype == np.float16:
+            return "float16"
+        layers = (self.gate_kan, self.up_kan, self.down_kan)
+        if all(getattr(k, "_quantized_from", None) == "bfloat16" and k._resolve_compute() == "bfloat16"
+               for k in layers):
+            return "bfloat16"
+        return None
+
     def _decode_engine(self) -> Optional[GatedEngine]:
         """The fused quantized block, when this block's weights allow it (see module docstring)."""
-        if self.dtype != np.float16:
+        if self._packed_compute() is None:
             return None
         fmt = packed_format(self.gate_kan)
         if fmt is None or packed_format(self.up_kan) != fmt or packed_format(self.down_kan) != fmt:
@@ -136,7 +148,12 @@ class GatedKAN:
         if x_2d.shape[0] > 0:
             eng = self._decode_engine()
             if eng is not None and fused_batch_ok(eng.fmt, self.degree, x_2d.shape[0]):
-                out = eng.forward_host(x_2d if x_2d.dtype == np.float16 else x_2d.astype(np.float32), np.float16, 1)
+                if self._packed_compute() == "bfloat16":
+                    # the fp16 kernels, gate / up / hidden and the result rounded to bf16
+                    out = eng.forward_host(np.asarray(x_2d, np.float32), "bfloat16", 2)
+                else:
+                    out = eng.forward_host(x_2d if x_2d.dtype == np.float16 else x_2d.astype(np.float32),
+                                           np.float16, 1)
                 self._saved_gate = self._saved_up = self._saved_hidden = None
                 if len(orig_shape) > 2:
                     return out.reshape(*orig_shape[:-1], self.d_model)

@@ -293,8 +293,11 @@ def make_block(lib, fmt, d, hdim, K=4, bias=False, seed=0):
 
 def gated_oracle(specs, x, round16):
     """float64 oracle block on the dequantized weights; with round16 the gate / up / hidden activations are
-    rounded to fp16, as a 16-bit model stores them."""
-    r = (lambda a: a.astype(np.float16).astype(np.float64)) if round16 else (lambda a: a)  # noqa: E731
+    rounded to fp16 (1) or bf16 (2), as a 16-bit model stores them."""
+    if round16 == 2:
+        r = lambda a: O.bf16_to_f32(O.bf16_round(a.astype(np.float32))).astype(np.float64)  # noqa: E731
+    else:
+        r = (lambda a: a.astype(np.float16).astype(np.float64)) if round16 else (lambda a: a)  # noqa: E731
     f = lambda L, z: O.kan_forward("cheby", z, L["W"], L["W_base"], L["bias"], {"K": L["K"]})  # noqa: E731
     g, u = r(f(specs[0], x)), r(f(specs[1], x))
     return f(specs[2], r(O.silu_clipped(g) * u))
@@ -428,6 +431,29 @@ def test_python_gatedkan_prefill(gpu, quant):
              for k in (blk.gate_kan, blk.up_kan, blk.down_kan)]
     ref = gated_oracle(specs, x.reshape(-1, 96).astype(np.float64), 1)
     assert O.rel_err(out.reshape(-1, 96).astype(np.float32), ref) <= 2e-2
+
+
+@pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
+def test_python_gatedkan_bf16_packed(gpu, quant):
+    """A GatedKAN whose layers were made bf16 before to_<quant>() runs the packed-weight block (decode at
+    B = 6, prefill at B = 150) with gate, up, hidden and the result rounded to bf16."""
+    import metal_kans as mk
+    from metal_kans._engine import from_bf16_bits, to_bf16_bits
+    np.random.seed(5)
+    blk = mk.GatedKAN(d_model=96, d_ffn=200, degree=4)
+    for k in (blk.gate_kan, blk.up_kan, blk.down_kan):
+        k.bfloat16()
+    getattr(blk, f"to_{quant}")()
+    specs = [{"W": k.w_cheby, "W_base": k.w_base, "bias": None, "K": 4}
+             for k in (blk.gate_kan, blk.up_kan, blk.down_kan)]
+    for B in (6, 150):
+        x = np.random.default_rng(B).normal(0, 1, (B, 96)).astype(np.float32)
+        out = blk(x)
+        assert blk.__dict__.get("_qblock") is not None
+        assert out.shape == (B, 96) and out.dtype == np.float32
+        assert np.array_equal(from_bf16_bits(to_bf16_bits(out)).reshape(out.shape), out)
+        ref = gated_oracle(specs, x.astype(np.float64), 2)
+        assert O.rel_err(out, ref) <= 2e-2
 
 
 @pytest.mark.parametrize("quant", ["int8", "int4", "ternary"])
