@@ -186,6 +186,10 @@ int kans_layer_set_tiling(kans_layer* layer, int wm, int nb, int splits);
    (32,1); elsewhere 1).  The groups split a tile's feature blocks and add their partial sums in a fixed
    order through LDS.  No reference counterpart (the reference has no tiling). */
 int kans_layer_set_wave_groups(kans_layer* layer, int groups);
+/* 8-wave 16-bit Chebyshev block kernel (one barrier per feature block): 1 (default) holds two feature
+   blocks in each LDS stage when both fit (K + has_base <= 5), so one barrier closes two blocks; 0 keeps
+   one.  Results are identical.  For tuning and tests; no reference counterpart. */
+int kans_layer_set_block_pairs(kans_layer* layer, int on);
 int kans_layer_describe(const kans_layer* layer, int B, int* wm, int* nb, int* splits);
 /* name of the fused kernel (and its tile) that a forward of batch B runs, NUL-terminated in name[len] */
 int kans_layer_kernel(const kans_layer* layer, int B, char* name, int len);

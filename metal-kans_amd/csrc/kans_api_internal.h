@@ -21,6 +21,7 @@ struct DenseLaunch {
   BasisParams bp;
   int wm, nb, splits;   // tile config
   int ks = 1;           // wave groups per workgroup (4-wave block kernel, block_wave_groups_ok)
+  int pair = 1;         // block kernels: two feature blocks per LDS stage when they fit (kan_fused_block)
 };
 
 // RBF parameters (centres, scaled centres, recurrence eligibility) of bp (bp.K set) from K centres and

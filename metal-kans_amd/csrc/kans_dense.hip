@@ -365,7 +365,7 @@ __host__ __device__ constexpr int block_min_wgs(int waves, int nb, int ks) {
   return waves == 4 && (ks == 1 || (ks == 2 && nb == 1)) ? 2 : 1;
 }
 
-template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES, int KS = 1>
+template <typename T, typename TX, typename TY, int BASIS, int WM, int NB, int WAVES, int KS = 1, bool PAIR = false>
 __global__ void __launch_bounds__(WAVES * 64 * KS, block_min_wgs(WAVES, NB, KS))
 kan_fused_block(const TX* __restrict__ X, long ldx,
                 const uint4* __restrict__ Wt, int nob_pad,
@@ -512,8 +512,17 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
     if (tid <= bp.K) rbf_tab[tid] = tid < bp.K ? bp.rbf_sc[tid] : 0.0f;
     gen.tab = rbf_tab;
   }
+  // PAIR: two feature blocks per stage (the launcher checks 2 KP <= SLOTS): one
+  // barrier per two blocks, the DMA of block fb + 2 issued in block fb into the
+  // same half of the other stage.  Same arithmetic in the same order as one
+  // block per stage.  A separate instantiation, so that the one-block kernels
+  // keep their registers and schedule.
+  static_assert(!PAIR || (KS == 1 && !kTab), "block pairs: one wave group, slot-loop kernels");
   if (KS == 1 || gb < ge) {
     dma(gb, st0);
+    if constexpr (PAIR) {
+      if (gb + 1 < ge) dma(gb + 1, st0 + KP * SLOT);
+    }
     xload(gb);
   }
   __syncthreads();
@@ -606,7 +615,9 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  auto block = [&](int fb, const uint4* cur, uint4* nxt) {
+  // ahead: the block whose weights this one copies into nxt (fb + 1, or fb + 2
+  // with two blocks per stage)
+  auto block = [&](int fb, const uint4* cur, uint4* nxt, int ahead) {
     float xf[NV];
     xunpack(fb, xf);
     if (fb + 1 < ge) xload(fb + 1);
@@ -615,8 +626,8 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
       // branch-free; waited for by the closing barrier like the others)
       dsrc = wtile + (long)min(fb + 1, ge - 1) * KP * nob_pad * 64;
       ddst = nxt;
-    } else if (fb + 1 < ge) {
-      dma(fb + 1, nxt);
+    } else if (fb + ahead < ge) {
+      dma(fb + ahead, nxt);
     }
     if constexpr (kTab) {
       // the table first: its selector reads and temporaries die before the
@@ -674,21 +685,36 @@ kan_fused_block(const TX* __restrict__ X, long ldx,
   // each block ends with the barrier that waits for its successor's DMA and
   // input loads and frees its stage
   if constexpr (KS == 1) {
-    for (int fb = fb_begin; fb < fb_end; fb += 2) {
-      block(fb, st0, st1);
-      __syncthreads();
-      if (fb + 1 < fb_end) {
-        block(fb + 1, st1, st0);
+    if constexpr (PAIR) {
+      uint4* const st0b = st0 + KP * SLOT;
+      uint4* const st1b = st1 + KP * SLOT;
+      for (int fb = fb_begin; fb < fb_end; fb += 4) {
+        block(fb, st0, st1, 2);
+        if (fb + 1 < fb_end) block(fb + 1, st0b, st1b, 2);
         __syncthreads();
+        if (fb + 2 < fb_end) {
+          block(fb + 2, st1, st0, 2);
+          if (fb + 3 < fb_end) block(fb + 3, st1b, st0b, 2);
+          __syncthreads();
+        }
+      }
+    } else {
+      for (int fb = fb_begin; fb < fb_end; fb += 2) {
+        block(fb, st0, st1, 1);
+        __syncthreads();
+        if (fb + 1 < fb_end) {
+          block(fb + 1, st1, st0, 1);
+          __syncthreads();
+        }
       }
     }
   } else {
     // every group runs `rounds` rounds; a group past its run only joins the barrier
     for (int it = 0; it < rounds; it += 2) {
-      if (gb + it < ge) block(gb + it, st0, st1);
+      if (gb + it < ge) block(gb + it, st0, st1, 1);
       __syncthreads();
       if (it + 1 < rounds) {
-        if (gb + it + 1 < ge) block(gb + it + 1, st1, st0);
+        if (gb + it + 1 < ge) block(gb + it + 1, st1, st0, 1);
         __syncthreads();
       }
     }
@@ -914,9 +940,20 @@ static hipError_t launch_dense_t(const DenseLaunch& L, hipStream_t st) {
       const int m_tiles8 = (L.B + 8 * WM - 1) / (8 * WM);
       auto go = [&](auto BBC) {
         constexpr int BB = decltype(BBC)::value;
-        hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8>), dim3(m_tiles8 * n_tiles, splits), dim3(512),
-                           0, st, (const TX*)L.X, L.ldx, (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y,
-                           L.ldy, part, L.B, L.D_in, L.D_out, m_tiles8, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+        auto launch = [&](auto PC) {
+          hipLaunchKernelGGL((kan_fused_block<T, TX, TY, BB, WM, NB, 8, 1, decltype(PC)::value>),
+                             dim3(m_tiles8 * n_tiles, splits), dim3(512), 0, st, (const TX*)L.X, L.ldx,
+                             (const uint4*)L.Wt, L.nob_pad, (const T*)L.bias, (TY*)L.Y, L.ldy, part, L.B, L.D_in,
+                             L.D_out, m_tiles8, n_tiles, L.nfb, fbps, L.has_base, L.bp);
+        };
+        // two feature blocks per LDS stage (Chebyshev, K + has_base <= 5)
+        if constexpr (BB == BASIS_CHEBY_POST) {
+          if (L.pair && 2 * (L.bp.K + L.has_base) <= block_slots(8, BB)) {
+            launch(std::true_type{});
+            return;
+          }
+        }
+        launch(std::false_type{});
       };
       if constexpr (BASIS == BASIS_RBF) {
         // uniform centres: the two-multiply recurrence; otherwise exp2 per value

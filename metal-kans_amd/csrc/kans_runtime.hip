@@ -129,6 +129,7 @@ struct kans_layer {
   bool have_weights = false;
   int forced_wm = 0, forced_nb = 0, forced_splits = 0;  // tuning overrides (0 = heuristic)
   int forced_ks = 0;  // wave groups per workgroup override (0 = heuristic)
+  int block_pairs = 1;  // block kernels: two feature blocks per LDS stage when they fit
   unsigned gen = 0;  // bumped whenever a buffer captured by a graph may have moved
 };
 
@@ -265,6 +266,14 @@ int kans_layer_set_wave_groups(kans_layer* L, int groups) {
   if (groups != 0 && groups != 1 && groups != 2 && groups != 4)
     return kans_fail(KANS_ERR_ARG, "wave groups must be 0 (automatic), 1, 2 or 4");
   L->forced_ks = groups;
+  ++L->gen;
+  return 0;
+}
+
+int kans_layer_set_block_pairs(kans_layer* L, int on) {
+  if (!L) return kans_fail(KANS_ERR_ARG, "null layer");
+  if (on != 0 && on != 1) return kans_fail(KANS_ERR_ARG, "block pairs must be 0 or 1");
+  L->block_pairs = on;
   ++L->gen;
   return 0;
 }
@@ -486,6 +495,7 @@ static int layer_launch_locked(kans_layer* L, const void* X, long ldx, void* Y, 
   if (cfg_B <= 0) cfg_B = B;
   choose_tiling(L, cfg_B, &D.wm, &D.nb, &D.splits);
   D.ks = choose_wave_groups(L, cfg_B, D.wm, D.nb, D.splits);
+  D.pair = L->block_pairs;
   if (D.splits > 1) {
     if (L->part.cap < (size_t)D.splits * B * L->D_out * sizeof(float))
       return kans_fail(KANS_ERR_STATE, "split workspace not reserved");
@@ -685,6 +695,7 @@ static int layer_kernel_name(const kans_layer* L, int B, bool io, int x_dtype, i
   const int ks = choose_wave_groups(L, B, wm, nb, splits);
   char groups[32] = "";
   if (ks > 1) snprintf(groups, sizeof groups, " x %d groups", ks);
+  const bool pairs = waves == 8 && L->basis == BASIS_CHEBY && L->block_pairs && 2 * (L->K + L->has_base) <= 10;
   char types[64];
   if (io)
     snprintf(types, sizeof types, "%s, %s, %s", dt[L->dtype], dt[x_dtype == DT_F32 ? DT_F32 : L->dtype],
@@ -701,7 +712,9 @@ static int layer_kernel_name(const kans_layer* L, int B, bool io, int x_dtype, i
                  wm, nb, waves, groups);
   else
     n = snprintf(name, len, "kans::kan_fused_dense<%s, %s, %d, %d>", types, bs[L->basis], wm, nb);
-  if (n >= 0 && splits > 1) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);
+  if (n >= 0 && splits > 1)
+    n += snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), " x %d feature splits", splits);
+  if (n >= 0 && pairs) snprintf(name + std::min(n, len - 1), len - std::min(n, len - 1), ", 2 feature blocks per stage");
   return 0;
 }
 

@@ -71,6 +71,7 @@ SIGNATURES = {
     "kans_layer_set_bspline": (c_int, [P, c_int, c_float, c_float]),
     "kans_layer_set_tiling": (c_int, [P, c_int, c_int, c_int]),
     "kans_layer_set_wave_groups": (c_int, [P, c_int]),
+    "kans_layer_set_block_pairs": (c_int, [P, c_int]),
     "kans_layer_describe": (c_int, [P, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
     "kans_layer_kernel": (c_int, [P, c_int, ctypes.c_char_p, c_int]),
     "kans_layer_kernel_ex": (c_int, [P, c_int, c_int, c_int, ctypes.c_char_p, c_int]),

@@ -138,6 +138,37 @@ def test_block_kernel_256x256_tile(gpu, dtype, kind, K, base, bias):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("K,base,bias", [(4, True, True), (4, False, False), (2, True, False), (1, False, True)])
+@pytest.mark.parametrize("d_in", [112, 200, 16, 40])
+def test_block_kernel_two_blocks_per_stage(gpu, dtype, K, base, bias, d_in):
+    """8-wave Chebyshev block kernel with K + base <= 5: two feature blocks per LDS stage (one barrier per
+    pair) against one block per stage, bit for bit, and against the oracle; 7, 13 (ragged), 1 and 3
+    feature blocks, with and without feature splits (odd and one-block splits)."""
+    import metal_kans as mk
+    L = make_layer(mk, "cheby", d_in, 300, K, bias=bias, base=base, seed=23)
+    x = np.random.default_rng(7).uniform(-1.3, 1.3, (520, d_in)).astype(np.float32)
+    y_ref = oracle_of(L, x)
+    cast(L, dtype)
+    for splits in (1, 2, 3):
+        L.set_tiling(32, 8, splits)
+        L(x)  # the device layer exists after its first forward
+        h = L._engine().handle
+        outs = []
+        for on in (1, 0):
+            assert gpu.kans_layer_set_block_pairs(h, on) == 0
+            y = np.asarray(L(x), np.float32)
+            assert O.rel_err(y, y_ref) <= TOL[dtype], (splits, on)
+            name = ctypes.create_string_buffer(200)
+            assert gpu.kans_layer_kernel(h, 520, name, 200) == 0
+            assert b"32, 8, 8 waves>" in name.value, name.value
+            assert (b"2 feature blocks per stage" in name.value) == bool(on), name.value
+            outs.append(y)
+        assert np.array_equal(outs[0], outs[1]), splits
+    assert gpu.kans_layer_set_block_pairs(h, 2) < 0
+    assert gpu.kans_layer_set_block_pairs(h, 1) == 0
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("K,base,bias", [(9, True, True), (4, False, True), (1, True, False)])
 @pytest.mark.parametrize("d_in", [200, 64, 16])
 def test_block_kernel_small_tile_stages(gpu, dtype, K, base, bias, d_in):
