@@ -370,6 +370,11 @@ int kans_decode_set_pre_basis(int mode);
  * Results do not depend on it.  Returns the previous mode, or a negative error code for a mode
  * outside 0..2 (no reference counterpart: a tuning and test switch). */
 int kans_decode_set_weight_loads(int mode);
+/* Quantized prefill kernel at Chebyshev K = 4 (the GatedKAN shape): 1 (the default) holds two feature
+ * blocks in each LDS stage, so one barrier closes two blocks; 0 one block per stage.  Results are
+ * identical.  Returns the previous setting, or a negative error code (no reference counterpart: a tuning
+ * and test switch). */
+int kans_prefill_set_block_pairs(int on);
 
 /* Measured ceilings for the roofline report (no reference counterpart; measurement only).
  * kans_mfma_ceiling: TFLOP/s of back-to-back v_mfma_f32_32x32x16 (dtype DT_F16 / DT_BF16) on 16 A and

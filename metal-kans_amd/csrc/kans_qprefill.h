@@ -124,6 +124,10 @@ struct QPLaunch {
   int epi, round16;
 };
 
+// Chebyshev K = 4 prefill kernels: two feature blocks per LDS stage (1, the
+// default) or one (0); kans_prefill_set_block_pairs.
+extern int g_qp_block_pairs;
+
 // Split-K workspace floats a launch needs (0 when unsplit).
 long qp_part_floats(const QPLaunch& L);
 // Feature splits the launcher picks for B rows (so the grid fills the GPU).

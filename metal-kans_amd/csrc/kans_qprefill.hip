@@ -181,6 +181,8 @@ long qp_part_floats(const QPLaunch& L) {
   return (long)L.splits * L.B * n_tiles * 256;
 }
 
+int g_qp_block_pairs = 1;
+
 hipError_t qp_launch(const QPLaunch& L, hipStream_t st) {
   if (!qp_supported(L.qt, L.K, L.has_base, L.basis, L.bp.rbf_rec) || (L.grp != 4 && L.grp != 8) || L.B <= 0 ||
       (L.basis != BASIS_CHEBY && (L.grp != 8 || L.bp.K != L.K)))

@@ -266,6 +266,7 @@ struct QPArgs {
   int B, D_in, m_tiles, n_tiles, nfb, fb_per_split;
   int epi, round16;
   BasisParams bp;  // RBF / B-spline parameters
+  int pair;        // dispatch: two feature blocks per LDS stage (PAIR instantiation) where built
 };
 
 }  // namespace
@@ -275,8 +276,12 @@ struct QPArgs {
 // feature (1 .. kQPMaxK); HB: SiLU base branch; BASIS: the A-fragment generator
 // (BASIS_CHEBY_POST, BASIS_RBF_REC, BASIS_BSPLINE; see BasisGen).  Grid:
 // m_tiles * n_tiles workgroups (x) by feature splits (y), 512 threads.
+// PAIR: each LDS stage holds two feature blocks (2 KP <= 10 slots, a group
+// geometry that repeats every block): one barrier per two blocks, and the
+// block decoded during block fb is fb + 2, into the same half of the other
+// stage.  The arithmetic and its order are those of one block per stage.
 // ---------------------------------------------------------------------------
-template <int QT, int KQ, int HB, int BASIS = BASIS_CHEBY_POST>
+template <int QT, int KQ, int HB, int BASIS = BASIS_CHEBY_POST, bool PAIR = false>
 __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   constexpr int KP = KQ + HB;
   constexpr int NV = 8;
@@ -295,8 +300,11 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
   constexpr int PER = qp_period(KQ, GS);
   static_assert(NGRP <= 3 && (PER == 1 || PER == 2 || PER == 4), "group geometry");
 
-  __shared__ uint4 stage0[KP * SLOT];
-  __shared__ uint4 stage1[KP * SLOT];
+  static_assert(!PAIR || (PER == 1 && 2 * KP <= 10 && BASIS != BASIS_BSPLINE_TAB), "block pairs");
+  constexpr int AH = PAIR ? 2 : 1;          // blocks between the one multiplied and the one decoded
+  constexpr int HALF = KP * SLOT;           // uint4 of one feature block's tiles
+  __shared__ uint4 stage0[(PAIR ? 2 : 1) * HALF];
+  __shared__ uint4 stage1[(PAIR ? 2 : 1) * HALF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -534,6 +542,21 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     });
     load_all(fb_begin + 1, Ph1{}, R);
   }
+  if constexpr (PAIR) {
+    // block fb_begin + 1 into the second half of stage 0 (past the split: the
+    // clamped last block, never read); the registers then hold fb_begin + 2
+    DqGroups<NGRP> pb;
+    DqGroups<1> pw;
+    params_of(R, pb, pw);
+    const bool tail = is_tail(fb_begin + 1);
+    static_for<0, KP>([&](auto SCC) __attribute__((always_inline)) {
+      constexpr int SC = decltype(SCC)::value;
+      uint4 d = dq_slot(SCC, Ph0{}, R, pb, pw);
+      if (tail) mask_tail(fb_begin + 1, d);
+      stage0[HALF + (SC * kQNB + wave) * 64 + lane] = d;
+    });
+    load_all(fb_begin + 2, Ph0{}, R);
+  }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
@@ -552,11 +575,12 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     gen_emit_tab<decltype(KNC)::value>(gen, a1);
   };
 
-  // One feature block: MFMAs of block fb from `cur`, decode of block fb + 1 (in
-  // R) into `nxt`, R refilled with block fb + 2.
+  // One feature block: MFMAs of block fb from `cur`, decode of block fb + AH
+  // (in R) into `nxt`, R refilled with block fb + AH + 1.
   // PHC: the phase of fb (fb mod PER); block fb + 1 is decoded in the next
-  // phase, and R is refilled with block fb + 2 in the one after.
-  auto block = [&](int fb, const uint4* cur, uint4* nxt, auto PHC) __attribute__((always_inline)) {
+  // phase, and R is refilled with block fb + 2 in the one after (PAIR: one
+  // phase, PER = 1).  SYNC: end with the barrier (PAIR: every second block).
+  auto block = [&](int fb, const uint4* cur, uint4* nxt, auto PHC, auto SYNC) __attribute__((always_inline)) {
     constexpr int ph = decltype(PHC)::value;
     using PhN = std::integral_constant<int, (ph + 1) % PER>;
     using PhNN = std::integral_constant<int, (ph + 2) % PER>;
@@ -566,8 +590,8 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
     DqGroups<NGRP> pb;
     DqGroups<1> pw;
     params_of(R, pb, pw);
-    const bool tail = is_tail(fb + 1);
-    load_params(fb + 2, PhNN{}, R);
+    const bool tail = is_tail(fb + AH);
+    load_params(fb + AH + 1, PhNN{}, R);
     bread(bf, cur, 0);
     if constexpr (kTab) gen.begin(xf, bp, bs_sel);
     else gen.begin(xf, bp, HB != 0);
@@ -601,9 +625,9 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
           pack(af[P ^ 1], v);
         }
       }
-      // decode slot SC of block fb + 1, then refill its code word with block fb + 2
+      // decode slot SC of block fb + AH, then refill its code word with block fb + AH + 1
       const uint4 d = dq_slot(SCC, PhN{}, R, pb, pw);
-      reload_slot(SCC, fb + 2, R);
+      reload_slot(SCC, fb + AH + 1, R);
 #pragma unroll
       for (int nb = 0; nb < kQNB; ++nb) {
         acc[nb] = Mfma<_Float16>::mma(af[P], bf[nb], acc[nb]);
@@ -634,23 +658,47 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
 #pragma unroll
       for (int sc = 0; sc < KP; ++sc) {
         uint4 v = nxt[(sc * kQNB + wave) * 64 + lane];
-        mask_tail(fb + 1, v);
+        mask_tail(fb + AH, v);
         nxt[(sc * kQNB + wave) * 64 + lane] = v;
       }
     }
     // the decoded block is in LDS (lgkmcnt(0)) and every wave is done with `cur`;
     // the register loads stay in flight across the barrier
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    if constexpr (decltype(SYNC)::value) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
   };
-  constexpr int UNR = PER == 4 ? 4 : 2;  // blocks per loop round: the stages alternate, phases repeat
-  for (int fb = fb_begin; fb < fb_end; fb += UNR) {
-    block(fb, stage0, stage1, Ph0{});
-    if (fb + 1 < fb_end) block(fb + 1, stage1, stage0, Ph1{});
-    if constexpr (PER == 4) {
-      if (fb + 2 < fb_end) block(fb + 2, stage0, stage1, std::integral_constant<int, 2>{});
-      if (fb + 3 < fb_end) block(fb + 3, stage1, stage0, std::integral_constant<int, 3>{});
+  using Sync = std::true_type;
+  using NoSync = std::false_type;
+  if constexpr (PAIR) {
+    // stage s holds blocks fb (first half) and fb + 1 (second half); the closing
+    // barrier runs on every path (the conditions are uniform per workgroup)
+    auto barrier = [&]() __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    for (int fb = fb_begin; fb < fb_end; fb += 4) {
+      block(fb, stage0, stage1, Ph0{}, NoSync{});
+      if (fb + 1 < fb_end) block(fb + 1, stage0 + HALF, stage1 + HALF, Ph0{}, NoSync{});
+      barrier();
+      if (fb + 2 < fb_end) {
+        block(fb + 2, stage1, stage0, Ph0{}, NoSync{});
+        if (fb + 3 < fb_end) block(fb + 3, stage1 + HALF, stage0 + HALF, Ph0{}, NoSync{});
+        barrier();
+      }
+    }
+  } else {
+    constexpr int UNR = PER == 4 ? 4 : 2;  // blocks per loop round: the stages alternate, phases repeat
+    for (int fb = fb_begin; fb < fb_end; fb += UNR) {
+      block(fb, stage0, stage1, Ph0{}, Sync{});
+      if (fb + 1 < fb_end) block(fb + 1, stage1, stage0, Ph1{}, Sync{});
+      if constexpr (PER == 4) {
+        if (fb + 2 < fb_end) block(fb + 2, stage0, stage1, std::integral_constant<int, 2>{}, Sync{});
+        if (fb + 3 < fb_end) block(fb + 3, stage1, stage0, std::integral_constant<int, 3>{}, Sync{});
+      }
     }
   }
 
@@ -708,6 +756,13 @@ __global__ void __launch_bounds__(kQThreads, 1) kan_qfused_block(QPArgs A) {
 
 template <int QT, int KQ, int HB, int BASIS>
 static void qp_go(const QPArgs& A, dim3 grid, hipStream_t st) {
+  // two feature blocks per stage: Chebyshev K = 4 (the GatedKAN shape; its groups repeat every block)
+  if constexpr (BASIS == BASIS_CHEBY_POST && KQ == 4) {
+    if (A.pair) {
+      hipLaunchKernelGGL((kan_qfused_block<QT, KQ, HB, BASIS, true>), grid, dim3(kQThreads), 0, st, A);
+      return;
+    }
+  }
   hipLaunchKernelGGL((kan_qfused_block<QT, KQ, HB, BASIS>), grid, dim3(kQThreads), 0, st, A);
 }
 
@@ -773,6 +828,7 @@ hipError_t qp_run(const QPLaunch& L, const QPGrid& G, hipStream_t st) {
   A.epi = L.epi;
   A.round16 = L.round16;
   A.bp = L.bp;
+  A.pair = g_qp_block_pairs;
   return qp_dispatch_basis<QT, HB>(L, A, dim3((unsigned)(G.m_tiles * G.n_tiles), (unsigned)G.nsp), st);
 }
 

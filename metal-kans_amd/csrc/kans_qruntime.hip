@@ -905,6 +905,14 @@ int kans_decode_set_weight_loads(int mode) {
   return prev;
 }
 
+int kans_prefill_set_block_pairs(int on) {
+  if (on != 0 && on != 1) return kans_fail(KANS_ERR_ARG, "block pairs must be 0 or 1 (got %d)", on);
+  std::lock_guard<std::mutex> lk(kans_mutex());
+  const int prev = g_qp_block_pairs;
+  g_qp_block_pairs = on;
+  return prev;
+}
+
 int kans_gated_set_fused_swiglu(int on) {
   std::lock_guard<std::mutex> lk(kans_mutex());
   const int prev = g_fused_swiglu ? 1 : 0;

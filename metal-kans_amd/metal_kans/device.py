@@ -129,6 +129,7 @@ SIGNATURES = {
     "kans_gated_set_fused_swiglu": (c_int, [c_int]),
     "kans_decode_set_pre_basis": (c_int, [c_int]),
     "kans_decode_set_weight_loads": (c_int, [c_int]),
+    "kans_prefill_set_block_pairs": (c_int, [c_int]),
     "kans_mfma_ceiling": (c_int, [c_int, P, P, c_int, P]),
     "kans_stream_ceiling": (c_int, [P, c_size_t, P]),
 }

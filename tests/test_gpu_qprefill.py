@@ -172,6 +172,49 @@ def test_qlayer_prefill(gpu, fmt, K, base, bias, B, d_in, d_out):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
+@pytest.mark.parametrize("base", [True, False])
+@pytest.mark.parametrize("B,d_in,d_out", [(300, 100, 70), (40, 256, 300), (600, 16, 33), (64, 48, 40), (2000, 112, 256)])
+def test_qlayer_prefill_block_pairs(gpu, fmt, base, B, d_in, d_out):
+    """Chebyshev K = 4 prefill with two feature blocks per LDS stage against one block per stage, bit for
+    bit (7, 16, 1, 3 and 7 feature blocks; the batch sizes give 1 to several feature splits), and the
+    GatedKAN prefill block (column-paired gate|up launch, then down) the same way."""
+    lib = gpu
+    h, L = make_qlayer(lib, fmt, d_in, d_out, 4, base, True, seed=B + d_in)
+    try:
+        x = np.random.default_rng(d_out).uniform(-1.3, 1.3, (B, d_in)).astype(np.float32)
+        assert lib.kans_qlayer_fused(h, B) == 1
+        ys = []
+        for on in (1, 0):
+            prev = lib.kans_prefill_set_block_pairs(on)
+            assert prev in (0, 1)
+            ys.append(run(lib, h, x, d_out))
+        assert lib.kans_prefill_set_block_pairs(1) == 0
+        np.testing.assert_array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+        assert O.rel_err(ys[0], oracle(L, x)) <= 2e-2
+    finally:
+        lib.kans_prefill_set_block_pairs(1)
+        lib.kans_qlayer_destroy(h)
+    if (B, d_in) == (300, 100):
+        blk, layers, specs = make_block(lib, fmt, 96, 200, K=4, bias=base, seed=3)
+        try:
+            xb = np.random.default_rng(1).normal(0, 1, (B, 96)).astype(np.float16)
+            outs = []
+            for on in (1, 0):
+                lib.kans_prefill_set_block_pairs(on)
+                y = np.zeros((B, 96), np.float16)
+                assert lib.kans_gated_forward_host(blk, xb.ctypes.data, 1, y.ctypes.data, 1, B, 1) == 0
+                outs.append(y)
+            np.testing.assert_array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+            assert O.rel_err(outs[0].astype(np.float32), gated_oracle(specs, xb.astype(np.float64), 1)) <= 2e-2
+        finally:
+            lib.kans_prefill_set_block_pairs(1)
+            lib.kans_gated_destroy(blk)
+            for hnd in layers:
+                lib.kans_qlayer_destroy(hnd)
+    assert lib.kans_prefill_set_block_pairs(2) < 0
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "ternary"])
 @pytest.mark.parametrize("kind,K", [("rbf", 8), ("rbf", 4), ("rbf", 3), ("rbf", 5), ("rbf", 7), ("bspline", 8),
                                     ("bspline", 4)])
 @pytest.mark.parametrize("base,bias", [(True, True), (False, False)])
