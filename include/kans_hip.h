@@ -365,8 +365,8 @@ int kans_gated_set_fused_swiglu(int on);
  * 0..2 (no reference counterpart: a tuning and test switch). */
 int kans_decode_set_pre_basis(int mode);
 /* Cache policy of the decode path's weight-record loads: 0 automatic (the default), 1 plain, 2
- * non-temporal.  Automatic loads INT4 and ternary records non-temporally and INT8 records with plain
- * loads, the faster form for each when a model's weights stream from HBM on every decode step.
+ * non-temporal.  Automatic loads every format's records non-temporally, the faster form when a
+ * model's weights stream from HBM on every decode step.
  * Results do not depend on it.  Returns the previous mode, or a negative error code for a mode
  * outside 0..2 (no reference counterpart: a tuning and test switch). */
 int kans_decode_set_weight_loads(int mode);

@@ -61,11 +61,15 @@ template <int QT>
 __host__ __device__ __forceinline__ long qrec_offset(int rb, int c, int C_tot) {
   return ((long)(rb / kQNW) * C_tot + c) * qrec_bytes(QT);
 }
-// byte offset of lane `lane`'s code word of row block rb, superchunk c
+// byte offset of lane `lane`'s code word of row block rb, superchunk c (INT8:
+// of its first 16 bytes; the second 16 follow 1 KB later, so that each of the
+// tile's two 16-byte loads per lane reads 1 KB of whole cache lines)
 template <int QT>
 __host__ __device__ __forceinline__ long qcode_offset(int rb, int c, int C_tot, int lane) {
   if constexpr (QT == Q_TERN)  // row blocks 2p and 2p+1 paired: lane l's 16 bytes at 1 KB p + 16 l
     return qrec_offset<QT>(rb, c, C_tot) + (long)((rb % kQNW) >> 1) * 1024 + (long)lane * 16 + ((rb % kQNW) & 1) * 8;
+  if constexpr (QT == Q_INT8)
+    return qrec_offset<QT>(rb, c, C_tot) + (long)(rb % kQNW) * qtile_bytes(QT) + (long)lane * 16;
   return qrec_offset<QT>(rb, c, C_tot) + (long)(rb % kQNW) * qtile_bytes(QT) + (long)lane * (qtile_bytes(QT) / 64);
 }
 // code loads per record and lane (one 16-byte load per ternary tile pair)
@@ -110,7 +114,8 @@ __global__ void k_tile_int4(const unsigned char* __restrict__ qw, long rowbytes,
 // INT8 qweight: row n is `rowbytes` bytes, one code per byte.  Q[rb][c][lane],
 // lane = (q = l/16, r = l%16): dwords 2t, 2t+1 hold the 8 codes of row
 // 16*rb + r at reduction indices 128c + 32t + 8q .. +7 (bytes of the row in
-// order), i.e. 32 bytes per lane.
+// order), i.e. 32 bytes per lane: dwords 0-3 at 16 l in the tile, dwords 4-7 at
+// 1024 + 16 l (qcode_offset).
 __global__ void k_tile_int8(const unsigned char* __restrict__ qw, long rowbytes, int D_out, int nrb, int C,
                             int c_off, int C_tot, char* __restrict__ R) {
   const long total = (long)nrb * C * 64;
@@ -134,9 +139,9 @@ __global__ void k_tile_int8(const unsigned char* __restrict__ qw, long rowbytes,
           }
         }
     }
-    uint4* dst = reinterpret_cast<uint4*>(R + qcode_offset<Q_INT8>(rb, c_off + c, C_tot, lane));
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    char* dst = R + qcode_offset<Q_INT8>(rb, c_off + c, C_tot, lane);
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(dst + 1024) = make_uint4(w[4], w[5], w[6], w[7]);
   }
 }
 
@@ -674,6 +679,13 @@ __device__ __forceinline__ void load_codes(const char* rec, int lane, QW (&qw)[k
       const uint4 v = load_rec<NT, uint4>(rec + p * 1024 + lane * 16);
       qw[2 * p] = make_uint2(v.x, v.y);
       qw[2 * p + 1] = make_uint2(v.z, v.w);
+    }
+  } else if constexpr (QT == Q_INT8) {
+    // the two halves of the lane's 32 bytes, 1 KB apart (qcode_offset)
+#pragma unroll
+    for (int w = 0; w < kQNW; ++w) {
+      qw[w].lo = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + lane * 16);
+      qw[w].hi = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + 1024 + lane * 16);
     }
   } else {
 #pragma unroll

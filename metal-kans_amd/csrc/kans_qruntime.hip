@@ -81,20 +81,23 @@ size_t rec_bytes(const kans_qlayer* L) {
   return (size_t)(L->nrb_pad / L->nw) * L->C_tot * qrec_bytes(L->quant);
 }
 
-// Cache policy of the weight-record loads, by format.  A decode step of a
-// model streams every layer's weights once, and a model whose quantized layers
-// together exceed the 256 MB MALL finds none of them cached on its next step,
-// so the choice is made for weights read from HBM: measured on the config-5
-// blocks with three weight copies used in turn (one box, same run):
-//   INT4    B = 1: 83.0 us non-temporal, 91.4 plain; B = 32: 130.7 / 132.9
-//   ternary B = 1: 63.0 non-temporal, 66.3 plain;   B = 32: 104.2 / 105.4
-//   INT8    B = 1: 150.0 non-temporal, 141.7 plain; B = 32: 205.8 / 188.3
-// so INT4 and ternary load non-temporally and INT8 with plain loads.  (A
-// ternary block replayed alone stays in the MALL and is faster with plain
-// loads, 60 against 63 us, but that is not how a model's layers are read.)
-int use_nt(int quant) {
+// Cache policy of the weight-record loads.  A decode step of a model streams
+// every layer's weights once, and a model whose quantized layers together
+// exceed the 256 MB MALL finds none of them cached on its next step, so the
+// choice is made for weights read from HBM: measured on the config-5 blocks,
+// three weight copies chained in one decode-step graph (one box, same run,
+// us per block, non-temporal / plain):
+//   INT4    B = 1: 75.2 / 83.9;  B = 32: 122.3 / 127.9
+//   ternary B = 1: 52.6 / 57.2;  B = 32: 94.3 / 98.7
+//   INT8    B = 1: 122.1 / 136.4; B = 32: 167.7 / 180.1
+// so every format loads non-temporally.  (With each lane's 32 INT8 bytes
+// contiguous, so that each 16-byte load covered half of every cache line of
+// the tile, non-temporal loads were the slower form for INT8: 145.2 / 136.5
+// at B = 1.  A ternary block replayed alone stays in the MALL and is faster
+// with plain loads, but that is not how a model's layers are read.)
+int use_nt(int /*quant*/) {
   if (g_weight_loads != 0) return g_weight_loads == 2 ? 1 : 0;
-  return quant == Q_INT8 ? 0 : 1;
+  return 1;
 }
 
 // Superchunk ranges per row group: about items_per_cu work items (waves) per
