@@ -25,6 +25,12 @@ inline int items_per_cu(int /*quant*/, int B) { return B <= kSmallB ? 8 : 10; }
 constexpr int kQNW = 4;
 inline int qrow_blocks(int /*D_out*/) { return kQNW; }
 
+// Register-ring slots of the small-batch GEMV k_qgemv (superchunks in flight
+// while one is multiplied: depth - 1).  Three for every format: deeper rings
+// measured slower on the config-5 blocks at B = 1 (INT4 depth 4 / 5: 83.4 /
+// 82.0 us against 75.5; ternary depth 5 / 7: 61.0 / 63.5 against 52.6).
+__host__ __device__ constexpr int qring_depth(int /*quant*/) { return 3; }
+
 // Formats with a group affine (scale, bias) per 64 indices: INT4 and INT8 (the
 // kernels apply it to the fp32 accumulator with the group sums S of Phi).
 __host__ __device__ constexpr bool q_affine(int quant) { return quant != Q_TERN; }

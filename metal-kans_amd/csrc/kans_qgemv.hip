@@ -943,7 +943,9 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
     // of c (vmcnt counts in issue order).  A four-deep ring for ternary, whose
     // records are half the size, measured slower with this loop (cfg5 block
     // at B = 1: 73.2 against 69.2 us).
-    Ops o0, o1, o2;
+    // RD slots, superchunks c+1 .. c+RD-1 in flight while c is consumed
+    constexpr int RD = qring_depth(QT);
+    Ops o[RD];
     // activation fragments and group sums of superchunk c: from Phi / S, or
     // (PRE) from the wave's LDS slice
     auto issue_a = [&](int c, Ops& o) {
@@ -989,10 +991,10 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       auto kick = [&] {
         if (started || !live_rg) return;
         started = true;
-        fence();
-        issue_w(c_lo, o0);
-        fence();
-        issue_w(c_lo + 1, o1);
+        static_for<0, RD - 1>([&](auto J) __attribute__((always_inline)) {
+          fence();
+          issue_w(c_lo + decltype(J)::value, o[decltype(J)::value]);
+        });
         fence();
       };
       const long P_lo = (long)c_lo * 128, P_hi = (long)c_hi * 128;
@@ -1148,30 +1150,29 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
         __syncthreads();  // the group sums are in LDS before any wave reads them
       }
       if (!live_rg) return;  // a padding row group: its share of the basis is done
-      issue_a(c_lo, o0);
-      issue_a(c_lo + 1, o1);
+      static_for<0, RD - 1>([&](auto J) __attribute__((always_inline)) {
+        issue_a(c_lo + decltype(J)::value, o[decltype(J)::value]);
+      });
     } else {
-      issue(c_lo, o0);
-      fence();
-      issue(c_lo + 1, o1);
+      static_for<0, RD - 1>([&](auto J) __attribute__((always_inline)) {
+        if constexpr (decltype(J)::value > 0) fence();
+        issue(c_lo + decltype(J)::value, o[decltype(J)::value]);
+      });
     }
     int c = c_lo;
-    for (; c + 3 <= c_hi; c += 3) {
-      fence();
-      issue(c + 2, o2);
-      compute(o0);
-      fence();
-      issue(c + 3, o0);
-      compute(o1);
-      fence();
-      issue(c + 4, o1);
-      compute(o2);
+    for (; c + RD <= c_hi; c += RD) {
+      // slot j: refill the slot consumed last round with superchunk c + j + RD - 1, then multiply c + j
+      static_for<0, RD>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        fence();
+        issue(c + j + RD - 1, o[(j + RD - 1) % RD]);
+        compute(o[j]);
+      });
     }
-    // o0, o1 hold superchunks c, c + 1
-    if (c < c_hi) {
-      compute(o0);
-      if (c + 1 < c_hi) compute(o1);
-    }
+    // slots 0 .. RD-2 hold superchunks c .. c + RD - 2
+    static_for<0, RD - 1>([&](auto J) __attribute__((always_inline)) {
+      if (c + decltype(J)::value < c_hi) compute(o[decltype(J)::value]);
+    });
   }
 
   if (PRE && !live_rg) return;  // padding row group (an empty range skipped the basis work)
