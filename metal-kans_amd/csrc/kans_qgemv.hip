@@ -671,12 +671,16 @@ __device__ __forceinline__ Q load_rec(const char* p) {
 }
 
 // The kQNW code words of one record for this lane (layout of qcode_offset).
+// rec is wave-uniform and the lane's offset an unsigned 32-bit value, so each
+// load can take the scalar-base + vector-offset form (no 64-bit address in
+// vector registers that the compiler could reuse as the load's destination).
 template <bool NT, int QT, typename QW>
 __device__ __forceinline__ void load_codes(const char* rec, int lane, QW (&qw)[kQNW]) {
+  const unsigned lo = (unsigned)lane * 16u;
   if constexpr (QT == Q_TERN) {
 #pragma unroll
     for (int p = 0; p < kQNW / 2; ++p) {
-      const uint4 v = load_rec<NT, uint4>(rec + p * 1024 + lane * 16);
+      const uint4 v = load_rec<NT, uint4>(rec + p * 1024 + lo);
       qw[2 * p] = make_uint2(v.x, v.y);
       qw[2 * p + 1] = make_uint2(v.z, v.w);
     }
@@ -684,12 +688,47 @@ __device__ __forceinline__ void load_codes(const char* rec, int lane, QW (&qw)[k
     // the two halves of the lane's 32 bytes, 1 KB apart (qcode_offset)
 #pragma unroll
     for (int w = 0; w < kQNW; ++w) {
-      qw[w].lo = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + lane * 16);
-      qw[w].hi = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + 1024 + lane * 16);
+      qw[w].lo = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + lo);
+      qw[w].hi = load_rec<NT, uint4>(rec + w * qtile_bytes(QT) + 1024 + lo);
+    }
+  } else {
+    static_assert(sizeof(QW) == 16, "INT4 code words: 16 bytes per lane");
+#pragma unroll
+    for (int w = 0; w < kQNW; ++w) qw[w] = load_rec<NT, QW>(rec + w * qtile_bytes(QT) + lo);
+  }
+}
+
+// The same loads through a buffer resource over the wave's row group of
+// records (k_qgemv): the lane's offset is one loop-invariant vector register and
+// the record's offset a scalar, so no 64-bit address is rebuilt in vector
+// registers for every superchunk (with pointer loads the compiler made one
+// load's address registers its destination, and the ring loop then waited for
+// every load in flight before it could rebuild the next address).
+__device__ __forceinline__ uint4 load_buf16(__amdgpu_buffer_rsrc_t r, unsigned voff, int soff, bool nt) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = nt ? __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2)
+                     : __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <bool NT, int QT, typename QW>
+__device__ __forceinline__ void load_codes_buf(__amdgpu_buffer_rsrc_t r, int soff, int lane, QW (&qw)[kQNW]) {
+  const unsigned lo = (unsigned)lane * 16u;
+  if constexpr (QT == Q_TERN) {
+#pragma unroll
+    for (int p = 0; p < kQNW / 2; ++p) {
+      const uint4 v = load_buf16(r, lo + p * 1024, soff, NT);
+      qw[2 * p] = make_uint2(v.x, v.y);
+      qw[2 * p + 1] = make_uint2(v.z, v.w);
+    }
+  } else if constexpr (QT == Q_INT8) {
+#pragma unroll
+    for (int w = 0; w < kQNW; ++w) {
+      qw[w].lo = load_buf16(r, lo + w * qtile_bytes(QT), soff, NT);
+      qw[w].hi = load_buf16(r, lo + w * qtile_bytes(QT) + 1024, soff, NT);
     }
   } else {
 #pragma unroll
-    for (int w = 0; w < kQNW; ++w) qw[w] = load_rec<NT, QW>(rec + w * qtile_bytes(QT) + lane * (int)sizeof(QW));
+    for (int w = 0; w < kQNW; ++w) qw[w] = load_buf16(r, lo + w * qtile_bytes(QT), soff, NT);
   }
 }
 
@@ -846,7 +885,12 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
   static_assert(SR >= 1 && SR <= kSmallB, "small-batch kernel");
   constexpr int NW = kQNW;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // the wave index as a scalar: record bases, ranges and row groups are then
+  // wave-uniform, and the weight loads take the scalar-base + lane-offset form
+  // (with the base in vector registers the compiler reused a load's address
+  // registers as its destination, and the next round's address then waited for
+  // every load in flight at the top of the ring loop)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // PRE: the four waves of a workgroup take four consecutive row groups over
   // ONE superchunk range and compute its basis together (a workgroup past the
   // last row group still takes part in that, then stops); otherwise four
@@ -885,6 +929,9 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
 
   typedef QWordOf<QT> QWord;
   const char* rbase = M.rec + (long)rg_loc * C_tot * qrec_bytes(QT);
+  // this row group's records (C_tot of them) as one buffer (see load_codes_buf)
+  const __amdgpu_buffer_rsrc_t rrec =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(rbase), (short)0, C_tot * qrec_bytes(QT), 0x00020000);
 
   // operands of one superchunk: weights / group parameters (HBM stream) and
   // activation fragments / group sums (L2 resident).
@@ -969,10 +1016,10 @@ __global__ void __launch_bounds__(256) k_qgemv(QMatDev m0, QMatDev m1, int rg_sp
       }
     };
     auto issue_w = [&](int c, Ops& o) {
-      const int cc = min(c, c_hi - 1);
-      const char* rec = rbase + (long)cc * qrec_bytes(QT);
-      load_codes<NT, QT>(rec, lane, o.qw);
-      o.sb = load_rec<NT, float4>(rec + NW * qtile_bytes(QT) + lane * 16);
+      const int soff = min(c, c_hi - 1) * qrec_bytes(QT);
+      load_codes_buf<NT, QT>(rrec, soff, lane, o.qw);
+      const uint4 sb = load_buf16(rrec, (unsigned)lane * 16u + NW * qtile_bytes(QT), soff, NT);
+      o.sb = make_float4(__uint_as_float(sb.x), __uint_as_float(sb.y), __uint_as_float(sb.z), __uint_as_float(sb.w));
     };
     auto issue = [&](int c, Ops& o) {
       issue_a(c, o);
