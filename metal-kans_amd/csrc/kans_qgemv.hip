@@ -1757,6 +1757,8 @@ static void qgemv_launch(int qt, const QGemv& G, hipStream_t st) {
 
 hipError_t qgemv(int qt, const QGemv& G, hipStream_t st) {
   const bool small = G.B <= kSmallB;
+  // k_qgemv addresses a row group's records with 32-bit buffer offsets
+  if (small && (long)G.C_tot * qrec_bytes(qt) > 0x7fffffffL) return hipErrorInvalidValue;
   const int ep = G.epi.kind;
   if (ep != QEPI_PART && (!small || !G.epi.counters || G.ksplit > kMaxEpiSplit || !G.rec1 || G.D_out1 != G.D_out0))
     return hipErrorInvalidValue;
